@@ -1,0 +1,132 @@
+/*
+ * moe_mi355x.h -- C ABI of the MI355X (gfx950) MoE expert path for GLM-5.3-style layers.
+ *
+ * One shared library, libmoe_mi355x.so.  Every pointer argument is a DEVICE pointer owned by
+ * the caller (for example a PyTorch tensor's data_ptr()); every launch is enqueued on the
+ * caller's `stream` with no host synchronisation.  Scratch memory is passed in as an explicit,
+ * caller-owned workspace whose size is given by moe_workspace_bytes(); it must be zero-filled
+ * before its first use, and every successful call leaves it ready for the next call.  Calls
+ * that share one workspace must not overlap.
+ *
+ * Return codes: 0 ok; negative = invalid argument (MOE_E*), message in moe_last_error();
+ * positive = hipError_t of the failing HIP call.  No C++ exception crosses this boundary.
+ *
+ * Data types: bf16 and f16 are passed as uint16_t bit patterns; fp32 as float.
+ * Shapes: hidden h, intermediate m, experts E (routed + shared, the shared expert last).
+ *
+ * Each entry point names the reference interface it replaces (paths relative to the
+ * reference repository root).
+ */
+#ifndef MOE_MI355X_H
+#define MOE_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* moe_stream_t; /* hipStream_t */
+
+enum {
+  MOE_OK = 0,
+  MOE_EINVAL = -1,     /* bad shape / format / argument */
+  MOE_ENOTSUP = -2,    /* valid request outside what this build supports */
+  MOE_EWORKSPACE = -3, /* workspace missing or too small */
+};
+
+/* Library version string and the last error message of the calling thread. */
+const char* moe_version(void);
+const char* moe_last_error(void);
+
+/* Per-device setup (codebook table).  Called implicitly by every entry point; exposed so a
+ * caller can pay the cost up front.  Acts on the current HIP device. */
+int moe_init(void);
+
+/* Copy the 65536-entry E4M3 code table (one byte per 16-bit trellis state) to `dst`.
+ * Replaces: exlr8/trellis.py:43-50 mcg_codebook (as E4M3 codes; exlr8/static_cache.py:11-26). */
+int moe_codebook_e4m3(uint8_t* dst, moe_stream_t stream);
+
+/* ---------------------------------------------------------------- router */
+
+/* Sigmoid scores, bias-corrected top-8 (ties to the lower id), renormalised x2.5; slot 8 = 256.
+ * logits [rows,256] f32, bias [256] f32 -> indices [rows,9] u32, scores [rows,8] f32.
+ * Replaces: exlr8/fast_router.py:17-24 route (exlr8/metal/fast_router.metal:1-42);
+ *           exlr8/model.py:111-132 route_experts + 407-408 shared-expert append. */
+int moe_route_f32(const float* logits, const float* bias, int rows, uint32_t* indices, float* scores,
+                  moe_stream_t stream);
+
+/* Router GEMV: logits [rows,experts] = f32(x [rows,hidden] bf16) @ w [experts,hidden]^T.
+ * Replaces: the gate call gate(x.astype(f32)) of exlr8/fast_router.py:34 / exlr8/model.py:406
+ *           (DenseLinear format 6 with fp32 weight, exlr8/dense.py:158-159, exlr8/model.py:367-370). */
+int moe_router_logits(const uint16_t* x, const float* w, int rows, int hidden, int experts, float* logits,
+                      moe_stream_t stream);
+
+/* ---------------------------------------------------------------- K4 trellis */
+
+/* Decode expert `expert` of a packed trellis tensor to inner weights [in,out] as fp16 bits.
+ * packed_bytes is the size of the whole tensor (all experts); k must be 4 in this build.
+ * Replaces: exlr8/trellis.py:199-214 dequantize_trellis (inner part; exlr8/metal/decode.metal). */
+int moe_trellis_decode_f16(const void* packed, int64_t packed_bytes, int k, int in_features, int out_features,
+                           int side, int64_t expert, uint16_t* inner, moe_stream_t stream);
+
+/* Selected-expert trellis linear: y[slot] = bf16(out_scale[e] * H(H(x_row * in_scale[e]) @ inner_e)).
+ * ids [rows, slots] u32 (slots <= 9, rows*slots <= 72 per call); x [rows, in] bf16, or
+ * [rows*slots, in] when x_per_slot != 0; in_scale [E,in], out_scale [E,out] f16; y [rows*slots,out] bf16.
+ * Replaces: exlr8/trellis.py:172-196 expert_linear; exlr8/fast_decode.py:153-165 fast_expert_linear. */
+int moe_k4_expert_linear(const uint16_t* x, int x_per_slot, const uint32_t* ids, int rows, int slots,
+                         const void* packed, int64_t packed_bytes, const uint16_t* in_scale,
+                         const uint16_t* out_scale, int in_features, int out_features, int side, uint16_t* y,
+                         void* workspace, size_t workspace_bytes, moe_stream_t stream);
+
+/* Expert MLP over selected experts: values [rows, slots, h] bf16 (gate/up side 1, down side 2,
+ * typed SwiGLU, A.5 cast points).  Arguments as moe_k4_expert_linear; scale pairs per projection.
+ * Replaces: exlr8/experts.py:150-188 ExpertLayer.__call__ (resident K4);
+ *           exlr8/fast_decode.py:208-221 fast_expert_mlp. */
+int moe_k4_mlp(const uint16_t* x, const uint32_t* ids, int rows, int slots, const void* packed_gate,
+               const void* packed_up, const void* packed_down, int64_t packed_bytes, const uint16_t* in_gate,
+               const uint16_t* out_gate, const uint16_t* in_up, const uint16_t* out_up, const uint16_t* in_down,
+               const uint16_t* out_down, int hidden, int intermediate, uint16_t* values, void* workspace,
+               size_t workspace_bytes, moe_stream_t stream);
+
+/* Expert MLP plus weighted combine: out = bf16(residual + bf16(bf16(sum_i values_i*scores_i) + values_8)).
+ * ids [rows,9] (slot 8 = shared expert), scores [rows,8] f32, residual/out [rows,h] bf16.
+ * Replaces: exlr8/fast_decode.py:224-244 compiled_expert_mlp_finish (exlr8/metal/fast_decode_finish_fused.metal)
+ *           and the combine of exlr8/model.py:415-418. */
+int moe_k4_mlp_finish(const uint16_t* x, const uint32_t* ids, const float* scores, const uint16_t* residual, int rows,
+                      const void* packed_gate, const void* packed_up, const void* packed_down, int64_t packed_bytes,
+                      const uint16_t* in_gate, const uint16_t* out_gate, const uint16_t* in_up,
+                      const uint16_t* out_up, const uint16_t* in_down, const uint16_t* out_down, int hidden,
+                      int intermediate, uint16_t* out, void* workspace, size_t workspace_bytes, moe_stream_t stream);
+
+/* Whole routed MoE block for decode batches: router GEMV, route, expert MLP and combine.
+ * x/residual/out [rows,h] bf16 (rows <= 8 per call), router_w [256,h] f32, bias [256] f32;
+ * indices/scores (optional, may be NULL) receive the routing [rows,9] u32 / [rows,8] f32.
+ * Replaces: exlr8/fast_router.py:27-37 compiled_finish(...).call(x, residual). */
+int moe_k4_moe_decode(const uint16_t* x, const uint16_t* residual, int rows, const float* router_w,
+                      const float* bias, const void* packed_gate, const void* packed_up, const void* packed_down,
+                      int64_t packed_bytes, const uint16_t* in_gate, const uint16_t* out_gate,
+                      const uint16_t* in_up, const uint16_t* out_up, const uint16_t* in_down,
+                      const uint16_t* out_down, int hidden, int intermediate, uint16_t* out, uint32_t* indices,
+                      float* scores, void* workspace, size_t workspace_bytes, moe_stream_t stream);
+
+/* ---------------------------------------------------------------- profiling */
+
+/* Arm HIP events (hipEvent_t handles, NULL entries skipped) for the next K4 layer call made by
+ * the calling thread: events[0] before the router, [1] before the gate/up GEMV, [2] before the
+ * down GEMV, [3] after the down GEMV.  Used by bench.py to time each kernel on the stream it
+ * runs on.  No counterpart in the reference (its benchmarks time whole model steps). */
+int moe_profile_events(void** events, int count);
+
+/* ---------------------------------------------------------------- workspace */
+
+/* Bytes of workspace needed by the decode entry points above for the given shape on the
+ * current device (independent of rows up to 8). */
+size_t moe_workspace_bytes(int hidden, int intermediate);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOE_MI355X_H */

@@ -1,0 +1,95 @@
+"""ctypes loader for libmoe_mi355x.so and small helpers shared by the host modules."""
+import ctypes
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libmoe_mi355x.so"
+
+
+class LibraryMissing(RuntimeError):
+    """Raised when the HIP extension has not been built; there is no CPU fallback."""
+
+
+class MoeError(RuntimeError):
+    pass
+
+
+_lib = None
+
+_VP, _I32, _I64, _SZ = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t
+_SIGNATURES = {
+    "moe_version": (ctypes.c_char_p, []),
+    "moe_last_error": (ctypes.c_char_p, []),
+    "moe_init": (_I32, []),
+    "moe_codebook_e4m3": (_I32, [_VP, _VP]),
+    "moe_route_f32": (_I32, [_VP, _VP, _I32, _VP, _VP, _VP]),
+    "moe_router_logits": (_I32, [_VP, _VP, _I32, _I32, _I32, _VP, _VP]),
+    "moe_trellis_decode_f16": (_I32, [_VP, _I64, _I32, _I32, _I32, _I32, _I64, _VP, _VP]),
+    "moe_k4_expert_linear": (_I32, [_VP, _I32, _VP, _I32, _I32, _VP, _I64, _VP, _VP, _I32, _I32, _I32, _VP,
+                                    _VP, _SZ, _VP]),
+    "moe_k4_mlp": (_I32, [_VP, _VP, _I32, _I32, _VP, _VP, _VP, _I64] + [_VP] * 6 + [_I32, _I32, _VP, _VP, _SZ, _VP]),
+    "moe_k4_mlp_finish": (_I32, [_VP, _VP, _VP, _VP, _I32, _VP, _VP, _VP, _I64] + [_VP] * 6
+                          + [_I32, _I32, _VP, _VP, _SZ, _VP]),
+    "moe_k4_moe_decode": (_I32, [_VP, _VP, _I32, _VP, _VP, _VP, _VP, _VP, _I64] + [_VP] * 6
+                          + [_I32, _I32, _VP, _VP, _VP, _VP, _SZ, _VP]),
+    "moe_workspace_bytes": (_SZ, [_I32, _I32]),
+    "moe_profile_events": (_I32, [_VP, _I32]),
+}
+
+
+def lib():
+    """Load the HIP library (once).  Raises LibraryMissing if it was never built."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise LibraryMissing(f"{LIB_PATH} is missing: run `python -m mlxlr8_amd.build` "
+                                 "(the MoE path has no CPU fallback)")
+        handle = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in _SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype, fn.argtypes = res, args
+        _lib = handle
+    return _lib
+
+
+def exported_symbols():
+    return list(_SIGNATURES)
+
+
+def check(rc):
+    """Map a C-ABI return code to the reference's exception types."""
+    if rc == 0:
+        return
+    msg = lib().moe_last_error().decode(errors="replace")
+    if rc < 0:
+        raise ValueError(msg)
+    raise MoeError(f"HIP error {rc}: {msg}")
+
+
+def ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def stream(device=None):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+_workspaces = {}
+
+
+def workspace(device, hidden, intermediate):
+    """A zero-initialised scratch buffer per (device, shape), reused across calls on one stream."""
+    key = (str(device), int(hidden), int(intermediate))
+    ws = _workspaces.get(key)
+    if ws is None:
+        nbytes = lib().moe_workspace_bytes(int(hidden), int(intermediate))
+        ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws
+
+
+def require_cuda(*tensors):
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise ValueError("MoE kernels take device tensors (got a CPU tensor)")

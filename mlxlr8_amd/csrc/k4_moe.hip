@@ -1,0 +1,742 @@
+// K4 trellis expert path on gfx950: decode-fused GEMVs, gate finish, combine.
+//
+// Semantics follow the reference's resident K4 chain (paths relative to the reference root):
+//   prep      xh = H128(x * in_scale[e])                 exlr8/metal/fast_decode_prep.metal
+//   linear    inner = xh @ decode(packed_e)              exlr8/metal/fast_decode_linear.metal
+//   gate fin. a = H128(swiglu_T(H(g)*og, H(u)*ou)*id)    exlr8/metal/fast_decode_gate_finish.metal
+//   finish    T(H128(inner) * out_scale)                 exlr8/metal/fast_decode_finish.metal
+//   combine   routed sum, shared, residual               exlr8/metal/fast_decode_finish_fused.metal
+//
+// MI355X design (not a translation of the Metal kernels):
+//   * One persistent block of 16 waves per CU.  The 64 KB E4M3 code table lives in LDS once
+//     per CU; every wave streams a static, contiguous range of 1 KB "chunks".
+//   * A chunk is one 16-row input tile x 128 output columns (8 consecutive 128 B tiles).  Both
+//     storage orders keep a chunk contiguous, so each wave load is one fully coalesced 1 KB
+//     dwordx4 access.  Lane L holds 4 words of tile L/8 and owns output columns
+//     16*(L/8) + L%8 and +8 for all 16 rows: no cross-lane reduction inside the k loop.
+//   * Codewords are decoded by LDS table lookup or arithmetically (mix chosen at compile
+//     time) and accumulated in fp32.
+//   * Prep (scale + H128) is fused into the gate/up GEMV; the gate finish and the combine are
+//     done by the last wave to finish a (unit, column block) / column block, detected with a
+//     device-scope counter, so a layer is router + gate/up + down = few launches and the
+//     partial sums are reduced in a fixed order (deterministic).
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <mutex>
+
+#include "moe_device.h"
+#include "moe_host.h"
+#include "moe_plan.h"
+
+namespace moe {
+
+__device__ uint8_t g_codebook_e4m3[65536];
+
+// ============================================================== codebook
+
+__global__ void build_codebook_kernel() {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;  // pair index, 32768 pairs
+  if (i >= 32768u) return;
+  const uint32_t a = 2u * i, b = 2u * i + 1u;
+  const uint32_t bytes = decode_pair_fp8(a, b);
+  g_codebook_e4m3[a] = (uint8_t)(bytes & 0xFFu);
+  g_codebook_e4m3[b] = (uint8_t)(bytes >> 8);
+}
+
+__global__ void copy_codebook_kernel(uint8_t* dst) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < 65536u) dst[i] = g_codebook_e4m3[i];
+}
+
+// ============================================================== plan
+
+__global__ void plan_kernel(const uint32_t* __restrict__ ids, int rows, int slots, int experts, int max_users,
+                            Plan* plan) {
+  __shared__ int32_t unit_of_expert[257];
+  if (threadIdx.x != 0) return;
+  build_plan(ids, rows, slots, experts, max_users, plan, unit_of_expert);
+}
+
+// ============================================================== decode-only kernel
+
+// One thread per output element; inner [in, out] fp16.  exlr8/metal/decode.metal semantics.
+__global__ void trellis_decode_kernel(const uint32_t* __restrict__ packed, int in_f, int out_f, int side,
+                                      int64_t expert, uint16_t* __restrict__ inner) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)in_f * out_f) return;
+  const uint32_t r = (uint32_t)(idx / out_f), c = (uint32_t)(idx % out_f);
+  const uint32_t it = (uint32_t)in_f / 16u, ot = (uint32_t)out_f / 16u;
+  const uint32_t tk = r / 16u, tn = c / 16u, lr = r & 15u, lc = c & 15u;
+  const uint32_t lane = (lc & 7u) * 4u + ((lr & 7u) >> 1u);
+  const uint32_t slot = (lr & 1u) + ((lr & 8u) >> 2u) + ((lc & 8u) >> 1u);
+  const uint64_t e = (uint64_t)expert;
+  uint64_t tile = side == 2 ? ((((e * (it / 8u) + tk / 8u) * (ot / 8u) + tn / 8u) * 8u + tk % 8u) * 8u + tn % 8u)
+                            : (((e * (ot / 8u) + tn / 8u) * it + tk) * 8u + tn % 8u);
+  const uint32_t* w = packed + tile * 32u;
+  const uint32_t word = w[lane], prior = w[(lane + 31u) & 31u];
+  const uint32_t shift = 28u - 4u * slot;  // window of slot s ends 4*(s+1) bits into the word
+  const uint64_t merged = ((uint64_t)prior << 32) | word;
+  const uint32_t cw = (uint32_t)(merged >> shift) & 0xFFFFu;
+  const float v = fp8_to_f32(g_codebook_e4m3[cw]);
+  inner[idx] = __builtin_bit_cast(uint16_t, (_Float16)v);
+}
+
+// ============================================================== GEMV machinery
+
+enum InMode { IN_PREP = 0, IN_DIRECT = 1 };
+enum FinMode { FIN_GATE = 0, FIN_VALUES = 1, FIN_COMBINE = 2 };
+
+constexpr int kWaves = 16;            // waves per block (one block per CU)
+constexpr int kThreads = kWaves * 64;
+constexpr int kMaxBlocks = 256;
+constexpr int kMaxWaves = kMaxBlocks * kWaves;
+constexpr int kPartialStride = kMaxRows * 128;  // floats per (wave, visit)
+
+struct GemvArgs {
+  const uint8_t* packed[2];
+  int nproj;
+  int in_f, out_f, side;
+  int x_per_slot;              // PREP: x row index = slot (else token row)
+  const uint16_t* x_bf16;      // PREP: [rows or slots, in_f]
+  const uint16_t* in_scale[2]; // PREP: [E, in_f]
+  const float* x_f32;          // DIRECT: [slots, in_f]
+  const Plan* plan;
+  float* partial;              // [W][2][kMaxRows][128]
+  int32_t* counter_seg;        // chunks completed per segment
+  int32_t* counter_grp;        // segments completed per finish group
+  float* segbuf;               // GATE: reduced segment sums [seg][kMaxRows][128]
+  float* yslot;                // COMBINE: bf16-rounded expert outputs [slot][out_f]
+  const uint16_t* out_scale[2];
+  const uint16_t* in_down;     // GATE
+  float* down_xh;              // GATE output [slots, out_f]
+  uint16_t* values;            // VALUES output [slots, out_f]
+  const float* scores;         // COMBINE [rows, 8]
+  const uint16_t* residual;    // COMBINE [rows, out_f]
+  uint16_t* out;               // COMBINE [rows, out_f]
+};
+
+__device__ __forceinline__ uint64_t chunk_offset(int side, uint64_t e, uint32_t ob, uint32_t tk, uint32_t it,
+                                                 uint32_t obs) {
+  // 1 KB chunk (8 tiles of 128 B) of expert e, output block ob, input tile tk
+  if (side == 2) return ((((e * (it / 8u) + tk / 8u) * obs + ob) * 8u + tk % 8u) << 10);
+  return (((e * obs + ob) * it + tk) << 10);
+}
+
+__device__ __forceinline__ int64_t range_start(int64_t n, int w, int nw) { return n * w / nw; }
+
+// Cross-wave hand-off of partial sums inside one launch.  The XCDs' L2 caches are not coherent
+// with each other, and an agent-scope release would write back a whole L2.  Partials are
+// therefore stored write-through (system scope) and read back bypassing the L2; a
+// workgroup-scope fence (wait for the stores' acknowledgement) orders them before the counter.
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ float load_coherent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ void store_coherent2(float* p, float a, float b) {
+  const uint64_t v = (uint64_t)__float_as_uint(a) | ((uint64_t)__float_as_uint(b) << 32);
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ f32x2 load_coherent2(const float* p) {
+  const uint64_t v = __hip_atomic_load(reinterpret_cast<uint64_t*>(const_cast<float*>(p)), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_SYSTEM);
+  return f32x2{__uint_as_float((uint32_t)v), __uint_as_float((uint32_t)(v >> 32))};
+}
+__device__ __forceinline__ int counter_add(int32_t* c, int v) {
+  int old = 0;
+  if (lane_id() == 0) old = __hip_atomic_fetch_add(c, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  return __shfl(old, 0, 64);
+}
+__device__ __forceinline__ void counter_reset(int32_t* c) {
+  if (lane_id() == 0) __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+__device__ __forceinline__ int wave_of_chunk(int64_t c, int64_t n, int nw) {
+  int w = (int)((c * nw) / n);
+  while (w + 1 < nw && range_start(n, w + 1, nw) <= c) w++;
+  while (w > 0 && range_start(n, w, nw) > c) w--;
+  return w;
+}
+
+// Sum, in wave order, the partials of segment `seg` for token position `t` at columns
+// 2*lane and 2*lane+1.  Loads are issued in batches of 8 waves so one memory round trip
+// covers a batch; empty wave ranges contribute nothing.
+__device__ __forceinline__ void sum_partials(const float* __restrict__ partial, int64_t n, int nw, int it, int seg,
+                                             int t, float& v0, float& v1) {
+  const int64_t a = (int64_t)seg * it, b = a + it;
+  const int wa = wave_of_chunk(a, n, nw), wb = wave_of_chunk(b - 1, n, nw);
+  const int lane = lane_id();
+  v0 = 0.0f;
+  v1 = 0.0f;
+  for (int w0 = wa; w0 <= wb; w0 += 8) {
+    f32x2 p[8];
+    bool ok[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const int w = w0 + j;
+      const int64_t s = range_start(n, w, nw);
+      ok[j] = w <= wb && range_start(n, w + 1, nw) > s;
+      const int visit = (s >= a) ? 0 : 1;
+      const int64_t idx = ok[j] ? ((int64_t)w * 2 + visit) * kPartialStride + (int64_t)t * 128 + 2 * lane : 0;
+      p[j] = load_coherent2(partial + idx);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      if (ok[j]) { v0 += p[j].x; v1 += p[j].y; }
+    }
+  }
+}
+
+// Partial column order inside a 128-column block: lane L owns 16*(L/8)+L%8 (acc0) and +8 (acc1).
+__device__ __forceinline__ int col_acc0(int lane) { return 16 * (lane >> 3) + (lane & 7); }
+
+template <int NT>
+__device__ __forceinline__ void fma_word(const float f[8], const float* x, int i, float (&acc)[2]) {
+  // word i of the lane covers rows 2i, 2i+1, 2i+8, 2i+9
+  const int r0 = 2 * i;
+  acc[0] = fmaf(x[r0], f[0], acc[0]);
+  acc[0] = fmaf(x[r0 + 1], f[1], acc[0]);
+  acc[0] = fmaf(x[r0 + 8], f[2], acc[0]);
+  acc[0] = fmaf(x[r0 + 9], f[3], acc[0]);
+  acc[1] = fmaf(x[r0], f[4], acc[1]);
+  acc[1] = fmaf(x[r0 + 1], f[5], acc[1]);
+  acc[1] = fmaf(x[r0 + 8], f[6], acc[1]);
+  acc[1] = fmaf(x[r0 + 9], f[7], acc[1]);
+}
+
+template <int IM, int FM, int NT, int ALU>
+__global__ __launch_bounds__(kThreads) void k4_gemv_kernel(GemvArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t tab[65536];
+  __shared__ __attribute__((aligned(16))) float xs[IM == IN_PREP ? kWaves * NT * 128 : 4];
+
+  load_codebook_lds(tab);
+  __syncthreads();
+
+  const Plan* __restrict__ P = a.plan;
+  const int U = P->units;
+  const int it = a.in_f / 16;
+  const int obs = a.out_f / 128;
+  const int nproj = a.nproj;
+  const int64_t nseg = (int64_t)U * obs * nproj;
+  const int64_t n = nseg * it;
+  const int nw = gridDim.x * kWaves;
+  const int wave = blockIdx.x * kWaves + wave_id_in_block();
+  const int lane = lane_id();
+  const int64_t c_begin = range_start(n, wave, nw), c_end = range_start(n, wave + 1, nw);
+  float* xw = xs + (IM == IN_PREP ? wave_id_in_block() * NT * 128 : 0);
+  const int src_lane = (lane & 7) == 0 ? lane + 7 : lane - 1;
+
+  int visit = 0;
+  for (int64_t c = c_begin; c < c_end; visit++) {
+    const int seg = (int)(c / it);
+    const int tk0 = (int)(c % it);
+    const int tk1 = (int)min((int64_t)it, (int64_t)tk0 + (c_end - c));
+    const int proj = seg % nproj;
+    const int ob = (seg / nproj) % obs;
+    const int u = seg / (nproj * obs);
+    const int e = P->expert[u];
+    const int ntok = P->ntok[u];
+    const uint8_t* __restrict__ base = a.packed[proj];
+
+    float acc[NT][2];
+#pragma unroll
+    for (int t = 0; t < NT; t++) { acc[t][0] = 0.0f; acc[t][1] = 0.0f; }
+
+    // software pipeline: one chunk in flight ahead of the one being decoded
+    u32x4 next = *reinterpret_cast<const u32x4*>(base + chunk_offset(a.side, e, ob, tk0, it, obs) + lane * 16);
+    for (int tk = tk0; tk < tk1; tk++) {
+      const u32x4 v = next;
+      if (tk + 1 < tk1)
+        next = *reinterpret_cast<const u32x4*>(base + chunk_offset(a.side, e, ob, tk + 1, it, obs) + lane * 16);
+
+      if (IM == IN_PREP && (tk == tk0 || (tk & 7) == 0)) {
+        // xh for the 128-row block of tk, all rows of this unit: H128(x * in_scale[e])
+        const int blk = tk >> 3;
+        const uint16_t* __restrict__ sc = a.in_scale[proj] + (int64_t)e * a.in_f + blk * 128 + 2 * lane;
+        const float s0 = f16_to_f32(sc[0]), s1 = f16_to_f32(sc[1]);
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+          if (t < ntok) {
+            const int row = a.x_per_slot ? P->slot[u][t] : P->tok[u][t];
+            const uint16_t* __restrict__ xr = a.x_bf16 + (int64_t)row * a.in_f + blk * 128 + 2 * lane;
+            float v0 = bf16_to_f32(xr[0]) * s0, v1 = bf16_to_f32(xr[1]) * s1;
+            hadamard128_wave(v0, v1);
+            *reinterpret_cast<f32x2*>(xw + t * 128 + 2 * lane) = f32x2{v0, v1};
+          }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      }
+
+      const uint32_t prior0 = (uint32_t)__shfl((int)v.w, src_lane, 64);
+      const uint32_t W[4] = {v.x, v.y, v.z, v.w};
+      const uint32_t Pw[4] = {prior0, v.x, v.y, v.z};
+      float f[4][8];
+#pragma unroll
+      for (int i = 0; i < 4; i++) decode_word<ALU>(W[i], Pw[i], tab, f[i]);
+
+#pragma unroll
+      for (int t = 0; t < NT; t++) {
+        if (t < ntok) {
+          float x[16];
+          if (IM == IN_PREP) {
+            const f32x4* xp = reinterpret_cast<const f32x4*>(xw + t * 128 + (tk & 7) * 16);
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+              const f32x4 xv = xp[q];
+              x[4 * q] = xv.x; x[4 * q + 1] = xv.y; x[4 * q + 2] = xv.z; x[4 * q + 3] = xv.w;
+            }
+          } else {
+            const int slot = P->slot[u][t];
+            const float* __restrict__ xp = a.x_f32 + (int64_t)slot * a.in_f + tk * 16;
+#pragma unroll
+            for (int q = 0; q < 16; q++) x[q] = xp[q];
+          }
+#pragma unroll
+          for (int i = 0; i < 4; i++) fma_word<NT>(f[i], x, i, acc[t]);
+        }
+      }
+    }
+
+    // partials of this visit
+    float* pw = a.partial + ((int64_t)wave * 2 + visit) * kPartialStride;
+    const int c0 = col_acc0(lane);
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      if (t < ntok) {
+        store_coherent(pw + t * 128 + c0, acc[t][0]);
+        store_coherent(pw + t * 128 + c0 + 8, acc[t][1]);
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    const int nch = tk1 - tk0;
+    if (counter_add(&a.counter_seg[seg], nch) + nch == it) {
+      // this wave completed segment `seg`: reduce its partials once
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+      counter_reset(&a.counter_seg[seg]);
+      const int col = ob * 128 + 2 * lane;
+      if (FM == FIN_VALUES) {
+        for (int t = 0; t < ntok; t++) {
+          float v0, v1;
+          sum_partials(a.partial, n, nw, it, seg, t, v0, v1);
+          hadamard128_wave(v0, v1);
+          const int64_t si = (int64_t)e * a.out_f + col;
+          const int slot = P->slot[u][t];
+          const uint32_t packed2 = (uint32_t)f32_to_bf16(v0 * f16_to_f32(a.out_scale[0][si])) |
+                                   ((uint32_t)f32_to_bf16(v1 * f16_to_f32(a.out_scale[0][si + 1])) << 16);
+          *reinterpret_cast<uint32_t*>(a.values + (int64_t)slot * a.out_f + col) = packed2;
+        }
+      } else if (FM == FIN_GATE) {
+        for (int t = 0; t < ntok; t++) {
+          float v0, v1;
+          sum_partials(a.partial, n, nw, it, seg, t, v0, v1);
+          store_coherent2(a.segbuf + ((int64_t)seg * kMaxRows + t) * 128 + 2 * lane, v0, v1);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        const int grp = u * obs + ob;
+        if (counter_add(&a.counter_grp[grp], 1) + 1 == nproj) {
+          // gate and up of this column block are both reduced: gate finish
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+          counter_reset(&a.counter_grp[grp]);
+          for (int t = 0; t < ntok; t++) {
+            const f32x2 g = load_coherent2(a.segbuf + ((int64_t)(grp * 2 + 0) * kMaxRows + t) * 128 + 2 * lane);
+            const f32x2 uu = load_coherent2(a.segbuf + ((int64_t)(grp * 2 + 1) * kMaxRows + t) * 128 + 2 * lane);
+            float g0 = g.x, g1 = g.y, u0 = uu.x, u1 = uu.y;
+            hadamard128_wave(g0, g1);
+            hadamard128_wave(u0, u1);
+            const int64_t si = (int64_t)e * a.out_f + col;
+            float h0 = swiglu_bf16(g0 * f16_to_f32(a.out_scale[0][si]), u0 * f16_to_f32(a.out_scale[1][si]));
+            float h1 = swiglu_bf16(g1 * f16_to_f32(a.out_scale[0][si + 1]), u1 * f16_to_f32(a.out_scale[1][si + 1]));
+            h0 *= f16_to_f32(a.in_down[si]);
+            h1 *= f16_to_f32(a.in_down[si + 1]);
+            hadamard128_wave(h0, h1);
+            const int slot = P->slot[u][t];
+            *reinterpret_cast<f32x2*>(a.down_xh + (int64_t)slot * a.out_f + col) = f32x2{h0, h1};
+          }
+        }
+      } else {
+        // per-slot expert output of this column block: T(H128(inner) * out_scale)
+        for (int t = 0; t < ntok; t++) {
+          float v0, v1;
+          sum_partials(a.partial, n, nw, it, seg, t, v0, v1);
+          hadamard128_wave(v0, v1);
+          const int64_t si = (int64_t)e * a.out_f + col;
+          const int slot = P->slot[u][t];
+          store_coherent2(a.yslot + (int64_t)slot * a.out_f + col, round_bf16(v0 * f16_to_f32(a.out_scale[0][si])),
+                          round_bf16(v1 * f16_to_f32(a.out_scale[0][si + 1])));
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        if (counter_add(&a.counter_grp[ob], 1) + 1 == U) {
+          // every unit of this column block is done: weighted routed sum, shared, residual
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+          counter_reset(&a.counter_grp[ob]);
+          for (int r = 0; r < P->rows; r++) {
+            f32x2 y[kSlots];
+#pragma unroll
+            for (int j = 0; j < kSlots; j++) y[j] = load_coherent2(a.yslot + (int64_t)(r * kSlots + j) * a.out_f + col);
+            float tot0 = y[0].x * a.scores[r * 8] + 0.0f, tot1 = y[0].y * a.scores[r * 8] + 0.0f;
+#pragma unroll
+            for (int j = 1; j < 8; j++) {
+              const float sc = a.scores[r * 8 + j];
+              tot0 = (y[j].x * sc + 0.0f) + tot0;
+              tot1 = (y[j].y * sc + 0.0f) + tot1;
+            }
+            const float c0f = round_bf16(round_bf16(tot0) + y[8].x);
+            const float c1f = round_bf16(round_bf16(tot1) + y[8].y);
+            const int64_t o = (int64_t)r * a.out_f + col;
+            const uint16_t* res = a.residual + o;
+            const uint32_t packed2 = (uint32_t)f32_to_bf16(bf16_to_f32(res[0]) + c0f) |
+                                     ((uint32_t)f32_to_bf16(bf16_to_f32(res[1]) + c1f) << 16);
+            *reinterpret_cast<uint32_t*>(a.out + o) = packed2;
+          }
+        }
+      }
+    }
+    c += tk1 - tk0;
+  }
+}
+
+// ============================================================== host side
+
+namespace {
+
+struct DeviceState {
+  bool ready = false;
+  int cus = 0;
+};
+std::mutex g_mutex;
+DeviceState g_devices[64];
+thread_local char g_error[512];
+thread_local hipEvent_t g_prof_events[4];
+
+}  // namespace
+
+// Record the armed profiling event `slot` on `s` (and disarm it).
+static void prof_mark(int slot, hipStream_t s) {
+  if (g_prof_events[slot]) {
+    (void)hipEventRecord(g_prof_events[slot], s);
+    g_prof_events[slot] = nullptr;
+  }
+}
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_error, sizeof(g_error), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int ensure_device_ready() {
+  int dev = 0;
+  MOE_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= 64) return fail(MOE_ENOTSUP, "device index %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_mutex);
+  DeviceState& st = g_devices[dev];
+  if (st.ready) return MOE_OK;
+  MOE_HIP(hipDeviceGetAttribute(&st.cus, hipDeviceAttributeMultiprocessorCount, dev));
+  hipLaunchKernelGGL(build_codebook_kernel, dim3(128), dim3(256), 0, 0);
+  MOE_HIP(hipGetLastError());
+  MOE_HIP(hipDeviceSynchronize());
+  st.ready = true;
+  return MOE_OK;
+}
+
+int device_cus() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  return g_devices[dev].cus;
+}
+
+// ---------------------------------------------------------------- workspace layout
+namespace {
+
+struct Workspace {
+  Plan* plan;
+  int32_t* counter_seg; // per-segment chunk counters (self-cleaning)
+  int32_t* counter_grp; // per-group segment counters (self-cleaning)
+  int32_t* router_counter;
+  float* partial;       // [kMaxWaves][2][kPartialStride]
+  float* segbuf;        // [kMaxWaves segments][kMaxRows][128]
+  float* yslot;         // [kMaxUnits][hidden]
+  float* down_xh;       // [kMaxUnits][inter]
+  float* logits;        // [kMaxRows][256]
+  uint32_t* ids;        // [kMaxRows][9]
+  float* scores;        // [kMaxRows][8]
+  size_t bytes;
+};
+
+constexpr size_t kCounters = 4096;
+
+size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
+
+Workspace carve(void* base, int hidden, int inter) {
+  Workspace w{};
+  size_t off = 0;
+  char* p = static_cast<char*>(base);
+  auto take = [&](size_t bytes) { char* r = p ? p + off : nullptr; off += align_up(bytes); return r; };
+  w.plan = reinterpret_cast<Plan*>(take(sizeof(Plan)));
+  w.counter_seg = reinterpret_cast<int32_t*>(take(kCounters * 4));
+  w.counter_grp = reinterpret_cast<int32_t*>(take(kCounters * 4));
+  w.router_counter = reinterpret_cast<int32_t*>(take(256));
+  w.partial = reinterpret_cast<float*>(take((size_t)kMaxWaves * 2 * kPartialStride * 4));
+  w.segbuf = reinterpret_cast<float*>(take((size_t)kMaxWaves * kMaxRows * 128 * 4));
+  w.yslot = reinterpret_cast<float*>(take((size_t)kMaxUnits * hidden * 4));
+  w.down_xh = reinterpret_cast<float*>(take((size_t)kMaxUnits * inter * 4));
+  w.logits = reinterpret_cast<float*>(take((size_t)kMaxRows * 256 * 4));
+  w.ids = reinterpret_cast<uint32_t*>(take((size_t)kMaxRows * 9 * 4));
+  w.scores = reinterpret_cast<float*>(take((size_t)kMaxRows * 8 * 4));
+  w.bytes = off;
+  return w;
+}
+
+int grid_blocks() {
+  int cus = device_cus();
+  return cus < 1 ? 1 : (cus > kMaxBlocks ? kMaxBlocks : cus);
+}
+
+// Every wave's static chunk range must span at most two segments (the partial buffer holds two
+// visits per wave), which holds when the number of waves is at least the number of segments.
+template <int IM, int FM>
+int launch_gemv(const GemvArgs& a, int max_ntok, int max_units, hipStream_t stream) {
+  const int64_t nseg_max = (int64_t)max_units * (a.out_f / 128) * a.nproj;
+  if (nseg_max > kMaxWaves)
+    return fail(MOE_ENOTSUP, "too many (unit, column block) segments: %lld > %d", (long long)nseg_max, kMaxWaves);
+  int blocks = grid_blocks();
+  const int need = (int)((nseg_max + kWaves - 1) / kWaves);
+  if (blocks < need) blocks = need;
+  const dim3 grid(blocks), block(kThreads);
+  if (max_ntok <= 1)
+    hipLaunchKernelGGL((k4_gemv_kernel<IM, FM, 1, 1>), grid, block, 0, stream, a);
+  else
+    hipLaunchKernelGGL((k4_gemv_kernel<IM, FM, kMaxRows, 1>), grid, block, 0, stream, a);
+  MOE_HIP(hipGetLastError());
+  return MOE_OK;
+}
+
+int check_trellis(int64_t bytes, int in_f, int out_f, int64_t* experts) {
+  MOE_ARG(in_f > 0 && out_f > 0 && in_f % 128 == 0 && out_f % 128 == 0,
+          "trellis dimensions must be positive multiples of 128");
+  const int64_t size = (int64_t)in_f * out_f / 2;
+  MOE_ARG(bytes > 0 && bytes % size == 0, "packed byte count does not match the trellis dimensions");
+  *experts = bytes / size;
+  return MOE_OK;
+}
+
+}  // namespace
+
+}  // namespace moe
+
+using namespace moe;
+
+extern "C" {
+
+const char* moe_version(void) { return "mlxlr8_amd 0.1.0 (gfx950)"; }
+const char* moe_last_error(void) { return g_error; }
+
+int moe_init(void) { return ensure_device_ready(); }
+
+int moe_codebook_e4m3(uint8_t* dst, moe_stream_t stream) {
+  MOE_ARG(dst != nullptr, "dst must not be NULL");
+  int rc = ensure_device_ready();
+  if (rc) return rc;
+  hipLaunchKernelGGL(copy_codebook_kernel, dim3(256), dim3(256), 0, (hipStream_t)stream, dst);
+  MOE_HIP(hipGetLastError());
+  return MOE_OK;
+}
+
+int moe_profile_events(void** events, int count) {
+  MOE_ARG(count >= 0 && count <= 4, "count must be in 0..4");
+  for (int i = 0; i < 4; i++) g_prof_events[i] = (events && i < count) ? (hipEvent_t)events[i] : nullptr;
+  return MOE_OK;
+}
+
+size_t moe_workspace_bytes(int hidden, int intermediate) {
+  (void)hidden;
+  return carve(nullptr, hidden > 0 ? hidden : 1, intermediate > 0 ? intermediate : 1).bytes;
+}
+
+int moe_trellis_decode_f16(const void* packed, int64_t packed_bytes, int k, int in_f, int out_f, int side,
+                           int64_t expert, uint16_t* inner, moe_stream_t stream) {
+  MOE_ARG(k == 4, "this build decodes K4 trellis only (got k=%d)", k);
+  MOE_ARG(side >= 0 && side <= 2, "sharded_side must be 0, 1, or 2");
+  MOE_ARG(packed && inner, "packed and inner must not be NULL");
+  int64_t experts = 0;
+  int rc = check_trellis(packed_bytes, in_f, out_f, &experts);
+  if (rc) return rc;
+  MOE_ARG(expert >= 0 && expert < experts, "expert %lld out of range (%lld experts)", (long long)expert,
+          (long long)experts);
+  rc = ensure_device_ready();
+  if (rc) return rc;
+  const int64_t total = (int64_t)in_f * out_f;
+  hipLaunchKernelGGL(trellis_decode_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, (const uint32_t*)packed, in_f, out_f, side, expert, inner);
+  MOE_HIP(hipGetLastError());
+  return MOE_OK;
+}
+
+static int validate_ws(void* workspace, size_t bytes, int hidden, int inter) {
+  MOE_ARG(workspace != nullptr, "workspace must not be NULL");
+  const size_t need = carve(nullptr, hidden, inter).bytes;
+  if (bytes < need) return fail(MOE_EWORKSPACE, "workspace too small: %zu < %zu bytes", bytes, need);
+  return MOE_OK;
+}
+
+int moe_k4_expert_linear(const uint16_t* x, int x_per_slot, const uint32_t* ids, int rows, int slots,
+                         const void* packed, int64_t packed_bytes, const uint16_t* in_scale,
+                         const uint16_t* out_scale, int in_f, int out_f, int side, uint16_t* y, void* workspace,
+                         size_t workspace_bytes, moe_stream_t stream) {
+  MOE_ARG(x && ids && packed && in_scale && out_scale && y, "null pointer argument");
+  MOE_ARG(rows >= 1 && slots >= 1 && slots <= kSlots && rows * slots <= kMaxUnits,
+          "rows*slots must be in 1..%d with slots <= %d", kMaxUnits, kSlots);
+  MOE_ARG(side >= 0 && side <= 2, "sharded_side must be 0, 1, or 2");
+  int64_t experts = 0;
+  int rc = check_trellis(packed_bytes, in_f, out_f, &experts);
+  if (rc) return rc;
+  const int wdim = out_f > in_f ? out_f : in_f;
+  if ((rc = validate_ws(workspace, workspace_bytes, wdim, wdim))) return rc;
+  if ((rc = ensure_device_ready())) return rc;
+  Workspace w = carve(workspace, wdim, wdim);
+  hipStream_t s = (hipStream_t)stream;
+  const int max_users = (x_per_slot || rows == 1) ? 1 : kMaxRows;
+  hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(64), 0, s, ids, rows, slots, (int)(experts > 257 ? 257 : experts),
+                     max_users, w.plan);
+  MOE_HIP(hipGetLastError());
+  GemvArgs a{};
+  a.packed[0] = (const uint8_t*)packed;
+  a.nproj = 1;
+  a.in_f = in_f; a.out_f = out_f; a.side = side;
+  a.x_per_slot = x_per_slot;
+  a.x_bf16 = x;
+  a.in_scale[0] = in_scale;
+  a.plan = w.plan;
+  a.partial = w.partial;
+  a.counter_seg = w.counter_seg;
+  a.counter_grp = w.counter_grp;
+  a.out_scale[0] = out_scale;
+  a.values = y;
+  return launch_gemv<IN_PREP, FIN_VALUES>(a, max_users, rows * slots, s);
+}
+
+static int k4_mlp_common(const uint16_t* x, const uint32_t* ids, const float* scores, const uint16_t* residual,
+                         int rows, int slots, const void* pg, const void* pu, const void* pd, int64_t bytes,
+                         const uint16_t* in_g, const uint16_t* out_g, const uint16_t* in_u, const uint16_t* out_u,
+                         const uint16_t* in_d, const uint16_t* out_d, int h, int m, uint16_t* values, uint16_t* out,
+                         void* workspace, size_t workspace_bytes, hipStream_t s, bool ids_on_plan) {
+  MOE_ARG(x && pg && pu && pd && in_g && out_g && in_u && out_u && in_d && out_d, "null pointer argument");
+  MOE_ARG(rows >= 1 && rows <= kMaxRows && slots >= 1 && slots <= kSlots,
+          "rows must be in 1..%d and slots in 1..%d", kMaxRows, kSlots);
+  int64_t experts = 0;
+  int rc = check_trellis(bytes, h, m, &experts);
+  if (rc) return rc;
+  MOE_ARG(experts >= 1, "no experts");
+  if ((rc = validate_ws(workspace, workspace_bytes, h, m))) return rc;
+  if ((rc = ensure_device_ready())) return rc;
+  Workspace w = carve(workspace, h, m);
+  const int max_users = rows == 1 ? 1 : kMaxRows;
+  if (!ids_on_plan) {
+    MOE_ARG(ids != nullptr, "ids must not be NULL");
+    hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(64), 0, s, ids, rows, slots, (int)(experts > 257 ? 257 : experts),
+                       max_users, w.plan);
+    MOE_HIP(hipGetLastError());
+  }
+  GemvArgs g{};
+  g.packed[0] = (const uint8_t*)pg;
+  g.packed[1] = (const uint8_t*)pu;
+  g.nproj = 2;
+  g.in_f = h; g.out_f = m; g.side = 1;
+  g.x_bf16 = x;
+  g.in_scale[0] = in_g; g.in_scale[1] = in_u;
+  g.plan = w.plan;
+  g.partial = w.partial;
+  g.counter_seg = w.counter_seg;
+  g.counter_grp = w.counter_grp;
+  g.segbuf = w.segbuf;
+  g.out_scale[0] = out_g; g.out_scale[1] = out_u;
+  g.in_down = in_d;
+  g.down_xh = w.down_xh;
+  prof_mark(1, s);
+  if ((rc = launch_gemv<IN_PREP, FIN_GATE>(g, max_users, rows * slots, s))) return rc;
+  prof_mark(2, s);
+
+  GemvArgs d{};
+  d.packed[0] = (const uint8_t*)pd;
+  d.nproj = 1;
+  d.in_f = m; d.out_f = h; d.side = 2;
+  d.x_f32 = w.down_xh;
+  d.plan = w.plan;
+  d.partial = w.partial;
+  d.out_scale[0] = out_d;
+  if (out) {
+    MOE_ARG(slots == kSlots && scores && residual, "the combined finish needs 9 slots, scores and residual");
+    d.counter_seg = w.counter_seg;
+    d.counter_grp = w.counter_grp;
+    d.yslot = w.yslot;
+    d.scores = scores;
+    d.residual = residual;
+    d.out = out;
+    rc = launch_gemv<IN_DIRECT, FIN_COMBINE>(d, max_users, rows * slots, s);
+    prof_mark(3, s);
+    return rc;
+  }
+  d.counter_seg = w.counter_seg;
+  d.counter_grp = w.counter_grp;
+  d.values = values;
+  return launch_gemv<IN_DIRECT, FIN_VALUES>(d, max_users, rows * slots, s);
+}
+
+int moe_k4_mlp(const uint16_t* x, const uint32_t* ids, int rows, int slots, const void* packed_gate,
+               const void* packed_up, const void* packed_down, int64_t packed_bytes, const uint16_t* in_gate,
+               const uint16_t* out_gate, const uint16_t* in_up, const uint16_t* out_up, const uint16_t* in_down,
+               const uint16_t* out_down, int hidden, int intermediate, uint16_t* values, void* workspace,
+               size_t workspace_bytes, moe_stream_t stream) {
+  MOE_ARG(values != nullptr, "values must not be NULL");
+  return k4_mlp_common(x, ids, nullptr, nullptr, rows, slots, packed_gate, packed_up, packed_down, packed_bytes,
+                       in_gate, out_gate, in_up, out_up, in_down, out_down, hidden, intermediate, values, nullptr,
+                       workspace, workspace_bytes, (hipStream_t)stream, false);
+}
+
+int moe_k4_mlp_finish(const uint16_t* x, const uint32_t* ids, const float* scores, const uint16_t* residual, int rows,
+                      const void* packed_gate, const void* packed_up, const void* packed_down, int64_t packed_bytes,
+                      const uint16_t* in_gate, const uint16_t* out_gate, const uint16_t* in_up,
+                      const uint16_t* out_up, const uint16_t* in_down, const uint16_t* out_down, int hidden,
+                      int intermediate, uint16_t* out, void* workspace, size_t workspace_bytes,
+                      moe_stream_t stream) {
+  MOE_ARG(out != nullptr, "out must not be NULL");
+  return k4_mlp_common(x, ids, scores, residual, rows, kSlots, packed_gate, packed_up, packed_down, packed_bytes,
+                       in_gate, out_gate, in_up, out_up, in_down, out_down, hidden, intermediate, nullptr, out,
+                       workspace, workspace_bytes, (hipStream_t)stream, false);
+}
+
+int moe_k4_moe_decode(const uint16_t* x, const uint16_t* residual, int rows, const float* router_w, const float* bias,
+                      const void* packed_gate, const void* packed_up, const void* packed_down, int64_t packed_bytes,
+                      const uint16_t* in_gate, const uint16_t* out_gate, const uint16_t* in_up,
+                      const uint16_t* out_up, const uint16_t* in_down, const uint16_t* out_down, int hidden,
+                      int intermediate, uint16_t* out, uint32_t* indices, float* scores, void* workspace,
+                      size_t workspace_bytes, moe_stream_t stream) {
+  MOE_ARG(x && residual && router_w && bias && out, "null pointer argument");
+  MOE_ARG(rows >= 1 && rows <= kMaxRows, "rows must be in 1..%d", kMaxRows);
+  int rc = validate_ws(workspace, workspace_bytes, hidden, intermediate);
+  if (rc) return rc;
+  if ((rc = ensure_device_ready())) return rc;
+  Workspace w = carve(workspace, hidden, intermediate);
+  hipStream_t s = (hipStream_t)stream;
+  uint32_t* ids = indices ? indices : w.ids;
+  float* sc = scores ? scores : w.scores;
+  int64_t experts = 0;
+  if ((rc = check_trellis(packed_bytes, hidden, intermediate, &experts))) return rc;
+  MOE_ARG(experts == 257, "the routed decode block needs 256 routed experts plus the shared expert (got %lld)",
+          (long long)experts);
+  prof_mark(0, s);
+  rc = moe_router_fused_plan(x, router_w, bias, rows, hidden, 257, w.logits, ids, sc, w.plan, w.router_counter, s);
+  if (rc) return rc;
+  return k4_mlp_common(x, ids, sc, residual, rows, kSlots, packed_gate, packed_up, packed_down, packed_bytes, in_gate,
+                       out_gate, in_up, out_up, in_down, out_down, hidden, intermediate, nullptr, out, workspace,
+                       workspace_bytes, s, true);
+}
+
+}  // extern "C"

@@ -1,0 +1,37 @@
+// Host-side helpers shared by the C-ABI entry points: error reporting and per-device setup.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/moe_mi355x.h"
+#include "moe_plan.h"
+
+namespace moe {
+
+// Record a message for moe_last_error() and return `code`.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
+// Build the E4M3 codebook table on the current device once (thread-safe).
+int ensure_device_ready();
+
+// Number of compute units of the current device (cached per device).
+int device_cus();
+
+// Router GEMV + route + dispatch plan for decode batches (router.hip).
+int moe_router_fused_plan(const uint16_t* x, const float* w, const float* bias, int rows, int hidden, int experts,
+                          float* logits, uint32_t* ids, float* scores, Plan* plan, int32_t* counter,
+                          hipStream_t stream);
+
+}  // namespace moe
+
+#define MOE_HIP(expr)                                                              \
+  do {                                                                             \
+    hipError_t e_ = (expr);                                                        \
+    if (e_ != hipSuccess)                                                          \
+      return ::moe::fail((int)e_, "%s failed: %s", #expr, hipGetErrorString(e_));  \
+  } while (0)
+
+#define MOE_ARG(cond, ...)                                       \
+  do {                                                           \
+    if (!(cond)) return ::moe::fail(MOE_EINVAL, __VA_ARGS__);    \
+  } while (0)

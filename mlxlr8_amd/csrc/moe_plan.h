@@ -1,0 +1,65 @@
+// Token -> expert dispatch plan for decode-sized batches (up to 8 token rows, 9 slots each).
+//
+// The reference appends the shared expert (id 256) to the routed top-8 (exlr8/model.py:407-408)
+// and, for 2-4 rows, de-duplicates repeated experts so each expert's weights are read once
+// (REUSE_ROWS in exlr8/metal/fast_decode_linear.metal:36-61).  Here every distinct expert of
+// the batch becomes one "unit" that carries the list of token rows that selected it; the
+// GEMV kernels stream each unit's weights once and apply them to all of its rows.
+#pragma once
+#include <stdint.h>
+
+namespace moe {
+
+constexpr int kMaxRows = 8;             // token rows per plan
+constexpr int kSlots = 9;               // 8 routed + 1 shared
+constexpr int kMaxUnits = kMaxRows * kSlots;
+
+struct Plan {
+  int32_t units;                        // number of distinct experts U
+  int32_t rows;                         // token rows
+  int32_t pad[2];
+  int32_t expert[kMaxUnits];            // expert id of unit u
+  int32_t ntok[kMaxUnits];              // rows that use unit u
+  int32_t tok[kMaxUnits][kMaxRows];     // row index of the i-th user of unit u
+  int32_t slot[kMaxUnits][kMaxRows];    // slot index row*9 + j of the i-th user of unit u
+  int32_t slot_unit[kMaxUnits];         // unit of slot s
+  int32_t slot_pos[kMaxUnits];          // position of slot s inside its unit's row list
+};
+
+// Build the plan from indices [rows, slots] in first-appearance order (serial; <= 72 slots).
+// A unit holds at most `max_users` rows; further users of the same expert open a new unit,
+// so the kernels' per-unit row arrays never overflow.  Ids outside 0..experts-1 are clamped
+// to keep every weight access in bounds (callers validate ids beforehand).
+// `unit_of_expert` (257 entries) must hold -1 on entry (see build_plan below).
+__device__ inline void build_plan_serial(const uint32_t* idx, int rows, int slots, int experts, int max_users,
+                                         Plan* plan, int32_t* unit_of_expert) {
+  int units = 0;
+  for (int s = 0; s < rows * slots; s++) {
+    int e = (int)idx[s];
+    if (e < 0) e = 0;
+    if (e >= experts) e = experts - 1;
+    if (e > 256) e = 256;
+    int u = unit_of_expert[e];
+    if (u < 0 || plan->ntok[u] >= max_users) {
+      u = units++;
+      unit_of_expert[e] = u;
+      plan->expert[u] = e;
+      plan->ntok[u] = 0;
+    }
+    int i = plan->ntok[u]++;
+    plan->tok[u][i] = s / slots;
+    plan->slot[u][i] = s;
+    plan->slot_unit[s] = u;
+    plan->slot_pos[s] = i;
+  }
+  plan->units = units;
+  plan->rows = rows;
+}
+
+__device__ inline void build_plan(const uint32_t* idx, int rows, int slots, int experts, int max_users, Plan* plan,
+                                  int32_t* unit_of_expert /* 257 */) {
+  for (int e = 0; e < 257; e++) unit_of_expert[e] = -1;
+  build_plan_serial(idx, rows, slots, experts, max_users, plan, unit_of_expert);
+}
+
+}  // namespace moe

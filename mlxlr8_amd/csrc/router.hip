@@ -1,0 +1,283 @@
+// Router for the MoE expert path on gfx950: fp32 gate GEMV, sigmoid, bias-corrected top-8.
+//
+// Reference semantics (paths relative to the reference root):
+//   logits = f32(x) @ W^T with an fp32 weight          exlr8/dense.py:158-159, exlr8/model.py:367-370,406
+//   s = v < 0 ? y : 1 - y, y = 1 / (1 + exp(|v|))        exlr8/metal/fast_router.metal:7-9
+//   top-8 of s + bias, descending, ties -> lower id      exlr8/metal/fast_router.metal:13-34
+//   score = s / (1e-20 + sum s_sel) * 2.5, slot 8 = 256  exlr8/metal/fast_router.metal:35-42
+//
+// MI355X design: one wave (64 lanes, 4 experts per lane) per token row; the arg-max of each
+// of the 8 rounds is a 6-step butterfly over (value, id) pairs, so every lane learns the
+// winner without a second pass.  For decode batches the same block also builds the
+// token -> expert dispatch plan, so no route ever travels back to the host.
+#include <hip/hip_runtime.h>
+
+#include "moe_device.h"
+#include "moe_host.h"
+#include "moe_plan.h"
+
+namespace moe {
+
+// ---------------------------------------------------------------- logits, small batches
+// One block per expert row; each thread covers hidden/256 inputs with 16-byte loads.
+template <int R>
+__global__ __launch_bounds__(256) void router_logits_small(const uint16_t* __restrict__ x,
+                                                           const float* __restrict__ w, int rows, int hidden,
+                                                           int experts, float* __restrict__ logits) {
+  const int e = blockIdx.x;
+  const float* __restrict__ we = w + (int64_t)e * hidden;
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; r++) acc[r] = 0.0f;
+  for (int k = threadIdx.x * 4; k < hidden; k += 256 * 4) {
+    const f32x4 wv = *reinterpret_cast<const f32x4*>(we + k);
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      if (r < rows) {
+        const u32x2 xv = *reinterpret_cast<const u32x2*>(x + (int64_t)r * hidden + k);
+        acc[r] = fmaf(bf16_to_f32((uint16_t)(xv.x & 0xFFFFu)), wv.x, acc[r]);
+        acc[r] = fmaf(bf16_to_f32((uint16_t)(xv.x >> 16)), wv.y, acc[r]);
+        acc[r] = fmaf(bf16_to_f32((uint16_t)(xv.y & 0xFFFFu)), wv.z, acc[r]);
+        acc[r] = fmaf(bf16_to_f32((uint16_t)(xv.y >> 16)), wv.w, acc[r]);
+      }
+    }
+  }
+  __shared__ float red[R][4];
+  const int lane = lane_id(), wv = wave_id_in_block();
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    float v = acc[r];
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    if (lane == 0) red[r][wv] = v;
+  }
+  __syncthreads();
+  if (threadIdx.x < R && (int)threadIdx.x < rows) {
+    const int r = threadIdx.x;
+    logits[(int64_t)r * experts + e] = (red[r][0] + red[r][1]) + (red[r][2] + red[r][3]);
+  }
+}
+
+// ---------------------------------------------------------------- logits, prefill batches
+// 64 rows x 64 experts per block, K staged through LDS in fp32, 4x4 outputs per thread.
+__global__ __launch_bounds__(256) void router_logits_tiled(const uint16_t* __restrict__ x,
+                                                           const float* __restrict__ w, int rows, int hidden,
+                                                           int experts, float* __restrict__ logits) {
+  __shared__ float xs[32][64 + 1];
+  __shared__ float ws[32][64 + 1];
+  const int r0 = blockIdx.y * 64, e0 = blockIdx.x * 64;
+  const int tr = threadIdx.x / 16, te = threadIdx.x % 16;
+  float acc[4][4] = {};
+  for (int k0 = 0; k0 < hidden; k0 += 32) {
+    for (int i = threadIdx.x; i < 64 * 32; i += 256) {
+      const int rr = i / 32, kk = i % 32;
+      const int gr = r0 + rr, ge = e0 + rr;
+      xs[kk][rr] = gr < rows ? bf16_to_f32(x[(int64_t)gr * hidden + k0 + kk]) : 0.0f;
+      ws[kk][rr] = ge < experts ? w[(int64_t)ge * hidden + k0 + kk] : 0.0f;
+    }
+    __syncthreads();
+#pragma unroll 4
+    for (int kk = 0; kk < 32; kk++) {
+      float xv[4], wv[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) { xv[i] = xs[kk][tr * 4 + i]; wv[i] = ws[kk][te * 4 + i]; }
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = fmaf(xv[i], wv[j], acc[i][j]);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int gr = r0 + tr * 4 + i, ge = e0 + te * 4 + j;
+      if (gr < rows && ge < experts) logits[(int64_t)gr * experts + ge] = acc[i][j];
+    }
+}
+
+// ---------------------------------------------------------------- selection
+__device__ __forceinline__ float router_sigmoid(float v) {
+  const float y = 1.0f / (1.0f + expf(fabsf(v)));
+  return v < 0.0f ? y : 1.0f - y;
+}
+
+// One wave per row.  Lane l owns experts l, l+64, l+128, l+192.  COHERENT reads logits that
+// other blocks of the same launch wrote (L2-bypassing loads).
+template <bool COHERENT = false>
+__device__ __forceinline__ void route_row(const float* __restrict__ logits, const float* __restrict__ bias, int row,
+                                          uint32_t* __restrict__ ids, float* __restrict__ scores) {
+  const int lane = lane_id();
+  float orig[4], choice[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int e = lane + 64 * i;
+    const float* lp = logits + (int64_t)row * 256 + e;
+    const float lv = COHERENT ? __hip_atomic_load(const_cast<float*>(lp), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM)
+                              : *lp;
+    orig[i] = router_sigmoid(lv);
+    choice[i] = orig[i] + bias[e];
+  }
+  float sel[8];
+#pragma unroll
+  for (int rank = 0; rank < 8; rank++) {
+    float best = -INFINITY;
+    int idx = 256;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int e = lane + 64 * i;
+      if (choice[i] > best || (choice[i] == best && e < idx)) { best = choice[i]; idx = e; }
+    }
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+      const float ob = __shfl_xor(best, m, 64);
+      const int oi = __shfl_xor(idx, m, 64);
+      if (ob > best || (ob == best && oi < idx)) { best = ob; idx = oi; }
+    }
+    // weight of the winner: its lane holds orig[idx / 64]
+    const int owner = idx & 63, slot = idx >> 6;
+    float mine = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) if (i == slot) mine = orig[i];
+    sel[rank] = __shfl(mine, owner, 64);
+    if (lane == owner) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) if (i == slot) choice[i] = -INFINITY;
+    }
+    if (lane == 0) ids[(int64_t)row * 9 + rank] = (uint32_t)idx;
+  }
+  if (lane == 0) {
+    float total = 1e-20f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) total += sel[i];
+#pragma unroll
+    for (int i = 0; i < 8; i++) scores[(int64_t)row * 8 + i] = sel[i] / total * 2.5f;
+    ids[(int64_t)row * 9 + 8] = 256u;
+  }
+}
+
+__global__ __launch_bounds__(64) void route_kernel(const float* __restrict__ logits, const float* __restrict__ bias,
+                                                   int rows, uint32_t* __restrict__ ids, float* __restrict__ scores) {
+  const int row = blockIdx.x;
+  if (row < rows) route_row(logits, bias, row, ids, scores);
+}
+
+// Decode batches in one launch: block e computes logit e of every row; the last block to finish
+// routes all rows (one wave per row) and builds the token -> expert dispatch plan.
+template <int R>
+__global__ __launch_bounds__(256) void router_decode_kernel(const uint16_t* __restrict__ x,
+                                                            const float* __restrict__ w,
+                                                            const float* __restrict__ bias, int rows, int hidden,
+                                                            int experts, int max_users, float* logits,
+                                                            uint32_t* ids, float* __restrict__ scores, Plan* plan,
+                                                            int32_t* counter) {
+  const int e = blockIdx.x;
+  const float* __restrict__ we = w + (int64_t)e * hidden;
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; r++) acc[r] = 0.0f;
+  for (int k = threadIdx.x * 4; k < hidden; k += 256 * 4) {
+    const f32x4 wv = *reinterpret_cast<const f32x4*>(we + k);
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      if (r < rows) {
+        const u32x2 xv = *reinterpret_cast<const u32x2*>(x + (int64_t)r * hidden + k);
+        acc[r] = fmaf(bf16_to_f32((uint16_t)(xv.x & 0xFFFFu)), wv.x, acc[r]);
+        acc[r] = fmaf(bf16_to_f32((uint16_t)(xv.x >> 16)), wv.y, acc[r]);
+        acc[r] = fmaf(bf16_to_f32((uint16_t)(xv.y & 0xFFFFu)), wv.z, acc[r]);
+        acc[r] = fmaf(bf16_to_f32((uint16_t)(xv.y >> 16)), wv.w, acc[r]);
+      }
+    }
+  }
+  __shared__ float red[R][4];
+  __shared__ int last;
+  __shared__ int32_t unit_of_expert[257];
+  const int lane = lane_id(), wv = wave_id_in_block();
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    float v = acc[r];
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    if (lane == 0) red[r][wv] = v;
+  }
+  __syncthreads();
+  if (threadIdx.x < R && (int)threadIdx.x < rows) {
+    const int r = threadIdx.x;
+    const float lg = (red[r][0] + red[r][1]) + (red[r][2] + red[r][3]);
+    __hip_atomic_store(logits + (int64_t)r * 256 + e, lg, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __syncthreads();
+  if (threadIdx.x == 0)
+    last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) == (int)gridDim.x - 1;
+  __syncthreads();
+  if (!last) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  for (int i = threadIdx.x; i < 257; i += blockDim.x) unit_of_expert[i] = -1;
+  for (int row = wv; row < rows; row += 4) route_row<true>(logits, bias, row, ids, scores);
+  __threadfence_block();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    build_plan_serial(ids, rows, kSlots, experts, max_users, plan, unit_of_expert);
+    __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
+}
+
+int launch_router_logits(const uint16_t* x, const float* w, int rows, int hidden, int experts, float* logits,
+                         hipStream_t s) {
+  if (rows <= 1) {
+    hipLaunchKernelGGL(router_logits_small<1>, dim3(experts), dim3(256), 0, s, x, w, rows, hidden, experts, logits);
+  } else if (rows <= kMaxRows) {
+    hipLaunchKernelGGL(router_logits_small<kMaxRows>, dim3(experts), dim3(256), 0, s, x, w, rows, hidden, experts,
+                       logits);
+  } else {
+    dim3 grid((experts + 63) / 64, (rows + 63) / 64);
+    hipLaunchKernelGGL(router_logits_tiled, grid, dim3(256), 0, s, x, w, rows, hidden, experts, logits);
+  }
+  MOE_HIP(hipGetLastError());
+  return MOE_OK;
+}
+
+// Router GEMV + route + dispatch plan for decode batches (used by moe_k4_moe_decode).
+int moe_router_fused_plan(const uint16_t* x, const float* w, const float* bias, int rows, int hidden, int experts,
+                          float* logits, uint32_t* ids, float* scores, Plan* plan, int32_t* counter, hipStream_t s) {
+  MOE_ARG(hidden > 0 && hidden % 1024 == 0, "router hidden size must be a positive multiple of 1024");
+  MOE_ARG(rows >= 1 && rows <= kMaxRows, "decode routing handles 1..%d rows", kMaxRows);
+  const int max_users = rows == 1 ? 1 : kMaxRows;
+  if (rows == 1)
+    hipLaunchKernelGGL(router_decode_kernel<1>, dim3(256), dim3(256), 0, s, x, w, bias, rows, hidden, experts,
+                       max_users, logits, ids, scores, plan, counter);
+  else
+    hipLaunchKernelGGL(router_decode_kernel<kMaxRows>, dim3(256), dim3(256), 0, s, x, w, bias, rows, hidden, experts,
+                       max_users, logits, ids, scores, plan, counter);
+  MOE_HIP(hipGetLastError());
+  return MOE_OK;
+}
+
+}  // namespace moe
+
+using namespace moe;
+
+extern "C" {
+
+int moe_route_f32(const float* logits, const float* bias, int rows, uint32_t* indices, float* scores,
+                  moe_stream_t stream) {
+  MOE_ARG(logits && bias && indices && scores, "null pointer argument");
+  MOE_ARG(rows >= 0, "rows must be non-negative");
+  if (rows == 0) return MOE_OK;
+  hipLaunchKernelGGL(route_kernel, dim3(rows), dim3(64), 0, (hipStream_t)stream, logits, bias, rows, indices, scores);
+  MOE_HIP(hipGetLastError());
+  return MOE_OK;
+}
+
+int moe_router_logits(const uint16_t* x, const float* w, int rows, int hidden, int experts, float* logits,
+                      moe_stream_t stream) {
+  MOE_ARG(x && w && logits, "null pointer argument");
+  MOE_ARG(rows >= 0 && experts > 0, "rows must be non-negative and experts positive");
+  MOE_ARG(hidden > 0 && hidden % 1024 == 0, "router hidden size must be a positive multiple of 1024");
+  if (rows == 0) return MOE_OK;
+  return launch_router_logits(x, w, rows, hidden, experts, logits, (hipStream_t)stream);
+}
+
+}  // extern "C"

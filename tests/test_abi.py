@@ -1,0 +1,71 @@
+"""The C-ABI library loads on a CPU-only host and exports every symbol include/moe_mi355x.h declares.
+No compute is launched here (there is no GPU in the CPU test tier)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def _declared():
+    text = (ROOT / "include" / "moe_mi355x.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(moe_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def so():
+    from mlxlr8_amd._lib import LIB_PATH
+    if not LIB_PATH.exists():
+        pytest.fail("libmoe_mi355x.so is not built: run python -m mlxlr8_amd.build")
+    return ctypes.CDLL(str(LIB_PATH))
+
+
+def test_every_declared_symbol_is_exported(so):
+    names = _declared()
+    assert len(names) >= 10
+    for name in names:
+        assert hasattr(so, name), name
+
+
+def test_python_binding_covers_header():
+    from mlxlr8_amd._lib import exported_symbols
+    assert set(_declared()) <= set(exported_symbols())
+
+
+def test_version_and_workspace(so):
+    so.moe_version.restype = ctypes.c_char_p
+    assert b"gfx950" in so.moe_version()
+    so.moe_workspace_bytes.restype = ctypes.c_size_t
+    assert so.moe_workspace_bytes(6144, 2048) > 32 * 1024 * 1024
+
+
+def test_argument_errors_without_device():
+    from mlxlr8_amd._lib import lib
+    L = lib()
+    assert L.moe_route_f32(None, None, 1, None, None, None) == -1
+    assert b"null" in L.moe_last_error()
+    assert L.moe_trellis_decode_f16(ctypes.c_void_p(16), 128 * 128 // 2, 3, 128, 128, 1, 0, ctypes.c_void_p(16), None) == -1
+    assert b"K4" in L.moe_last_error()
+    assert L.moe_trellis_decode_f16(ctypes.c_void_p(16), 5, 4, 128, 128, 1, 0, ctypes.c_void_p(16), None) == -1
+    assert b"byte count" in L.moe_last_error()
+
+
+def test_host_validation_messages():
+    import torch
+    from mlxlr8_amd.trellis import _check_format
+    with pytest.raises(ValueError, match="byte count"):
+        _check_format(torch.zeros(5, dtype=torch.uint8), 4, 128, 128, 1)
+    with pytest.raises(ValueError, match="multiples of 128"):
+        _check_format(torch.zeros(64, dtype=torch.uint8), 4, 100, 128, 1)
+    with pytest.raises(ValueError, match="width"):
+        _check_format(torch.zeros(64, dtype=torch.uint8), 5, 128, 128, 1)
+    assert _check_format(torch.zeros(3 * 128 * 128 // 2, dtype=torch.uint8), 4, 128, 128, 1) == 3
+
+
+def test_product_never_imports_oracle():
+    for path in (ROOT / "mlxlr8_amd").rglob("*.py"):
+        text = path.read_text()
+        assert "import oracle" not in text and "from oracle" not in text, path

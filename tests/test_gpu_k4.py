@@ -1,0 +1,220 @@
+"""K4 trellis path on the MI355X: bit-exact codebook/decode/routing and layer parity with the oracle."""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import refmath
+from conftest import bf16_bits, bits_to_f32, f16_bits, rel_l2
+from test_oracle_router import _expected, router_case
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def test_codebook_table_bit_exact(cuda, orc):
+    import mlxlr8_amd
+    from mlxlr8_amd._lib import check, lib, ptr, stream
+    say("case: codebook table")
+    t = torch.empty(65536, dtype=torch.uint8, device=cuda)
+    check(lib().moe_codebook_e4m3(ptr(t), stream(cuda)))
+    torch.cuda.synchronize()
+    got = refmath.fp8_e4m3_decode(t.cpu().numpy())
+    want = orc.codebook().astype(np.float64)
+    np.testing.assert_array_equal(got, want)
+    assert mlxlr8_amd.lib() is not None
+
+
+@pytest.mark.parametrize("side", [1, 2])
+def test_decode_inner_bit_exact_small(cuda, orc, side):
+    from mlxlr8_amd.trellis import decode_inner
+    say(f"case: decode small side={side}")
+    rng = np.random.default_rng(11 + side)
+    nibs = [rng.integers(0, 16, (16, 24, 256), dtype=np.uint32) for _ in range(2)]
+    host = np.concatenate([refmath.build_trellis_matrix(n, side) for n in nibs])
+    packed = torch.from_numpy(host).to(cuda)
+    for e in range(2):
+        got = decode_inner(packed, 4, 256, 384, side, e).cpu().numpy().astype(np.float32)
+        np.testing.assert_array_equal(got, refmath.expected_inner(nibs[e]))
+
+
+@pytest.mark.parametrize("side,in_f,out_f", [(1, 6144, 2048), (2, 2048, 6144)])
+def test_decode_inner_bit_exact_glm_shapes(cuda, orc, side, in_f, out_f):
+    from mlxlr8_amd.trellis import decode_inner
+    say(f"case: decode glm side={side}")
+    g = torch.Generator(device=cuda)
+    g.manual_seed(5 + side)
+    packed = torch.randint(0, 256, (3 * in_f * out_f // 2,), generator=g, device=cuda, dtype=torch.uint8)
+    host = packed.cpu().numpy()
+    for e in (0, 2):
+        got = decode_inner(packed, 4, in_f, out_f, side, e).cpu().numpy().astype(np.float32)
+        np.testing.assert_array_equal(got, orc.decode(host, 4, in_f, out_f, side, e))
+
+
+@pytest.mark.parametrize("rows", [1, 2, 4, 8, 33])
+@pytest.mark.parametrize("case", ["random", "bias", "ties", "saturated", "zero"])
+def test_route_bit_exact(cuda, orc, rows, case):
+    from mlxlr8_amd.fast_router import route
+    say(f"case: route rows={rows} {case}")
+    host, bias = router_case(case, rows)
+    ids, scores = route(torch.from_numpy(host).to(cuda), torch.from_numpy(bias).to(cuda))
+    ids, scores = ids.cpu().numpy().astype(np.int64), scores.cpu().numpy()
+    oids, oscores = orc.route(host, bias)
+    np.testing.assert_array_equal(ids, oids.astype(np.int64))
+    np.testing.assert_allclose(scores, oscores, rtol=1e-6, atol=1e-7)
+    chosen, weights = _expected(host, bias)
+    np.testing.assert_array_equal(ids[:, :8], chosen)
+
+
+@pytest.mark.parametrize("rows", [1, 8, 512])
+def test_router_logits(cuda, orc, rows):
+    from mlxlr8_amd.fast_router import router_logits
+    say(f"case: router logits rows={rows}")
+    g = torch.Generator(device=cuda)
+    g.manual_seed(rows)
+    x = torch.randn((rows, 6144), generator=g, device=cuda).to(torch.bfloat16)
+    w = torch.randn((256, 6144), generator=g, device=cuda) * 0.02
+    got = router_logits(x, w).cpu().numpy()
+    want = orc.router_logits(bf16_bits(x), w.cpu().numpy())
+    assert np.abs(got - want).max() <= 2e-5 * np.abs(want).max()
+
+
+def _small_layer(cuda, seed, h=256, m=128, E=4):
+    from mlxlr8_amd import synth
+    layer = synth.k4_layer(cuda, seed, hidden=h, intermediate=m, experts=E)
+    host = {p: t.cpu().numpy() for p, t in layer["packed"].items()}
+    sc = {p: (f16_bits(a), f16_bits(b)) for p, (a, b) in layer["scales"].items()}
+    return layer, host, sc
+
+
+@pytest.mark.parametrize("side", [1, 2])
+@pytest.mark.parametrize("per_slot", [False, True])
+def test_expert_linear_small(cuda, orc, side, per_slot):
+    from mlxlr8_amd.trellis import expert_linear
+    say(f"case: expert_linear side={side} per_slot={per_slot}")
+    layer, host, sc = _small_layer(cuda, 31)
+    proj = "down" if side == 2 else "gate"
+    in_f, out_f = (128, 256) if side == 2 else (256, 128)
+    ids = torch.tensor([[2, 0], [1, 2], [3, 3]], dtype=torch.int32, device=cuda)
+    g = torch.Generator(device=cuda)
+    g.manual_seed(3)
+    shape = (3, 2, in_f) if per_slot else (3, in_f)
+    x = torch.randn(shape, generator=g, device=cuda).to(torch.bfloat16)
+    ins, outs = layer["scales"][proj]
+    y = expert_linear(x, ids, layer["packed"][proj], ins, outs, 4, in_f, out_f, side)
+    assert y.shape == (3, 2, out_f) and y.dtype == torch.bfloat16
+    xf = bits_to_f32(bf16_bits(x)).reshape(-1, in_f)
+    if not per_slot:
+        xf = np.repeat(xf, 2, axis=0)
+    want = orc.k4_linear(xf, ids.cpu().numpy().ravel(), host[proj], in_f, out_f, side, sc[proj][0], sc[proj][1])
+    got = bits_to_f32(bf16_bits(y)).reshape(-1, out_f)
+    assert rel_l2(got, want) < 4e-3  # bf16 output rounding only
+    np.testing.assert_allclose(got, want, rtol=2 ** -7, atol=1e-6)
+
+
+@pytest.mark.parametrize("rows", [1, 3, 8])
+def test_mlp_values_small(cuda, orc, rows):
+    from mlxlr8_amd.fast_decode import fast_expert_mlp
+    say(f"case: mlp small rows={rows}")
+    layer, host, sc = _small_layer(cuda, 181, E=5)
+    rng = np.random.default_rng(rows)
+    ids = torch.from_numpy(rng.integers(0, 5, (rows, 9)).astype(np.int32)).to(cuda)
+    x = torch.from_numpy(rng.normal(size=(rows, 256)).astype(np.float32)).to(cuda).to(torch.bfloat16)
+    values = fast_expert_mlp(x, ids, layer["packed"], layer["scales"], 4, 256, 128)
+    res = np.zeros((rows, 256), np.uint16)
+    _, want = orc.k4_moe(bf16_bits(x), ids.cpu().numpy(), np.zeros((rows, 8), np.float32), res, 256, 128,
+                         host["gate"], host["up"], host["down"],
+                         sc["gate"][0], sc["gate"][1], sc["up"][0], sc["up"][1], sc["down"][0], sc["down"][1],
+                         want_values=True)
+    got = bits_to_f32(bf16_bits(values))
+    err = rel_l2(got, bits_to_f32(want))
+    say(f"  rel_l2={err:.3e}")
+    assert err <= 1e-3
+
+
+@pytest.fixture(scope="module")
+def glm_layer(cuda):
+    from mlxlr8_amd import synth
+    say("building GLM-shaped K4 layer (257 experts)")
+    layer = synth.k4_layer(cuda, 1234)
+    w, bias = synth.router(cuda, 1234)
+    host = {p: t.cpu().numpy() for p, t in layer["packed"].items()}
+    sc = {p: (f16_bits(a), f16_bits(b)) for p, (a, b) in layer["scales"].items()}
+    from mlxlr8_amd.experts import ExpertLayer
+    experts = ExpertLayer(layer["packed"], layer["scales"], 6144, 2048)
+    return experts, layer, host, sc, w, bias
+
+
+def _check_decode_block(orc, glm_layer, rows, correlated, seed):
+    from mlxlr8_amd import synth
+    experts, layer, host, sc, w, bias = glm_layer
+    x, residual = synth.activations(w.device, seed, rows, correlated=correlated)
+    out, ids, scores = experts.decode_block_routes(x, residual, w, bias)
+    torch.cuda.synchronize()
+    ids = ids.cpu().numpy().astype(np.uint32)
+    logits = orc.router_logits(bf16_bits(x), w.cpu().numpy())
+    oids, oscores = orc.route(logits, bias.cpu().numpy())
+    mism = (ids != oids).any(axis=1)
+    if mism.any():
+        # only a near tie of corrected scores may flip (logits differ by fp32 summation order)
+        sig = 1 / (1 + np.exp(-logits.astype(np.float64)))
+        choice = sig + bias.cpu().numpy()
+        for r in np.where(mism)[0]:
+            srt = np.sort(choice[r])[::-1]
+            assert srt[7] - srt[8] < 1e-5, f"row {r}: routing differs without a near tie"
+    np.testing.assert_allclose(scores.cpu().numpy()[~mism], oscores[~mism], rtol=2e-6, atol=1e-7)
+    want = orc.k4_moe(bf16_bits(x), ids, scores.cpu().numpy(), bf16_bits(residual), 6144, 2048,
+                      host["gate"], host["up"], host["down"],
+                      sc["gate"][0], sc["gate"][1], sc["up"][0], sc["up"][1], sc["down"][0], sc["down"][1])
+    got = bits_to_f32(bf16_bits(out))
+    wantf = bits_to_f32(want)
+    err = rel_l2(got, wantf)
+    # the layer adds a N(0,1) residual; also check the MoE contribution alone
+    res = bits_to_f32(bf16_bits(residual))
+    err_moe = rel_l2(got - res, wantf - res)
+    say(f"  rows={rows} unique={len(np.unique(ids))} rel_l2={err:.3e} moe-part rel_l2={err_moe:.3e}")
+    assert err <= 1e-3
+    assert err_moe <= 1e-2
+    return out
+
+
+def test_moe_decode_block_config0(cuda, orc, glm_layer):
+    say("case: GLM decode block rows=1")
+    out = _check_decode_block(orc, glm_layer, 1, False, 7)
+    # deterministic: a second call reproduces every bit
+    experts, layer, host, sc, w, bias = glm_layer
+    from mlxlr8_amd import synth
+    x, residual = synth.activations(w.device, 7, 1)
+    out2 = experts.decode_block(x, residual, w, bias)
+    assert torch.equal(out.view(torch.int16), out2.view(torch.int16))
+
+
+def test_moe_decode_block_verify_batch(cuda, orc, glm_layer):
+    say("case: GLM decode block rows=8 correlated")
+    _check_decode_block(orc, glm_layer, 8, True, 21)
+
+
+def test_mlp_values_glm(cuda, orc, glm_layer):
+    from mlxlr8_amd.fast_decode import fast_expert_mlp
+    say("case: GLM values rows=2")
+    experts, layer, host, sc, w, bias = glm_layer
+    ids = torch.tensor([[5, 17, 256, 40, 5, 99, 1, 2, 3], [17, 0, 256, 250, 7, 8, 9, 10, 11]],
+                       dtype=torch.int32, device=cuda)
+    g = torch.Generator(device=cuda)
+    g.manual_seed(9)
+    x = torch.randn((2, 6144), generator=g, device=cuda).to(torch.bfloat16)
+    values = experts(x, ids)
+    res = np.zeros((2, 6144), np.uint16)
+    _, want = orc.k4_moe(bf16_bits(x), ids.cpu().numpy(), np.zeros((2, 8), np.float32), res, 6144, 2048,
+                         host["gate"], host["up"], host["down"],
+                         sc["gate"][0], sc["gate"][1], sc["up"][0], sc["up"][1], sc["down"][0], sc["down"][1],
+                         want_values=True)
+    err = rel_l2(bits_to_f32(bf16_bits(values)), bits_to_f32(want))
+    say(f"  rel_l2={err:.3e}")
+    assert err <= 1e-3
+    assert values.shape == (2, 9, 6144)
