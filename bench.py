@@ -45,6 +45,8 @@ def parse():
     p.add_argument("--seed", type=int, default=2026)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--calibrate-copy", action="store_true",
+                   help="also run a plain 1 GiB device copy (reference point for rocprofv3 FETCH/WRITE_SIZE)")
     return p.parse_args()
 
 
@@ -131,14 +133,16 @@ def main():
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(n)]
     L = lib()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # torch creates an event's HIP handle on its first record(): record each once first
+    for row in evs:
+        for e in row:
+            e.record()
+    handles = [(ctypes.c_void_p * 4)(*[ctypes.c_void_p(e.cuda_event) for e in row]) for row in evs]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     start.record()
     for i in range(n):
-        handles = (ctypes.c_void_p * 4)(*[ctypes.c_void_p(e.cuda_event) for e in evs[i]])
-        for e in evs[i]:
-            e.record()  # materialise the event object on the stream before arming it
-        L.moe_profile_events(handles, 4)
+        L.moe_profile_events(handles[i], 4)
         step(args.warmup + i)
     end.record()
     torch.cuda.synchronize()
@@ -183,6 +187,13 @@ def main():
                      "algorithmic_bytes": BYTES_GATEUP},
         "wall_s": round(wall, 3),
     }
+    if args.calibrate_copy:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        result["calibration_copy_bytes"] = 1 << 30
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(raw[0], w, bias, xs, rs, args.cpu_seconds)
     print(json.dumps(result), flush=True)

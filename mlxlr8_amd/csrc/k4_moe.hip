@@ -88,6 +88,15 @@ __global__ void trellis_decode_kernel(const uint32_t* __restrict__ packed, int i
 enum InMode { IN_PREP = 0, IN_DIRECT = 1 };
 enum FinMode { FIN_GATE = 0, FIN_VALUES = 1, FIN_COMBINE = 2 };
 
+// Decode mix (codeword pairs per word decoded arithmetically; the rest use the LDS table) and
+// the depth of the per-wave chunk prefetch ring, chosen by measurement on MI355X.
+#ifndef MOE_K4_ALU_PAIRS
+#define MOE_K4_ALU_PAIRS 1
+#endif
+#ifndef MOE_K4_PREFETCH
+#define MOE_K4_PREFETCH 3
+#endif
+
 constexpr int kWaves = 16;            // waves per block (one block per CU)
 constexpr int kThreads = kWaves * 64;
 constexpr int kMaxBlocks = 256;
@@ -193,24 +202,10 @@ __device__ __forceinline__ void sum_partials(const float* __restrict__ partial, 
 // Partial column order inside a 128-column block: lane L owns 16*(L/8)+L%8 (acc0) and +8 (acc1).
 __device__ __forceinline__ int col_acc0(int lane) { return 16 * (lane >> 3) + (lane & 7); }
 
-template <int NT>
-__device__ __forceinline__ void fma_word(const float f[8], const float* x, int i, float (&acc)[2]) {
-  // word i of the lane covers rows 2i, 2i+1, 2i+8, 2i+9
-  const int r0 = 2 * i;
-  acc[0] = fmaf(x[r0], f[0], acc[0]);
-  acc[0] = fmaf(x[r0 + 1], f[1], acc[0]);
-  acc[0] = fmaf(x[r0 + 8], f[2], acc[0]);
-  acc[0] = fmaf(x[r0 + 9], f[3], acc[0]);
-  acc[1] = fmaf(x[r0], f[4], acc[1]);
-  acc[1] = fmaf(x[r0 + 1], f[5], acc[1]);
-  acc[1] = fmaf(x[r0 + 8], f[6], acc[1]);
-  acc[1] = fmaf(x[r0 + 9], f[7], acc[1]);
-}
-
-template <int IM, int FM, int NT, int ALU>
+template <int IM, int FM, int NT, int ALU, int PF>
 __global__ __launch_bounds__(kThreads) void k4_gemv_kernel(GemvArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t tab[65536];
-  __shared__ __attribute__((aligned(16))) float xs[IM == IN_PREP ? kWaves * NT * 128 : 4];
+  __shared__ __attribute__((aligned(16))) float xs[kWaves * NT * 128];
 
   load_codebook_lds(tab);
   __syncthreads();
@@ -226,7 +221,7 @@ __global__ __launch_bounds__(kThreads) void k4_gemv_kernel(GemvArgs a) {
   const int wave = blockIdx.x * kWaves + wave_id_in_block();
   const int lane = lane_id();
   const int64_t c_begin = range_start(n, wave, nw), c_end = range_start(n, wave + 1, nw);
-  float* xw = xs + (IM == IN_PREP ? wave_id_in_block() * NT * 128 : 0);
+  float* xw = xs + wave_id_in_block() * NT * 128;
   const int src_lane = (lane & 7) == 0 ? lane + 7 : lane - 1;
 
   int visit = 0;
@@ -245,16 +240,14 @@ __global__ __launch_bounds__(kThreads) void k4_gemv_kernel(GemvArgs a) {
 #pragma unroll
     for (int t = 0; t < NT; t++) { acc[t][0] = 0.0f; acc[t][1] = 0.0f; }
 
-    // software pipeline: one chunk in flight ahead of the one being decoded
-    u32x4 next = *reinterpret_cast<const u32x4*>(base + chunk_offset(a.side, e, ob, tk0, it, obs) + lane * 16);
-    for (int tk = tk0; tk < tk1; tk++) {
-      const u32x4 v = next;
-      if (tk + 1 < tk1)
-        next = *reinterpret_cast<const u32x4*>(base + chunk_offset(a.side, e, ob, tk + 1, it, obs) + lane * 16);
-
-      if (IM == IN_PREP && (tk == tk0 || (tk & 7) == 0)) {
-        // xh for the 128-row block of tk, all rows of this unit: H128(x * in_scale[e])
-        const int blk = tk >> 3;
+    auto chunk_ptr = [&](int tk) {
+      return reinterpret_cast<const u32x4*>(base + chunk_offset(a.side, e, ob, tk, it, obs) + lane * 16);
+    };
+    // Stage x for the 128-row block holding tk in this wave's LDS slice: PREP computes
+    // H128(x * in_scale[e]) from bf16 rows; DIRECT copies already-transformed fp32 rows.
+    auto stage_block = [&](int tk) {
+      const int blk = tk >> 3;
+      if (IM == IN_PREP) {
         const uint16_t* __restrict__ sc = a.in_scale[proj] + (int64_t)e * a.in_f + blk * 128 + 2 * lane;
         const float s0 = f16_to_f32(sc[0]), s1 = f16_to_f32(sc[1]);
 #pragma unroll
@@ -267,37 +260,61 @@ __global__ __launch_bounds__(kThreads) void k4_gemv_kernel(GemvArgs a) {
             *reinterpret_cast<f32x2*>(xw + t * 128 + 2 * lane) = f32x2{v0, v1};
           }
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      } else {
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+          if (t < ntok) {
+            const int slot = P->slot[u][t];
+            *reinterpret_cast<f32x2*>(xw + t * 128 + 2 * lane) =
+                *reinterpret_cast<const f32x2*>(a.x_f32 + (int64_t)slot * a.in_f + blk * 128 + 2 * lane);
+          }
+        }
       }
-
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+    auto process = [&](const u32x4 v, int tk) {
+      if (tk == tk0 || (tk & 7) == 0) stage_block(tk);
       const uint32_t prior0 = (uint32_t)__shfl((int)v.w, src_lane, 64);
       const uint32_t W[4] = {v.x, v.y, v.z, v.w};
       const uint32_t Pw[4] = {prior0, v.x, v.y, v.z};
-      float f[4][8];
+      const float* xrow = xw + (tk & 7) * 16;
 #pragma unroll
-      for (int i = 0; i < 4; i++) decode_word<ALU>(W[i], Pw[i], tab, f[i]);
-
+      for (int i = 0; i < 4; i++) {
+        // word i covers rows 2i, 2i+1 (slots 0,1 / 4,5) and 2i+8, 2i+9 (slots 2,3 / 6,7)
+        float f[8];
+        decode_word<ALU>(W[i], Pw[i], tab, f);
 #pragma unroll
-      for (int t = 0; t < NT; t++) {
-        if (t < ntok) {
-          float x[16];
-          if (IM == IN_PREP) {
-            const f32x4* xp = reinterpret_cast<const f32x4*>(xw + t * 128 + (tk & 7) * 16);
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-              const f32x4 xv = xp[q];
-              x[4 * q] = xv.x; x[4 * q + 1] = xv.y; x[4 * q + 2] = xv.z; x[4 * q + 3] = xv.w;
-            }
-          } else {
-            const int slot = P->slot[u][t];
-            const float* __restrict__ xp = a.x_f32 + (int64_t)slot * a.in_f + tk * 16;
-#pragma unroll
-            for (int q = 0; q < 16; q++) x[q] = xp[q];
+        for (int t = 0; t < NT; t++) {
+          if (t < ntok) {
+            const f32x2 xa = *reinterpret_cast<const f32x2*>(xrow + t * 128 + 2 * i);
+            const f32x2 xb = *reinterpret_cast<const f32x2*>(xrow + t * 128 + 2 * i + 8);
+            acc[t][0] = fmaf(xa.x, f[0], acc[t][0]);
+            acc[t][0] = fmaf(xa.y, f[1], acc[t][0]);
+            acc[t][0] = fmaf(xb.x, f[2], acc[t][0]);
+            acc[t][0] = fmaf(xb.y, f[3], acc[t][0]);
+            acc[t][1] = fmaf(xa.x, f[4], acc[t][1]);
+            acc[t][1] = fmaf(xa.y, f[5], acc[t][1]);
+            acc[t][1] = fmaf(xb.x, f[6], acc[t][1]);
+            acc[t][1] = fmaf(xb.y, f[7], acc[t][1]);
           }
+        }
+      }
+    };
+
+    // software pipeline: a ring of PF chunk loads in flight ahead of the one being decoded
+    u32x4 ring[PF];
 #pragma unroll
-          for (int i = 0; i < 4; i++) fma_word<NT>(f[i], x, i, acc[t]);
+    for (int d = 0; d < PF; d++)
+      if (tk0 + d < tk1) ring[d] = *chunk_ptr(tk0 + d);
+    for (int tk = tk0; tk < tk1; tk += PF) {
+#pragma unroll
+      for (int d = 0; d < PF; d++) {
+        if (tk + d < tk1) {
+          const u32x4 v = ring[d];
+          if (tk + d + PF < tk1) ring[d] = *chunk_ptr(tk + d + PF);
+          process(v, tk + d);
         }
       }
     }
@@ -511,9 +528,9 @@ int launch_gemv(const GemvArgs& a, int max_ntok, int max_units, hipStream_t stre
   if (blocks < need) blocks = need;
   const dim3 grid(blocks), block(kThreads);
   if (max_ntok <= 1)
-    hipLaunchKernelGGL((k4_gemv_kernel<IM, FM, 1, 1>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((k4_gemv_kernel<IM, FM, 1, MOE_K4_ALU_PAIRS, MOE_K4_PREFETCH>), grid, block, 0, stream, a);
   else
-    hipLaunchKernelGGL((k4_gemv_kernel<IM, FM, kMaxRows, 1>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((k4_gemv_kernel<IM, FM, kMaxRows, MOE_K4_ALU_PAIRS, MOE_K4_PREFETCH>), grid, block, 0, stream, a);
   MOE_HIP(hipGetLastError());
   return MOE_OK;
 }

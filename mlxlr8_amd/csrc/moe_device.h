@@ -126,6 +126,23 @@ __device__ __forceinline__ float swiglu_bf16(float gate, float up) {
   return round_bf16(round_bf16(g * sig) * u);
 }
 
+// ---------------------------------------------------------------- wave reductions (DPP)
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xF,
+                                                                false));
+}
+// Sum over the 64 lanes; the total is valid in lane 63.
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp_f32<0xB1>(v);        // quad_perm [1,0,3,2]
+  v += dpp_f32<0x4E>(v);        // quad_perm [2,3,0,1]
+  v += dpp_f32<0x124>(v);       // row_ror:4
+  v += dpp_f32<0x128>(v);       // row_ror:8  -> every lane holds its row (16 lanes) sum
+  v += dpp_f32<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
+  v += dpp_f32<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
+  return v;
+}
+
 // ---------------------------------------------------------------- small wave helpers
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 __device__ __forceinline__ int wave_id_in_block() { return threadIdx.x >> 6; }
