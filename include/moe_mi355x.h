@@ -111,6 +111,32 @@ int moe_k4_moe_decode(const uint16_t* x, const uint16_t* residual, int rows, con
                       const uint16_t* out_down, int hidden, int intermediate, uint16_t* out, uint32_t* indices,
                       float* scores, void* workspace, size_t workspace_bytes, moe_stream_t stream);
 
+/* ---------------------------------------------------------------- joined MXFP4 */
+
+/* Resident joined-MXFP4 experts: gate_up codes [E, 2m, h/2] (e2m1, low nibble = even k) with e8m0
+ * scales [E, 2m, h/32]; down codes [E, h, m/2] + scales [E, h, m/32]; unit [h] fp16 (+-1);
+ * out_gate/out_up/in_down [E, m], out_down [E, h] fp16.  This build: h = 6144, m = 2048.
+ * values [rows*slots, h] bf16 (slots <= 9, rows*slots <= 72).
+ * Replaces: exlr8/joined_mxfp4.py:143-147 JoinedMXFP4.slots (_inner, exlr8/joined_mxfp4.py:90-134). */
+int moe_mxfp4_mlp(const uint16_t* x, const uint32_t* ids, int rows, int slots, const uint8_t* gate_up_codes,
+                  const uint8_t* gate_up_scales, const uint8_t* down_codes, const uint8_t* down_scales,
+                  int64_t experts, const uint16_t* unit, const uint16_t* out_gate, const uint16_t* out_up,
+                  const uint16_t* in_down, const uint16_t* out_down, int hidden, int intermediate, uint16_t* values,
+                  void* workspace, size_t workspace_bytes, moe_stream_t stream);
+
+/* Joined-MXFP4 MLP plus the weighted combine with the shared expert and residual (rows <= 8).
+ * Replaces: exlr8/joined_mxfp4.py:148-163 JoinedMXFP4.finish (exlr8/metal/joined_finish_sorted.metal,
+ *           exlr8/metal/fast_decode_finish_fused.metal). */
+int moe_mxfp4_mlp_finish(const uint16_t* x, const uint32_t* ids, const float* scores, const uint16_t* residual,
+                         int rows, const uint8_t* gate_up_codes, const uint8_t* gate_up_scales,
+                         const uint8_t* down_codes, const uint8_t* down_scales, int64_t experts,
+                         const uint16_t* unit, const uint16_t* out_gate, const uint16_t* out_up,
+                         const uint16_t* in_down, const uint16_t* out_down, int hidden, int intermediate,
+                         uint16_t* out, void* workspace, size_t workspace_bytes, moe_stream_t stream);
+
+/* Workspace bytes for the two MXFP4 entry points above. */
+size_t moe_mxfp4_workspace_bytes(int hidden, int intermediate);
+
 /* ---------------------------------------------------------------- profiling */
 
 /* Arm HIP events (hipEvent_t handles, NULL entries skipped) for the next K4 layer call made by

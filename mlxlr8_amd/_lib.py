@@ -35,6 +35,11 @@ _SIGNATURES = {
                           + [_I32, _I32, _VP, _VP, _VP, _VP, _SZ, _VP]),
     "moe_workspace_bytes": (_SZ, [_I32, _I32]),
     "moe_profile_events": (_I32, [_VP, _I32]),
+    "moe_mxfp4_mlp": (_I32, [_VP, _VP, _I32, _I32, _VP, _VP, _VP, _VP, _I64] + [_VP] * 5
+                      + [_I32, _I32, _VP, _VP, _SZ, _VP]),
+    "moe_mxfp4_mlp_finish": (_I32, [_VP, _VP, _VP, _VP, _I32, _VP, _VP, _VP, _VP, _I64] + [_VP] * 5
+                             + [_I32, _I32, _VP, _VP, _SZ, _VP]),
+    "moe_mxfp4_workspace_bytes": (_SZ, [_I32, _I32]),
 }
 
 
@@ -78,12 +83,13 @@ def stream(device=None):
 _workspaces = {}
 
 
-def workspace(device, hidden, intermediate):
-    """A zero-initialised scratch buffer per (device, shape), reused across calls on one stream."""
-    key = (str(device), int(hidden), int(intermediate))
+def workspace(device, hidden, intermediate, kind="k4"):
+    """A zero-initialised scratch buffer per (device, shape, kind), reused across calls on one stream."""
+    key = (str(device), int(hidden), int(intermediate), kind)
     ws = _workspaces.get(key)
     if ws is None:
-        nbytes = lib().moe_workspace_bytes(int(hidden), int(intermediate))
+        size_fn = lib().moe_mxfp4_workspace_bytes if kind == "mxfp4" else lib().moe_workspace_bytes
+        nbytes = size_fn(int(hidden), int(intermediate))
         ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
         _workspaces[key] = ws
     return ws

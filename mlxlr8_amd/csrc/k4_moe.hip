@@ -52,11 +52,20 @@ __global__ void copy_codebook_kernel(uint8_t* dst) {
 
 // ============================================================== plan
 
-__global__ void plan_kernel(const uint32_t* __restrict__ ids, int rows, int slots, int experts, int max_users,
-                            Plan* plan) {
-  __shared__ int32_t unit_of_expert[257];
-  if (threadIdx.x != 0) return;
-  build_plan(ids, rows, slots, experts, max_users, plan, unit_of_expert);
+__global__ __launch_bounds__(128) void plan_kernel(const uint32_t* __restrict__ ids, int rows, int slots,
+                                                    int experts, int max_users, Plan* plan) {
+  __shared__ int32_t sid[kMaxUnits];
+  __shared__ int32_t open[kMaxUnits];
+  const int n = rows * slots;
+  if ((int)threadIdx.x < n) {
+    int e = (int)ids[threadIdx.x];
+    if (e < 0) e = 0;
+    if (e >= experts) e = experts - 1;
+    if (e > 256) e = 256;
+    sid[threadIdx.x] = e;
+  }
+  __syncthreads();
+  build_plan_parallel(sid, rows, slots, max_users, plan, open);
 }
 
 // ============================================================== decode-only kernel
@@ -95,6 +104,22 @@ enum FinMode { FIN_GATE = 0, FIN_VALUES = 1, FIN_COMBINE = 2 };
 #endif
 #ifndef MOE_K4_PREFETCH
 #define MOE_K4_PREFETCH 3
+#endif
+// MFMA-accumulated decode GEMV (k4_mfma_kernel) and its per-word ALU pair counts (even, odd words)
+#ifndef MOE_K4_MFMA
+#define MOE_K4_MFMA 1
+#endif
+#ifndef MOE_K4_ALU_EVEN
+#define MOE_K4_ALU_EVEN 1
+#endif
+#ifndef MOE_K4_ALU_ODD
+#define MOE_K4_ALU_ODD 2
+#endif
+#ifndef MOE_K4_MFMA_WAVES
+#define MOE_K4_MFMA_WAVES 8
+#endif
+#ifndef MOE_K4_CHAIN
+#define MOE_K4_CHAIN 0
 #endif
 
 constexpr int kWaves = 16;            // waves per block (one block per CU)
@@ -171,11 +196,13 @@ __device__ __forceinline__ int wave_of_chunk(int64_t c, int64_t n, int nw) {
 }
 
 // Sum, in wave order, the partials of segment `seg` for token position `t` at columns
-// 2*lane and 2*lane+1.  Loads are issued in batches of 8 waves so one memory round trip
-// covers a batch; empty wave ranges contribute nothing.
-__device__ __forceinline__ void sum_partials(const float* __restrict__ partial, int64_t n, int nw, int it, int seg,
+// 2*lane and 2*lane+1.  Work is partitioned in units (a chunk, or a quad of chunks); segment
+// `seg` covers units [seg*ups, (seg+1)*ups) of `n` units split over `nw` waves.  Loads are
+// issued in batches of 8 waves so one memory round trip covers a batch; empty wave ranges
+// contribute nothing.
+__device__ __forceinline__ void sum_partials(const float* __restrict__ partial, int64_t n, int nw, int ups, int seg,
                                              int t, float& v0, float& v1) {
-  const int64_t a = (int64_t)seg * it, b = a + it;
+  const int64_t a = (int64_t)seg * ups, b = a + ups;
   const int wa = wave_of_chunk(a, n, nw), wb = wave_of_chunk(b - 1, n, nw);
   const int lane = lane_id();
   v0 = 0.0f;
@@ -195,6 +222,97 @@ __device__ __forceinline__ void sum_partials(const float* __restrict__ partial, 
 #pragma unroll
     for (int j = 0; j < 8; j++) {
       if (ok[j]) { v0 += p[j].x; v1 += p[j].y; }
+    }
+  }
+}
+
+// After a wave has stored the partials of one visit (`units` work units of segment `seg`):
+// count them, and if this completes the segment reduce it and run the finish stage that the
+// segment unlocks (gate finish, per-slot values, or the column-block combine).
+template <int FM>
+__device__ __forceinline__ void complete_visit(const GemvArgs& a, const Plan* __restrict__ P, int seg, int units,
+                                               int ups, int64_t n, int nw, int nproj, int U, int u, int ob, int e,
+                                               int ntok) {
+  const int lane = lane_id();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  if (counter_add(&a.counter_seg[seg], units) + units != ups) return;
+  // this wave completed segment `seg`: reduce its partials once
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  counter_reset(&a.counter_seg[seg]);
+  const int obs = a.out_f / 128;
+  const int col = ob * 128 + 2 * lane;
+  if (FM == FIN_VALUES) {
+    for (int t = 0; t < ntok; t++) {
+      float v0, v1;
+      sum_partials(a.partial, n, nw, ups, seg, t, v0, v1);
+      hadamard128_wave(v0, v1);
+      const int64_t si = (int64_t)e * a.out_f + col;
+      const int slot = P->slot[u][t];
+      const uint32_t packed2 = (uint32_t)f32_to_bf16(v0 * f16_to_f32(a.out_scale[0][si])) |
+                               ((uint32_t)f32_to_bf16(v1 * f16_to_f32(a.out_scale[0][si + 1])) << 16);
+      *reinterpret_cast<uint32_t*>(a.values + (int64_t)slot * a.out_f + col) = packed2;
+    }
+  } else if (FM == FIN_GATE) {
+    for (int t = 0; t < ntok; t++) {
+      float v0, v1;
+      sum_partials(a.partial, n, nw, ups, seg, t, v0, v1);
+      store_coherent2(a.segbuf + ((int64_t)seg * kMaxRows + t) * 128 + 2 * lane, v0, v1);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    const int grp = u * obs + ob;
+    if (counter_add(&a.counter_grp[grp], 1) + 1 != nproj) return;
+    // gate and up of this column block are both reduced: gate finish
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    counter_reset(&a.counter_grp[grp]);
+    for (int t = 0; t < ntok; t++) {
+      const f32x2 g = load_coherent2(a.segbuf + ((int64_t)(grp * 2 + 0) * kMaxRows + t) * 128 + 2 * lane);
+      const f32x2 uu = load_coherent2(a.segbuf + ((int64_t)(grp * 2 + 1) * kMaxRows + t) * 128 + 2 * lane);
+      float g0 = g.x, g1 = g.y, u0 = uu.x, u1 = uu.y;
+      hadamard128_wave(g0, g1);
+      hadamard128_wave(u0, u1);
+      const int64_t si = (int64_t)e * a.out_f + col;
+      float h0 = swiglu_bf16(g0 * f16_to_f32(a.out_scale[0][si]), u0 * f16_to_f32(a.out_scale[1][si]));
+      float h1 = swiglu_bf16(g1 * f16_to_f32(a.out_scale[0][si + 1]), u1 * f16_to_f32(a.out_scale[1][si + 1]));
+      h0 *= f16_to_f32(a.in_down[si]);
+      h1 *= f16_to_f32(a.in_down[si + 1]);
+      hadamard128_wave(h0, h1);
+      const int slot = P->slot[u][t];
+      *reinterpret_cast<f32x2*>(a.down_xh + (int64_t)slot * a.out_f + col) = f32x2{h0, h1};
+    }
+  } else {
+    // per-slot expert output of this column block: T(H128(inner) * out_scale)
+    for (int t = 0; t < ntok; t++) {
+      float v0, v1;
+      sum_partials(a.partial, n, nw, ups, seg, t, v0, v1);
+      hadamard128_wave(v0, v1);
+      const int64_t si = (int64_t)e * a.out_f + col;
+      const int slot = P->slot[u][t];
+      store_coherent2(a.yslot + (int64_t)slot * a.out_f + col, round_bf16(v0 * f16_to_f32(a.out_scale[0][si])),
+                      round_bf16(v1 * f16_to_f32(a.out_scale[0][si + 1])));
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    if (counter_add(&a.counter_grp[ob], 1) + 1 != U) return;
+    // every unit of this column block is done: weighted routed sum, shared, residual
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    counter_reset(&a.counter_grp[ob]);
+    for (int r = 0; r < P->rows; r++) {
+      f32x2 y[kSlots];
+#pragma unroll
+      for (int j = 0; j < kSlots; j++) y[j] = load_coherent2(a.yslot + (int64_t)(r * kSlots + j) * a.out_f + col);
+      float tot0 = y[0].x * a.scores[r * 8] + 0.0f, tot1 = y[0].y * a.scores[r * 8] + 0.0f;
+#pragma unroll
+      for (int j = 1; j < 8; j++) {
+        const float sc = a.scores[r * 8 + j];
+        tot0 = (y[j].x * sc + 0.0f) + tot0;
+        tot1 = (y[j].y * sc + 0.0f) + tot1;
+      }
+      const float c0f = round_bf16(round_bf16(tot0) + y[8].x);
+      const float c1f = round_bf16(round_bf16(tot1) + y[8].y);
+      const int64_t o = (int64_t)r * a.out_f + col;
+      const uint16_t* res = a.residual + o;
+      const uint32_t packed2 = (uint32_t)f32_to_bf16(bf16_to_f32(res[0]) + c0f) |
+                               ((uint32_t)f32_to_bf16(bf16_to_f32(res[1]) + c1f) << 16);
+      *reinterpret_cast<uint32_t*>(a.out + o) = packed2;
     }
   }
 }
@@ -329,91 +447,273 @@ __global__ __launch_bounds__(kThreads) void k4_gemv_kernel(GemvArgs a) {
         store_coherent(pw + t * 128 + c0 + 8, acc[t][1]);
       }
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    const int nch = tk1 - tk0;
-    if (counter_add(&a.counter_seg[seg], nch) + nch == it) {
-      // this wave completed segment `seg`: reduce its partials once
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-      counter_reset(&a.counter_seg[seg]);
-      const int col = ob * 128 + 2 * lane;
-      if (FM == FIN_VALUES) {
-        for (int t = 0; t < ntok; t++) {
-          float v0, v1;
-          sum_partials(a.partial, n, nw, it, seg, t, v0, v1);
-          hadamard128_wave(v0, v1);
-          const int64_t si = (int64_t)e * a.out_f + col;
-          const int slot = P->slot[u][t];
-          const uint32_t packed2 = (uint32_t)f32_to_bf16(v0 * f16_to_f32(a.out_scale[0][si])) |
-                                   ((uint32_t)f32_to_bf16(v1 * f16_to_f32(a.out_scale[0][si + 1])) << 16);
-          *reinterpret_cast<uint32_t*>(a.values + (int64_t)slot * a.out_f + col) = packed2;
-        }
-      } else if (FM == FIN_GATE) {
-        for (int t = 0; t < ntok; t++) {
-          float v0, v1;
-          sum_partials(a.partial, n, nw, it, seg, t, v0, v1);
-          store_coherent2(a.segbuf + ((int64_t)seg * kMaxRows + t) * 128 + 2 * lane, v0, v1);
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-        const int grp = u * obs + ob;
-        if (counter_add(&a.counter_grp[grp], 1) + 1 == nproj) {
-          // gate and up of this column block are both reduced: gate finish
-          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-          counter_reset(&a.counter_grp[grp]);
-          for (int t = 0; t < ntok; t++) {
-            const f32x2 g = load_coherent2(a.segbuf + ((int64_t)(grp * 2 + 0) * kMaxRows + t) * 128 + 2 * lane);
-            const f32x2 uu = load_coherent2(a.segbuf + ((int64_t)(grp * 2 + 1) * kMaxRows + t) * 128 + 2 * lane);
-            float g0 = g.x, g1 = g.y, u0 = uu.x, u1 = uu.y;
-            hadamard128_wave(g0, g1);
-            hadamard128_wave(u0, u1);
-            const int64_t si = (int64_t)e * a.out_f + col;
-            float h0 = swiglu_bf16(g0 * f16_to_f32(a.out_scale[0][si]), u0 * f16_to_f32(a.out_scale[1][si]));
-            float h1 = swiglu_bf16(g1 * f16_to_f32(a.out_scale[0][si + 1]), u1 * f16_to_f32(a.out_scale[1][si + 1]));
-            h0 *= f16_to_f32(a.in_down[si]);
-            h1 *= f16_to_f32(a.in_down[si + 1]);
-            hadamard128_wave(h0, h1);
-            const int slot = P->slot[u][t];
-            *reinterpret_cast<f32x2*>(a.down_xh + (int64_t)slot * a.out_f + col) = f32x2{h0, h1};
+    complete_visit<FM>(a, P, seg, tk1 - tk0, it, n, nw, nproj, U, u, ob, e, ntok);
+    c += tk1 - tk0;
+  }
+}
+
+// ============================================================== MFMA decode GEMV
+//
+// Same work split as k4_gemv_kernel, but in quads of 4 chunks and with the accumulation on the
+// matrix cores (v_mfma_f32_16x16x32_f16), so the vector ALUs only decode.
+//
+//   * Lane l = 16g + n loads, for each of 4 sets s, the 16 B piece (tile 2s + n/8, word group n%8)
+//     of chunk tk+g: 4 words = all 16 rows of output columns q = n%8 and q+8 of that tile.
+//   * A word's 8 codewords become two fp8 dwords (c0,c1,c4,c5) and (c2,c3,c6,c7) -- by LDS table
+//     lookup or arithmetic decode -- and four f16 pairs.  Two words of a piece form one B
+//     fragment (8 rows x 1 column) per output-column half h and row half rh, so a piece feeds
+//     4 MFMAs; the 4 k-groups of the MFMA are the 4 chunks of the quad.
+//   * A = x split into fp16 rows hi = f16(x) and lo = f16((x - hi) * 2^11) (x to ~22 bits), rows 2t
+//     and 2t+1 for token row t of the unit; staged once per 128-row block in the wave's LDS slice
+//     in A order.
+//   * D[2t] + 2^-11 * D[2t+1] gives token t's fp32 dot products.
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ f16x2 pair_sums(uint32_t v) {  // v = cw_lo | cw_hi << 16
+  const f16x2 ha = __builtin_bit_cast(f16x2, mcg_halves(v & 0xFFFFu));
+  const f16x2 hb = __builtin_bit_cast(f16x2, mcg_halves(v >> 16));
+  f16x2 s;
+  s.x = ha.x + ha.y;
+  s.y = hb.x + hb.y;
+  return s;
+}
+__device__ __forceinline__ uint32_t fp8_pair_into(uint32_t old, f16x2 sums, bool hi_word) {
+  const i16x2 o = __builtin_bit_cast(i16x2, old);
+  return __builtin_bit_cast(uint32_t, hi_word ? __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(o, sums, 1.0f, true)
+                                              : __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(o, sums, 1.0f, false));
+}
+__device__ __forceinline__ uint32_t lds_pair(const uint8_t* tab, uint32_t a, uint32_t b) {
+  return (uint32_t)tab[a] | ((uint32_t)tab[b] << 16);  // bytes [tab[a], 0, tab[b], 0]
+}
+
+// One word -> ea = fp8 bytes (c0, c1, c4, c5), eb = (c2, c3, c6, c7).  ALU pairs are taken in the
+// order (7,3), (6,2), (5,1), (4,0); the others are looked up.
+template <int ALU>
+__device__ __forceinline__ void decode_word_fp8(uint32_t w, uint32_t p, const uint8_t* tab, uint32_t& ea,
+                                                uint32_t& eb) {
+  const uint32_t a4 = __builtin_amdgcn_alignbit(p, w, 4);    // c6 | c2 << 16
+  const uint32_t a8 = __builtin_amdgcn_alignbit(p, w, 8);    // c5 | c1 << 16
+  const uint32_t a12 = __builtin_amdgcn_alignbit(p, w, 12);  // c4 | c0 << 16
+  // eb from pairs (7,3) = w and (6,2) = a4
+  if (ALU >= 2) {
+    uint32_t d = fp8_pair_into(0u, pair_sums(a4), false);   // [c6, c2, -, -]
+    d = fp8_pair_into(d, pair_sums(w), true);                // [c6, c2, c7, c3]
+    eb = __builtin_amdgcn_perm(d, d, 0x02000301u);           // [c2, c3, c6, c7]
+  } else if (ALU == 1) {
+    const uint32_t d = fp8_pair_into(0u, pair_sums(w), true);  // [-, -, c7, c3]
+    const uint32_t v = lds_pair(tab, a4 & 0xFFFFu, a4 >> 16);  // [c6, 0, c2, 0]
+    eb = __builtin_amdgcn_perm(d, v, 0x06000702u);             // [c2, c3, c6, c7]
+  } else {
+    const uint32_t v23 = lds_pair(tab, a4 >> 16, w >> 16);       // [c2, 0, c3, 0]
+    const uint32_t v67 = lds_pair(tab, a4 & 0xFFFFu, w & 0xFFFFu); // [c6, 0, c7, 0]
+    eb = __builtin_amdgcn_perm(v67, v23, 0x06040200u);
+  }
+  // ea from pairs (5,1) = a8 and (4,0) = a12
+  if (ALU >= 4) {
+    uint32_t d = fp8_pair_into(0u, pair_sums(a12), false);  // [c4, c0, -, -]
+    d = fp8_pair_into(d, pair_sums(a8), true);               // [c4, c0, c5, c1]
+    ea = __builtin_amdgcn_perm(d, d, 0x02000301u);           // [c0, c1, c4, c5]
+  } else if (ALU == 3) {
+    const uint32_t d = fp8_pair_into(0u, pair_sums(a8), true);    // [-, -, c5, c1]
+    const uint32_t v = lds_pair(tab, a12 & 0xFFFFu, a12 >> 16);   // [c4, 0, c0, 0]
+    ea = __builtin_amdgcn_perm(d, v, 0x06000702u);
+  } else {
+    const uint32_t v01 = lds_pair(tab, a12 >> 16, a8 >> 16);          // [c0, 0, c1, 0]
+    const uint32_t v45 = lds_pair(tab, a12 & 0xFFFFu, a8 & 0xFFFFu);  // [c4, 0, c5, 0]
+    ea = __builtin_amdgcn_perm(v45, v01, 0x06040200u);
+  }
+}
+
+__device__ __forceinline__ f16x2 fp8x2_to_f16(uint32_t e, bool hi_word) {
+  return hi_word ? __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(e, 1.0f, true)
+                 : __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(e, 1.0f, false);
+}
+__device__ __forceinline__ f16x8 frag(f16x2 a, f16x2 b, f16x2 c, f16x2 d) {
+  f16x8 r;
+  r[0] = a.x; r[1] = a.y; r[2] = b.x; r[3] = b.y; r[4] = c.x; r[5] = c.y; r[6] = d.x; r[7] = d.y;
+  return r;
+}
+
+// block element r (row within a 16-row tile) -> (row half, position inside the 8-wide k group)
+__device__ __forceinline__ int a_rh(int r) { return (r >> 2) & 1; }
+__device__ __forceinline__ int a_j(int r) { return 4 * ((r >> 1) & 1) + 2 * ((r >> 3) & 1) + (r & 1); }
+
+template <int IM, int FM, int NT, int ALU_EVEN, int ALU_ODD, int WV>
+__global__ __launch_bounds__(WV * 64) void k4_mfma_kernel(GemvArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t tab[65536];
+  // per wave: A fragments for the two quads of the current 128-row block [Qb][rh][m][g][8]
+  __shared__ __attribute__((aligned(16))) _Float16 xa[WV * 2 * 2 * (2 * NT) * 4 * 8];
+
+  load_codebook_lds(tab);
+  __syncthreads();
+
+  const Plan* __restrict__ P = a.plan;
+  const int U = P->units;
+  const int it = a.in_f / 16;
+  const int ups = it / 4;  // quads per segment
+  const int obs = a.out_f / 128;
+  const int nproj = a.nproj;
+  const int64_t nseg = (int64_t)U * obs * nproj;
+  const int64_t nq = nseg * ups;
+  const int nw = gridDim.x * WV;
+  const int wave = blockIdx.x * WV + wave_id_in_block();
+  const int lane = lane_id();
+  const int g = lane >> 4, nn = lane & 15;
+  const int64_t q_begin = range_start(nq, wave, nw), q_end = range_start(nq, wave + 1, nw);
+  _Float16* xw = xa + wave_id_in_block() * (2 * 2 * (2 * NT) * 4 * 8);
+  const int src_lane = (lane & 7) == 0 ? lane + 7 : lane - 1;
+
+  int visit = 0;
+  for (int64_t c = q_begin; c < q_end; visit++) {
+    const int seg = (int)(c / ups);
+    const int tq0 = (int)(c % ups);
+    const int tq1 = (int)min((int64_t)ups, (int64_t)tq0 + (q_end - c));
+    const int proj = seg % nproj;
+    const int ob = (seg / nproj) % obs;
+    const int u = seg / (nproj * obs);
+    const int e = P->expert[u];
+    const int ntok = P->ntok[u];
+    const uint8_t* __restrict__ base = a.packed[proj];
+
+    // MFMA chains restart from zero every MOE_K4_CHAIN quads and are folded into an fp32
+    // (round-to-nearest) VALU accumulator, bounding the accumulation error inside the matrix cores
+    f32x4 acc[4][2], tot[4][2];
+#pragma unroll
+    for (int s4 = 0; s4 < 4; s4++)
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        acc[s4][h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        tot[s4][h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+
+    auto piece_ptr = [&](int tq, int s4) {
+      const int tk = 4 * tq + g;
+      return reinterpret_cast<const u32x4*>(base + chunk_offset(a.side, e, ob, tk, it, obs) +
+                                            (2 * s4 + (nn >> 3)) * 128 + (nn & 7) * 16);
+    };
+    auto stage_block = [&](int blk) {
+      // xh of rows [128*blk, +128) for every token of the unit -> fp16 hi/lo A fragments
+      float v0[NT], v1[NT];
+      if (IM == IN_PREP) {
+        const uint16_t* __restrict__ sc = a.in_scale[proj] + (int64_t)e * a.in_f + blk * 128 + 2 * lane;
+        const float s0 = f16_to_f32(sc[0]), s1 = f16_to_f32(sc[1]);
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+          if (t < ntok) {
+            const int row = a.x_per_slot ? P->slot[u][t] : P->tok[u][t];
+            const uint16_t* __restrict__ xr = a.x_bf16 + (int64_t)row * a.in_f + blk * 128 + 2 * lane;
+            v0[t] = bf16_to_f32(xr[0]) * s0;
+            v1[t] = bf16_to_f32(xr[1]) * s1;
+            hadamard128_wave(v0[t], v1[t]);
           }
         }
       } else {
-        // per-slot expert output of this column block: T(H128(inner) * out_scale)
-        for (int t = 0; t < ntok; t++) {
-          float v0, v1;
-          sum_partials(a.partial, n, nw, it, seg, t, v0, v1);
-          hadamard128_wave(v0, v1);
-          const int64_t si = (int64_t)e * a.out_f + col;
-          const int slot = P->slot[u][t];
-          store_coherent2(a.yslot + (int64_t)slot * a.out_f + col, round_bf16(v0 * f16_to_f32(a.out_scale[0][si])),
-                          round_bf16(v1 * f16_to_f32(a.out_scale[0][si + 1])));
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-        if (counter_add(&a.counter_grp[ob], 1) + 1 == U) {
-          // every unit of this column block is done: weighted routed sum, shared, residual
-          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-          counter_reset(&a.counter_grp[ob]);
-          for (int r = 0; r < P->rows; r++) {
-            f32x2 y[kSlots];
 #pragma unroll
-            for (int j = 0; j < kSlots; j++) y[j] = load_coherent2(a.yslot + (int64_t)(r * kSlots + j) * a.out_f + col);
-            float tot0 = y[0].x * a.scores[r * 8] + 0.0f, tot1 = y[0].y * a.scores[r * 8] + 0.0f;
-#pragma unroll
-            for (int j = 1; j < 8; j++) {
-              const float sc = a.scores[r * 8 + j];
-              tot0 = (y[j].x * sc + 0.0f) + tot0;
-              tot1 = (y[j].y * sc + 0.0f) + tot1;
-            }
-            const float c0f = round_bf16(round_bf16(tot0) + y[8].x);
-            const float c1f = round_bf16(round_bf16(tot1) + y[8].y);
-            const int64_t o = (int64_t)r * a.out_f + col;
-            const uint16_t* res = a.residual + o;
-            const uint32_t packed2 = (uint32_t)f32_to_bf16(bf16_to_f32(res[0]) + c0f) |
-                                     ((uint32_t)f32_to_bf16(bf16_to_f32(res[1]) + c1f) << 16);
-            *reinterpret_cast<uint32_t*>(a.out + o) = packed2;
+        for (int t = 0; t < NT; t++) {
+          if (t < ntok) {
+            const int slot = P->slot[u][t];
+            const f32x2 xv = *reinterpret_cast<const f32x2*>(a.x_f32 + (int64_t)slot * a.in_f + blk * 128 + 2 * lane);
+            v0[t] = xv.x;
+            v1[t] = xv.y;
           }
         }
       }
+#pragma unroll
+      for (int jj = 0; jj < 2; jj++) {
+        const int el = 2 * lane + jj;  // row within the 128-row block
+        const int qb = el >> 6, gg = (el >> 4) & 3, r = el & 15;
+        const int base_off = (qb * 2 + a_rh(r)) * (2 * NT);
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+          if (t < ntok) {
+            float xv = jj ? v1[t] : v0[t];
+            // materialise x in fp32 first: otherwise the compiler may fuse the Hadamard scale into
+            // one of the two f16 conversions below and round hi differently in each of them
+            asm volatile("" : "+v"(xv));
+            const _Float16 hi = (_Float16)xv;
+            // the remainder is stored scaled by 2^11 so it stays a normal fp16 (the matrix cores
+            // flush fp16 denormals); the lo row of the product is scaled back by 2^-11 (exact)
+            const _Float16 lo = (_Float16)((xv - (float)hi) * 2048.0f);
+            xw[((base_off + 2 * t) * 4 + gg) * 8 + a_j(r)] = hi;
+            xw[((base_off + 2 * t + 1) * 4 + gg) * 8 + a_j(r)] = lo;
+          }
+        }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+
+    // each piece's register slot is refilled with the next quad's piece as soon as it is decoded
+    u32x4 cur[4];
+#pragma unroll
+    for (int s4 = 0; s4 < 4; s4++) cur[s4] = *piece_ptr(tq0, s4);
+    for (int tq = tq0; tq < tq1; tq++) {
+      if (tq == tq0 || (tq & 1) == 0) stage_block(tq >> 1);
+      f16x8 A[2];
+      const int m = nn;
+      const bool live = m < 2 * ntok;
+#pragma unroll
+      for (int rh = 0; rh < 2; rh++) {
+        A[rh] = live ? *reinterpret_cast<const f16x8*>(xw + ((((tq & 1) * 2 + rh) * (2 * NT) + m) * 4 + g) * 8)
+                     : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      }
+#pragma unroll
+      for (int s4 = 0; s4 < 4; s4++) {
+        const u32x4 v = cur[s4];
+        if (tq + 1 < tq1) cur[s4] = *piece_ptr(tq + 1, s4);
+        const uint32_t prior0 = (uint32_t)__shfl((int)v.w, src_lane, 64);
+        uint32_t ea[4], eb[4];
+        decode_word_fp8<ALU_EVEN>(v.x, prior0, tab, ea[0], eb[0]);
+        decode_word_fp8<ALU_ODD>(v.y, v.x, tab, ea[1], eb[1]);
+        decode_word_fp8<ALU_EVEN>(v.z, v.y, tab, ea[2], eb[2]);
+        decode_word_fp8<ALU_ODD>(v.w, v.z, tab, ea[3], eb[3]);
+#pragma unroll
+        for (int rh = 0; rh < 2; rh++) {
+          const int w0 = 2 * rh, w1 = 2 * rh + 1;
+          // h = 0: slots (0,1),(2,3) ; h = 1: slots (4,5),(6,7) of words w0, w1
+          const f16x8 b0 = frag(fp8x2_to_f16(ea[w0], false), fp8x2_to_f16(eb[w0], false),
+                                fp8x2_to_f16(ea[w1], false), fp8x2_to_f16(eb[w1], false));
+          const f16x8 b1 = frag(fp8x2_to_f16(ea[w0], true), fp8x2_to_f16(eb[w0], true),
+                                fp8x2_to_f16(ea[w1], true), fp8x2_to_f16(eb[w1], true));
+          acc[s4][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[rh], b0, acc[s4][0], 0, 0, 0);
+          acc[s4][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[rh], b1, acc[s4][1], 0, 0, 0);
+        }
+      }
+      if (MOE_K4_CHAIN > 0 && ((tq - tq0 + 1) % (MOE_K4_CHAIN > 0 ? MOE_K4_CHAIN : 1) == 0 || tq + 1 == tq1)) {
+#pragma unroll
+        for (int s4 = 0; s4 < 4; s4++)
+#pragma unroll
+          for (int h = 0; h < 2; h++) {
+            tot[s4][h] += acc[s4][h];
+            acc[s4][h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+          }
+      }
     }
-    c += tk1 - tk0;
+    if (MOE_K4_CHAIN == 0) {
+#pragma unroll
+      for (int s4 = 0; s4 < 4; s4++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) tot[s4][h] = acc[s4][h];
+    }
+
+    // partials of this visit: token t = D rows 2t + 2t+1, held by lanes 16*(t/2) + n, regs 2(t%2), +1
+    float* pw = a.partial + ((int64_t)wave * 2 + visit) * kPartialStride;
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      if (t < ntok && g == (t >> 1)) {
+        const int r0 = 2 * (t & 1);
+#pragma unroll
+        for (int s4 = 0; s4 < 4; s4++)
+#pragma unroll
+          for (int h = 0; h < 2; h++) {
+            const int col = 16 * (2 * s4 + (nn >> 3)) + (nn & 7) + 8 * h;
+            store_coherent(pw + t * 128 + col, fmaf(tot[s4][h][r0 + 1], 1.0f / 2048.0f, tot[s4][h][r0]));
+          }
+      }
+    }
+    complete_visit<FM>(a, P, seg, tq1 - tq0, ups, nq, nw, nproj, U, u, ob, e, ntok);
+    c += tq1 - tq0;
   }
 }
 
@@ -527,10 +827,29 @@ int launch_gemv(const GemvArgs& a, int max_ntok, int max_units, hipStream_t stre
   const int need = (int)((nseg_max + kWaves - 1) / kWaves);
   if (blocks < need) blocks = need;
   const dim3 grid(blocks), block(kThreads);
+#if MOE_K4_MFMA
+  {
+    constexpr int WV = MOE_K4_MFMA_WAVES;
+    int mblocks = grid_blocks();
+    const int mneed = (int)((nseg_max + WV - 1) / WV);
+    if (mblocks < mneed) mblocks = mneed;
+    if (mblocks * WV > kMaxWaves)
+      return fail(MOE_ENOTSUP, "too many waves for the partial buffer (%d)", mblocks * WV);
+    if (max_ntok <= 1)
+      hipLaunchKernelGGL((k4_mfma_kernel<IM, FM, 1, MOE_K4_ALU_EVEN, MOE_K4_ALU_ODD, WV>), dim3(mblocks), dim3(WV * 64),
+                         0, stream, a);
+    else
+      hipLaunchKernelGGL((k4_mfma_kernel<IM, FM, kMaxRows, MOE_K4_ALU_EVEN, MOE_K4_ALU_ODD, WV>), dim3(mblocks),
+                         dim3(WV * 64), 0, stream, a);
+  }
+  (void)grid;
+  (void)block;
+#else
   if (max_ntok <= 1)
     hipLaunchKernelGGL((k4_gemv_kernel<IM, FM, 1, MOE_K4_ALU_PAIRS, MOE_K4_PREFETCH>), grid, block, 0, stream, a);
   else
     hipLaunchKernelGGL((k4_gemv_kernel<IM, FM, kMaxRows, MOE_K4_ALU_PAIRS, MOE_K4_PREFETCH>), grid, block, 0, stream, a);
+#endif
   MOE_HIP(hipGetLastError());
   return MOE_OK;
 }
@@ -620,7 +939,7 @@ int moe_k4_expert_linear(const uint16_t* x, int x_per_slot, const uint32_t* ids,
   Workspace w = carve(workspace, wdim, wdim);
   hipStream_t s = (hipStream_t)stream;
   const int max_users = (x_per_slot || rows == 1) ? 1 : kMaxRows;
-  hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(64), 0, s, ids, rows, slots, (int)(experts > 257 ? 257 : experts),
+  hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(128), 0, s, ids, rows, slots, (int)(experts > 257 ? 257 : experts),
                      max_users, w.plan);
   MOE_HIP(hipGetLastError());
   GemvArgs a{};
@@ -657,7 +976,7 @@ static int k4_mlp_common(const uint16_t* x, const uint32_t* ids, const float* sc
   const int max_users = rows == 1 ? 1 : kMaxRows;
   if (!ids_on_plan) {
     MOE_ARG(ids != nullptr, "ids must not be NULL");
-    hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(64), 0, s, ids, rows, slots, (int)(experts > 257 ? 257 : experts),
+    hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(128), 0, s, ids, rows, slots, (int)(experts > 257 ? 257 : experts),
                        max_users, w.plan);
     MOE_HIP(hipGetLastError());
   }

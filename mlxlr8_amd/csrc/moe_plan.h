@@ -62,4 +62,53 @@ __device__ inline void build_plan(const uint32_t* idx, int rows, int slots, int 
   build_plan_serial(idx, rows, slots, experts, max_users, plan, unit_of_expert);
 }
 
+// Parallel plan build by one block (blockDim >= rows*slots, ids already in LDS `sid`), same result
+// as build_plan: units in order of first appearance, each expert's users split into consecutive
+// groups of `max_users`.  Pass 1: each slot finds its position among its expert's users and the
+// slot that opens its group; pass 2: its unit is the number of group-opening slots before that.
+// `open` is LDS scratch of kMaxUnits entries.  Every thread of the block must call this.
+__device__ inline void build_plan_parallel(const int32_t* sid, int rows, int slots, int max_users, Plan* plan,
+                                           int32_t* open) {
+  const int n = rows * slots;
+  const int s = threadIdx.x;
+  int pos = 0, start = s, total = 0, e = 0;
+  if (s < n) {
+    e = sid[s];
+    for (int q = 0; q < n; q++) {
+      if (sid[q] != e) continue;
+      if (q < s) pos++;
+      total++;
+    }
+    const int want = (pos / max_users) * max_users;
+    int seen = 0;
+    for (int q = 0; q <= s; q++) {
+      if (sid[q] != e) continue;
+      if (seen == want) { start = q; break; }
+      seen++;
+    }
+    open[s] = (pos % max_users) == 0;
+  }
+  __syncthreads();
+  if (s < n) {
+    int unit = 0;
+    for (int q = 0; q < start; q++) unit += open[q];
+    const int i = pos % max_users;
+    if (i == 0) {
+      plan->expert[unit] = e;
+      const int left = total - pos;
+      plan->ntok[unit] = left < max_users ? left : max_users;
+    }
+    plan->tok[unit][i] = s / slots;
+    plan->slot[unit][i] = s;
+    plan->slot_unit[s] = unit;
+    plan->slot_pos[s] = i;
+    if (s == 0) {
+      int units = 0;
+      for (int q = 0; q < n; q++) units += open[q];
+      plan->units = units;
+      plan->rows = rows;
+    }
+  }
+}
+
 }  // namespace moe

@@ -1,0 +1,366 @@
+// Resident joined-MXFP4 expert path on gfx950 (decode batches).
+//
+// Reference semantics (paths relative to the reference root):
+//   xh = H128(x * unit), shared by all slots                  exlr8/joined_mxfp4.py:96
+//   gu = xh @ W_gate_up[e]^T (MXFP4, group 32 along K)          exlr8/joined_mxfp4.py:106-113
+//   hidden = H128(swiglu_T(H(g)*og, H(u)*ou) * in_down)        exlr8/metal/joined_gate_finish.metal
+//   v = hidden @ W_down[e]^T                                     exlr8/joined_mxfp4.py:121-130
+//   finish: T(H128(v) * out_down), routed sum, shared, residual exlr8/metal/fast_decode_finish_fused.metal
+//   e2m1 codes, low nibble = even k; e8m0 scale 2^(s-127)        exlr8/metal/joined_gather_order*.metal
+//
+// MI355X design: HBM-bound GEMV.  Each wave owns a contiguous range of output rows; a lane holds
+// the activations of its fixed K positions in VGPRs (K/64 floats), streams 16 B of codes per
+// 32-wide group with coalesced dwordx4 loads, converts 2 codes per instruction with the hardware
+// scaled FP4->f32 conversion (the e8m0 scale folded in, exact), and the row sum is one DPP
+// reduction.  Completion counters hand 128-row blocks to the gate finish / combine, as in the
+// K4 path.
+#include <hip/hip_runtime.h>
+
+#include "moe_device.h"
+#include "moe_host.h"
+#include "moe_plan.h"
+
+namespace moe {
+
+constexpr int kMxWaves = 8;
+constexpr int kMxThreads = kMxWaves * 64;
+
+enum MxMode { MX_GATEUP = 0, MX_DOWN_COMBINE = 1, MX_DOWN_VALUES = 2 };
+
+struct MxArgs {
+  const uint8_t* codes;        // [E][N][K/2]
+  const uint8_t* scales;       // [E][N][K/32]
+  int K, N;                    // input features, output rows per expert
+  const uint32_t* ids;         // [slots] expert id per slot (row-major [rows, slots_per_row])
+  int slots, slots_per_row;
+  int experts;
+  const uint16_t* x_bf16;      // GATEUP: [rows, K]
+  const uint16_t* unit;        // GATEUP: [K] fp16 (+-1)
+  const float* x_f32;          // DOWN: [slots, K] hidden
+  float* rowout;               // [slots][N] fp32 row results (write-through)
+  int32_t* counter_blk;        // [slots * N/128]
+  int32_t* counter_grp;        // GATEUP: [slots * (N/2)/128]; DOWN: [N/128]
+  const uint16_t* out_gate;    // [E][m]
+  const uint16_t* out_up;      // [E][m]
+  const uint16_t* in_down;     // [E][m]
+  float* hidden;               // GATEUP output [slots][m]
+  const uint16_t* out_down;    // [E][h]
+  const float* scores;         // [rows][8]
+  const uint16_t* residual;    // [rows][h]
+  uint16_t* out;               // [rows][h]
+  uint16_t* values;            // [slots][h]
+};
+
+__device__ __forceinline__ void st_wt(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ f32x2 ld_wt2(const float* p) {
+  const uint64_t v = __hip_atomic_load(reinterpret_cast<uint64_t*>(const_cast<float*>(p)), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_SYSTEM);
+  return f32x2{__uint_as_float((uint32_t)v), __uint_as_float((uint32_t)(v >> 32))};
+}
+__device__ __forceinline__ int cnt_add(int32_t* c, int v) {
+  int old = 0;
+  if (lane_id() == 0) old = __hip_atomic_fetch_add(c, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  return __shfl(old, 0, 64);
+}
+__device__ __forceinline__ void cnt_reset(int32_t* c) {
+  if (lane_id() == 0) __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ int slot_expert(const MxArgs& a, int s) {
+  int e = (int)a.ids[s];
+  if (e < 0) e = 0;
+  if (e >= a.experts) e = a.experts - 1;
+  return e;
+}
+
+// 8 scaled fp4 codes of a 32-bit word -> 8 floats, accumulated against x[0..7]
+__device__ __forceinline__ float dot8_fp4(uint32_t w, float scale, const float* x, float acc) {
+  const f32x2 v0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, scale, 0);
+  const f32x2 v1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, scale, 1);
+  const f32x2 v2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, scale, 2);
+  const f32x2 v3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, scale, 3);
+  acc = fmaf(x[0], v0.x, acc);
+  acc = fmaf(x[1], v0.y, acc);
+  acc = fmaf(x[2], v1.x, acc);
+  acc = fmaf(x[3], v1.y, acc);
+  acc = fmaf(x[4], v2.x, acc);
+  acc = fmaf(x[5], v2.y, acc);
+  acc = fmaf(x[6], v3.x, acc);
+  acc = fmaf(x[7], v3.y, acc);
+  return acc;
+}
+
+__device__ __forceinline__ float e8m0_to_f32(uint32_t s) { return __uint_as_float(s == 0 ? 0x00400000u : s << 23); }
+
+// KC = K / 2048 (16-byte chunks per lane per row): 3 for K = 6144 (gate/up), 1 for K = 2048 (down).
+template <int MODE, int KC>
+__global__ __launch_bounds__(kMxThreads) void mx_gemv_kernel(MxArgs a) {
+  __shared__ __attribute__((aligned(16))) float xs[2][KC * 2048];
+  const int K = KC * 2048;
+  const int N = a.N;
+  const int64_t total = (int64_t)a.slots * N;
+  const int G = gridDim.x;
+  const int64_t r0 = total * blockIdx.x / G, r1 = total * (blockIdx.x + 1) / G;
+  if (r0 >= r1) return;
+  const int s0 = (int)(r0 / N);
+  const int s1 = (int)((r1 - 1) / N);  // s1 <= s0 + 1 (host guarantees rows per block <= N)
+  const int lane = lane_id(), wv = wave_id_in_block();
+
+  // ---- stage the activation rows of the (at most two) slots this block touches
+  for (int q = 0; q <= s1 - s0; q++) {
+    const int s = s0 + q;
+    float* dst = xs[q];
+    if (MODE == MX_GATEUP) {
+      // H128(x_row * unit) for the slot's token row, one 128-block per wave iteration
+      const int row = s / a.slots_per_row;
+      for (int blk = wv; blk < K / 128; blk += kMxWaves) {
+        const int c = blk * 128 + 2 * lane;
+        const uint16_t* xr = a.x_bf16 + (int64_t)row * K + c;
+        float v0 = bf16_to_f32(xr[0]) * f16_to_f32(a.unit[c]);
+        float v1 = bf16_to_f32(xr[1]) * f16_to_f32(a.unit[c + 1]);
+        hadamard128_wave(v0, v1);
+        dst[c] = v0;
+        dst[c + 1] = v1;
+      }
+    } else {
+      for (int c = threadIdx.x * 4; c < K; c += kMxThreads * 4)
+        *reinterpret_cast<f32x4*>(dst + c) = *reinterpret_cast<const f32x4*>(a.x_f32 + (int64_t)s * K + c);
+    }
+  }
+  __syncthreads();
+
+  // ---- this wave's rows
+  const int64_t w0 = r0 + (r1 - r0) * wv / kMxWaves, w1 = r0 + (r1 - r0) * (wv + 1) / kMxWaves;
+  float x[KC * 32];
+  int cur = -1;
+  int64_t run_start = w0;
+  for (int64_t r = w0; r < w1; r++) {
+    const int s = (int)(r / N);
+    const int n = (int)(r % N);
+    if (s != cur) {
+      cur = s;
+      const float* src = xs[s - s0];
+      // lane holds k = 2048*i + 32*lane + j (static register indices)
+#pragma unroll
+      for (int i = 0; i < KC; i++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          const f32x4 v = *reinterpret_cast<const f32x4*>(src + 2048 * i + 32 * lane + 4 * j);
+          x[32 * i + 4 * j] = v.x; x[32 * i + 4 * j + 1] = v.y; x[32 * i + 4 * j + 2] = v.z; x[32 * i + 4 * j + 3] = v.w;
+        }
+    }
+    const int e = slot_expert(a, s);
+    const uint8_t* crow = a.codes + ((int64_t)e * N + n) * (K / 2);
+    const uint8_t* srow = a.scales + ((int64_t)e * N + n) * (K / 32);
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < KC; i++) {
+      const u32x4 w = *reinterpret_cast<const u32x4*>(crow + 1024 * i + 16 * lane);
+      const float sc = e8m0_to_f32(srow[64 * i + lane]);
+      acc = dot8_fp4(w.x, sc, x + 32 * i, acc);
+      acc = dot8_fp4(w.y, sc, x + 32 * i + 8, acc);
+      acc = dot8_fp4(w.z, sc, x + 32 * i + 16, acc);
+      acc = dot8_fp4(w.w, sc, x + 32 * i + 24, acc);
+    }
+    acc = wave_sum(acc);
+    if (lane == 63) st_wt(a.rowout + (int64_t)s * N + n, acc);
+
+    // close a run at the end of a 128-row block or of the wave's range
+    const bool block_end = ((n & 127) == 127) || (r + 1 == w1);
+    if (!block_end) continue;
+    const int nb = n >> 7;
+    const int run = (int)(r + 1 - run_start);
+    run_start = r + 1;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    const int cb = s * (N / 128) + nb;
+    if (cnt_add(&a.counter_blk[cb], run) + run != 128) continue;
+    // 128-row block (s, nb) complete
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    cnt_reset(&a.counter_blk[cb]);
+    if (MODE == MX_GATEUP) {
+      const int m = N / 2;
+      const int b = nb % (m / 128);
+      const int grp = s * (m / 128) + b;
+      if (cnt_add(&a.counter_grp[grp], 1) + 1 != 2) continue;
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+      cnt_reset(&a.counter_grp[grp]);
+      const int col = b * 128 + 2 * lane;
+      f32x2 g = ld_wt2(a.rowout + (int64_t)s * N + col);
+      f32x2 u = ld_wt2(a.rowout + (int64_t)s * N + m + col);
+      float g0 = g.x, g1 = g.y, u0 = u.x, u1 = u.y;
+      hadamard128_wave(g0, g1);
+      hadamard128_wave(u0, u1);
+      const int64_t si = (int64_t)e * m + col;
+      float h0 = swiglu_bf16(g0 * f16_to_f32(a.out_gate[si]), u0 * f16_to_f32(a.out_up[si]));
+      float h1 = swiglu_bf16(g1 * f16_to_f32(a.out_gate[si + 1]), u1 * f16_to_f32(a.out_up[si + 1]));
+      h0 *= f16_to_f32(a.in_down[si]);
+      h1 *= f16_to_f32(a.in_down[si + 1]);
+      hadamard128_wave(h0, h1);
+      *reinterpret_cast<f32x2*>(a.hidden + (int64_t)s * m + col) = f32x2{h0, h1};
+    } else if (MODE == MX_DOWN_VALUES) {
+      const int col = nb * 128 + 2 * lane;
+      f32x2 v = ld_wt2(a.rowout + (int64_t)s * N + col);
+      float v0 = v.x, v1 = v.y;
+      hadamard128_wave(v0, v1);
+      const int64_t si = (int64_t)e * N + col;
+      const uint32_t pk = (uint32_t)f32_to_bf16(v0 * f16_to_f32(a.out_down[si])) |
+                          ((uint32_t)f32_to_bf16(v1 * f16_to_f32(a.out_down[si + 1])) << 16);
+      *reinterpret_cast<uint32_t*>(a.values + (int64_t)s * N + col) = pk;
+    } else {
+      // per-slot bf16 value of this block, then the block's combine once every slot is done
+      const int col = nb * 128 + 2 * lane;
+      f32x2 v = ld_wt2(a.rowout + (int64_t)s * N + col);
+      float v0 = v.x, v1 = v.y;
+      hadamard128_wave(v0, v1);
+      const int64_t si = (int64_t)e * N + col;
+      const uint64_t pk = (uint64_t)__float_as_uint(round_bf16(v0 * f16_to_f32(a.out_down[si]))) |
+                          ((uint64_t)__float_as_uint(round_bf16(v1 * f16_to_f32(a.out_down[si + 1]))) << 32);
+      __hip_atomic_store(reinterpret_cast<uint64_t*>(a.rowout + (int64_t)s * N + col), pk, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_SYSTEM);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+      if (cnt_add(&a.counter_grp[nb], 1) + 1 != a.slots) continue;
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+      cnt_reset(&a.counter_grp[nb]);
+      const int rows = a.slots / kSlots;
+      for (int rr = 0; rr < rows; rr++) {
+        f32x2 y[kSlots];
+#pragma unroll
+        for (int j = 0; j < kSlots; j++) y[j] = ld_wt2(a.rowout + (int64_t)(rr * kSlots + j) * N + col);
+        float t0 = y[0].x * a.scores[rr * 8] + 0.0f, t1 = y[0].y * a.scores[rr * 8] + 0.0f;
+#pragma unroll
+        for (int j = 1; j < 8; j++) {
+          const float sc = a.scores[rr * 8 + j];
+          t0 = (y[j].x * sc + 0.0f) + t0;
+          t1 = (y[j].y * sc + 0.0f) + t1;
+        }
+        const float c0 = round_bf16(round_bf16(t0) + y[8].x);
+        const float c1 = round_bf16(round_bf16(t1) + y[8].y);
+        const int64_t o = (int64_t)rr * N + col;
+        const uint32_t pk2 = (uint32_t)f32_to_bf16(bf16_to_f32(a.residual[o]) + c0) |
+                             ((uint32_t)f32_to_bf16(bf16_to_f32(a.residual[o + 1]) + c1) << 16);
+        *reinterpret_cast<uint32_t*>(a.out + o) = pk2;
+      }
+    }
+  }
+}
+
+namespace {
+
+size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
+
+struct MxWorkspace {
+  int32_t* counter_blk;  // [72 * 48]
+  int32_t* counter_grp;  // [72 * 16] / [48]
+  float* rowout;         // [72][max(2m, h)]
+  float* hidden;         // [72][m]
+  size_t bytes;
+};
+
+MxWorkspace mx_carve(void* base, int h, int m) {
+  MxWorkspace w{};
+  size_t off = 0;
+  char* p = static_cast<char*>(base);
+  auto take = [&](size_t bytes) { char* r = p ? p + off : nullptr; off += align_up(bytes); return r; };
+  const int rowmax = 2 * m > h ? 2 * m : h;
+  w.counter_blk = reinterpret_cast<int32_t*>(take((size_t)kMaxUnits * (rowmax / 128) * 4));
+  w.counter_grp = reinterpret_cast<int32_t*>(take((size_t)kMaxUnits * (rowmax / 128) * 4));
+  w.rowout = reinterpret_cast<float*>(take((size_t)kMaxUnits * rowmax * 4));
+  w.hidden = reinterpret_cast<float*>(take((size_t)kMaxUnits * m * 4));
+  w.bytes = off;
+  return w;
+}
+
+int mx_blocks(int64_t rows_total, int n) {
+  int g = device_cus();
+  if (g < 1) g = 1;
+  if (g > 1024) g = 1024;
+  // each block must span at most two slots: rows per block <= n
+  const int64_t need = (rows_total + n - 1) / n;
+  if (g < need) g = (int)need;
+  return g;
+}
+
+int mx_common(const uint16_t* x, const uint32_t* ids, const float* scores, const uint16_t* residual, int rows,
+              int slots_per_row, const uint8_t* gu_codes, const uint8_t* gu_scales, const uint8_t* d_codes,
+              const uint8_t* d_scales, int64_t experts, const uint16_t* unit, const uint16_t* out_gate,
+              const uint16_t* out_up, const uint16_t* in_down, const uint16_t* out_down, int h, int m,
+              uint16_t* values, uint16_t* out, void* workspace, size_t workspace_bytes, hipStream_t s) {
+  MOE_ARG(x && ids && gu_codes && gu_scales && d_codes && d_scales && unit && out_gate && out_up && in_down && out_down,
+          "null pointer argument");
+  MOE_ARG(h == 6144 && m == 2048, "this build's MXFP4 kernels are specialised for hidden 6144, intermediate 2048");
+  MOE_ARG(rows >= 1 && slots_per_row >= 1 && slots_per_row <= kSlots && rows * slots_per_row <= kMaxUnits,
+          "rows*slots must be in 1..%d", kMaxUnits);
+  MOE_ARG(experts >= 1 && experts <= 257, "expert count must be in 1..257");
+  MOE_ARG(workspace != nullptr, "workspace must not be NULL");
+  MxWorkspace w = mx_carve(nullptr, h, m);
+  if (workspace_bytes < w.bytes) return fail(MOE_EWORKSPACE, "workspace too small: %zu < %zu", workspace_bytes, w.bytes);
+  int rc = ensure_device_ready();
+  if (rc) return rc;
+  w = mx_carve(workspace, h, m);
+  const int slots = rows * slots_per_row;
+
+  MxArgs g{};
+  g.codes = gu_codes; g.scales = gu_scales; g.K = h; g.N = 2 * m;
+  g.ids = ids; g.slots = slots; g.slots_per_row = slots_per_row; g.experts = (int)experts;
+  g.x_bf16 = x; g.unit = unit;
+  g.rowout = w.rowout; g.counter_blk = w.counter_blk; g.counter_grp = w.counter_grp;
+  g.out_gate = out_gate; g.out_up = out_up; g.in_down = in_down; g.hidden = w.hidden;
+  hipLaunchKernelGGL((mx_gemv_kernel<MX_GATEUP, 3>), dim3(mx_blocks((int64_t)slots * 2 * m, 2 * m)), dim3(kMxThreads),
+                     0, s, g);
+  MOE_HIP(hipGetLastError());
+
+  MxArgs d{};
+  d.codes = d_codes; d.scales = d_scales; d.K = m; d.N = h;
+  d.ids = ids; d.slots = slots; d.slots_per_row = slots_per_row; d.experts = (int)experts;
+  d.x_f32 = w.hidden;
+  d.rowout = w.rowout; d.counter_blk = w.counter_blk; d.counter_grp = w.counter_grp;
+  d.out_down = out_down;
+  const dim3 grid(mx_blocks((int64_t)slots * h, h));
+  if (out) {
+    MOE_ARG(slots_per_row == kSlots && scores && residual, "the combined finish needs 9 slots, scores and residual");
+    d.scores = scores; d.residual = residual; d.out = out;
+    hipLaunchKernelGGL((mx_gemv_kernel<MX_DOWN_COMBINE, 1>), grid, dim3(kMxThreads), 0, s, d);
+  } else {
+    d.values = values;
+    hipLaunchKernelGGL((mx_gemv_kernel<MX_DOWN_VALUES, 1>), grid, dim3(kMxThreads), 0, s, d);
+  }
+  MOE_HIP(hipGetLastError());
+  return MOE_OK;
+}
+
+}  // namespace
+}  // namespace moe
+
+using namespace moe;
+
+extern "C" {
+
+size_t moe_mxfp4_workspace_bytes(int hidden, int intermediate) {
+  return mx_carve(nullptr, hidden > 0 ? hidden : 1, intermediate > 0 ? intermediate : 1).bytes;
+}
+
+int moe_mxfp4_mlp(const uint16_t* x, const uint32_t* ids, int rows, int slots, const uint8_t* gate_up_codes,
+                  const uint8_t* gate_up_scales, const uint8_t* down_codes, const uint8_t* down_scales,
+                  int64_t experts, const uint16_t* unit, const uint16_t* out_gate, const uint16_t* out_up,
+                  const uint16_t* in_down, const uint16_t* out_down, int hidden, int intermediate, uint16_t* values,
+                  void* workspace, size_t workspace_bytes, moe_stream_t stream) {
+  MOE_ARG(values != nullptr, "values must not be NULL");
+  return mx_common(x, ids, nullptr, nullptr, rows, slots, gate_up_codes, gate_up_scales, down_codes, down_scales,
+                   experts, unit, out_gate, out_up, in_down, out_down, hidden, intermediate, values, nullptr,
+                   workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int moe_mxfp4_mlp_finish(const uint16_t* x, const uint32_t* ids, const float* scores, const uint16_t* residual,
+                         int rows, const uint8_t* gate_up_codes, const uint8_t* gate_up_scales,
+                         const uint8_t* down_codes, const uint8_t* down_scales, int64_t experts,
+                         const uint16_t* unit, const uint16_t* out_gate, const uint16_t* out_up,
+                         const uint16_t* in_down, const uint16_t* out_down, int hidden, int intermediate,
+                         uint16_t* out, void* workspace, size_t workspace_bytes, moe_stream_t stream) {
+  MOE_ARG(out != nullptr, "out must not be NULL");
+  return mx_common(x, ids, scores, residual, rows, kSlots, gate_up_codes, gate_up_scales, down_codes, down_scales,
+                   experts, unit, out_gate, out_up, in_down, out_down, hidden, intermediate, nullptr, out, workspace,
+                   workspace_bytes, (hipStream_t)stream);
+}
+
+}  // extern "C"

@@ -116,7 +116,8 @@ __device__ __forceinline__ uint32_t float_key(float f) {
 // are then ranked against each other and the scores summed in rank order.
 template <bool COHERENT = false>
 __device__ __forceinline__ void route_row(const float* __restrict__ logits, const float* __restrict__ bias, int row,
-                                          uint32_t* __restrict__ ids, float* __restrict__ scores) {
+                                          uint32_t* __restrict__ ids, float* __restrict__ scores,
+                                          int32_t* sid = nullptr) {
   const int lane = lane_id();
   float orig[4];
   uint64_t key[4];
@@ -181,6 +182,7 @@ __device__ __forceinline__ void route_row(const float* __restrict__ logits, cons
     }
     ids[(int64_t)row * 9 + 8] = 256u;
   }
+  if (sid != nullptr && lane < 9) sid[row * 9 + lane] = lane < 8 ? idl[lane] : 256;
 }
 
 __global__ __launch_bounds__(64) void route_kernel(const float* __restrict__ logits, const float* __restrict__ bias,
@@ -218,7 +220,8 @@ __global__ __launch_bounds__(256) void router_decode_kernel(const uint16_t* __re
   }
   __shared__ float red[R][4];
   __shared__ int last;
-  __shared__ int32_t unit_of_expert[257];
+  __shared__ int32_t sid[kMaxUnits];
+  __shared__ int32_t open[kMaxUnits];
   const int lane = lane_id(), wv = wave_id_in_block();
 #pragma unroll
   for (int r = 0; r < R; r++) {
@@ -238,14 +241,11 @@ __global__ __launch_bounds__(256) void router_decode_kernel(const uint16_t* __re
   __syncthreads();
   if (!last) return;
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-  for (int i = threadIdx.x; i < 257; i += blockDim.x) unit_of_expert[i] = -1;
-  for (int row = wv; row < rows; row += 4) route_row<true>(logits, bias, row, ids, scores);
-  __threadfence_block();
+  for (int row = wv; row < rows; row += 4) route_row<true>(logits, bias, row, ids, scores, sid);
   __syncthreads();
-  if (threadIdx.x == 0) {
-    build_plan_serial(ids, rows, kSlots, experts, max_users, plan, unit_of_expert);
-    __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-  }
+  (void)experts;  // routed ids are 0..255 plus the shared expert 256
+  build_plan_parallel(sid, rows, kSlots, max_users, plan, open);
+  if (threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 int launch_router_logits(const uint16_t* x, const float* w, int rows, int hidden, int experts, float* logits,

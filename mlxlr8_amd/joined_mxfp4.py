@@ -1,0 +1,87 @@
+"""Resident joined-MXFP4 experts (mirrors the reference ``exlr8/joined_mxfp4.py``).
+
+Gate and up of every expert are one ``[2m, h]`` MXFP4 matrix (e2m1 codes, one e8m0 scale per
+32 along K, the per-128-block input scale magnitudes folded in); down is ``[h, m]``.  All
+slots share ``xh = H128(x * unit)``.  ``slots`` returns per-slot expert values and ``finish``
+the combined layer output; both run in ``libmoe_mi355x.so``.
+"""
+import torch
+
+from ._lib import check, lib, ptr, require_cuda, stream, workspace
+
+BF16 = torch.bfloat16
+
+
+def encode(expert):
+    """Load-time K4 -> MXFP4 conversion (exlr8/joined_mxfp4.py:12-47).
+
+    Not part of this build: the reference quantises with MLX's ``mx.quantize(mode="mxfp4")``,
+    whose scale/rounding choice cannot be pinned here.  Construct ``JoinedMXFP4`` from MXFP4
+    tensors directly.
+    """
+    raise NotImplementedError("K4 -> MXFP4 encoding is not built (MLX quantizer parity is unpinned)")
+
+
+class JoinedMXFP4:
+    """``weights = {"gate_up": (codes, scales), "down": (codes, scales)}``, ``unit`` fp16 [h],
+    ``scales = {"gate": (None, out_gate), "up": (None, out_up), "down": (in_down, out_down)}``."""
+
+    def __init__(self, weights, unit, scales, hidden, intermediate):
+        self.weights, self.unit, self.scales = weights, unit, scales
+        self.hidden, self.intermediate = hidden, intermediate
+        codes, sc = weights["gate_up"]
+        if codes.dim() != 3 or tuple(codes.shape[1:]) != (2 * intermediate, hidden // 2) \
+                or tuple(sc.shape) != (codes.shape[0], 2 * intermediate, hidden // 32):
+            raise ValueError("gate_up must be [experts, 2m, h/2] codes with [experts, 2m, h/32] scales")
+        dcodes, dsc = weights["down"]
+        if tuple(dcodes.shape) != (codes.shape[0], hidden, intermediate // 2) \
+                or tuple(dsc.shape) != (codes.shape[0], hidden, intermediate // 32):
+            raise ValueError("down must be [experts, h, m/2] codes with [experts, h, m/32] scales")
+        self.experts = codes.shape[0]
+        require_cuda(codes, sc, dcodes, dsc, unit)
+
+    def _args(self):
+        (gc, gs), (dc, ds) = self.weights["gate_up"], self.weights["down"]
+        return [ptr(gc), ptr(gs), ptr(dc), ptr(ds), self.experts, ptr(self.unit), ptr(self.scales["gate"][1]),
+                ptr(self.scales["up"][1]), ptr(self.scales["down"][0]), ptr(self.scales["down"][1])]
+
+    def slots(self, x, ids):
+        """values [*ids.shape, h] (exlr8/joined_mxfp4.py:143-147)."""
+        h = self.hidden
+        if x.shape[-1] != h or tuple(x.shape[:-1]) != tuple(ids.shape[:-1]):
+            raise ValueError("activation rows do not match the expert indices")
+        if x.dtype != BF16:
+            raise ValueError("this build computes bf16 activations")
+        slots = ids.shape[-1]
+        idx = ids.reshape(-1, slots).to(torch.int32).contiguous()
+        rows = idx.shape[0]
+        xr = x.reshape(rows, h).contiguous()
+        values = torch.empty((rows * slots, h), dtype=BF16, device=x.device)
+        ws = workspace(x.device, h, self.intermediate, "mxfp4")
+        st = stream(x.device)
+        step = max(1, 72 // slots)
+        for r0 in range(0, rows, step):
+            r1 = min(rows, r0 + step)
+            check(lib().moe_mxfp4_mlp(ptr(xr[r0:r1]), ptr(idx[r0:r1]), r1 - r0, slots, *self._args(), h,
+                                      self.intermediate, ptr(values[r0 * slots:r1 * slots]), ptr(ws), ws.numel(), st))
+        return values.reshape(*ids.shape, h)
+
+    def finish(self, x, ids, scores, residual):
+        """residual + T(sum_i values_i * scores_i) + shared (exlr8/joined_mxfp4.py:148-163)."""
+        h = self.hidden
+        rows = x.numel() // h
+        if x.dtype != BF16:
+            raise ValueError("this build computes bf16 activations")
+        xr = x.reshape(rows, h).contiguous()
+        idx = ids.reshape(rows, 9).to(torch.int32).contiguous()
+        sc = scores.reshape(rows, 8).to(torch.float32).contiguous()
+        res = residual.reshape(rows, h).to(BF16).contiguous()
+        out = torch.empty((rows, h), dtype=BF16, device=x.device)
+        ws = workspace(x.device, h, self.intermediate, "mxfp4")
+        st = stream(x.device)
+        for r0 in range(0, rows, 8):
+            r1 = min(rows, r0 + 8)
+            check(lib().moe_mxfp4_mlp_finish(ptr(xr[r0:r1]), ptr(idx[r0:r1]), ptr(sc[r0:r1]), ptr(res[r0:r1]), r1 - r0,
+                                             *self._args(), h, self.intermediate, ptr(out[r0:r1]), ptr(ws), ws.numel(),
+                                             st))
+        return out.reshape(residual.shape)
