@@ -70,26 +70,59 @@ __global__ __launch_bounds__(128) void plan_kernel(const uint32_t* __restrict__ 
 
 // ============================================================== decode-only kernel
 
-// One thread per output element; inner [in, out] fp16.  exlr8/metal/decode.metal semantics.
-__global__ void trellis_decode_kernel(const uint32_t* __restrict__ packed, int in_f, int out_f, int side,
-                                      int64_t expert, uint16_t* __restrict__ inner) {
+// Inner [in, out] fp16 of one expert (exlr8/metal/decode.metal semantics), decoded with the same
+// device code as the GEMVs: thread = one 16 B piece (4 consecutive words of a tile), words
+// decoded in pairs by decode_pair_words_f16.  Each block uses one of four arithmetic/table mixes,
+// so a full decode exercises every route of the GEMV decoder.
+template <int NE, int NO>
+__device__ __forceinline__ void decode_piece_to_inner(const uint32_t* __restrict__ tw, int qg, const uint8_t* tab,
+                                                      uint16_t* __restrict__ inner, int out_f, uint32_t row0,
+                                                      uint32_t col0) {
+  const u32x4 v = *reinterpret_cast<const u32x4*>(tw + 4 * qg);
+  const uint32_t prior = tw[(4 * qg + 31) & 31];
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    f16x2 q[2][4];
+    if (h == 0)
+      decode_pair_words_f16<NE, NO>(v.x, v.y, prior, tab, q);
+    else
+      decode_pair_words_f16<NE, NO>(v.z, v.w, v.y, tab, q);
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        // word 2h+i, pair j: rows 2(2h+i) + 8*(j&1) + {0,1}, column qg + 8*(j>>1)
+        const uint32_t r = row0 + 2 * (2 * h + i) + 8 * (j & 1), c = col0 + qg + 8 * (j >> 1);
+        const uint32_t bits = __builtin_bit_cast(uint32_t, q[i][j]);
+        inner[(int64_t)r * out_f + c] = (uint16_t)(bits & 0xFFFFu);
+        inner[(int64_t)(r + 1) * out_f + c] = (uint16_t)(bits >> 16);
+      }
+  }
+}
+
+__global__ __launch_bounds__(1024) void trellis_decode_kernel(const uint32_t* __restrict__ packed, int in_f, int out_f,
+                                                              int side, int64_t expert, uint16_t* __restrict__ inner) {
+  __shared__ __attribute__((aligned(16))) uint8_t tab[65536];
+  load_codebook_lds(tab);
+  __syncthreads();
+  const int64_t pieces = (int64_t)in_f * out_f / 32;  // 8 pieces per 256-weight tile
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (int64_t)in_f * out_f) return;
-  const uint32_t r = (uint32_t)(idx / out_f), c = (uint32_t)(idx % out_f);
+  if (idx >= pieces) return;
   const uint32_t it = (uint32_t)in_f / 16u, ot = (uint32_t)out_f / 16u;
-  const uint32_t tk = r / 16u, tn = c / 16u, lr = r & 15u, lc = c & 15u;
-  const uint32_t lane = (lc & 7u) * 4u + ((lr & 7u) >> 1u);
-  const uint32_t slot = (lr & 1u) + ((lr & 8u) >> 2u) + ((lc & 8u) >> 1u);
+  const int64_t t = idx >> 3;
+  const int qg = (int)(idx & 7);
+  // tile t in row-major (tk, tn) order -> storage index of the side's layout
+  const uint32_t tk = (uint32_t)(t / ot), tn = (uint32_t)(t % ot);
   const uint64_t e = (uint64_t)expert;
-  uint64_t tile = side == 2 ? ((((e * (it / 8u) + tk / 8u) * (ot / 8u) + tn / 8u) * 8u + tk % 8u) * 8u + tn % 8u)
-                            : (((e * (ot / 8u) + tn / 8u) * it + tk) * 8u + tn % 8u);
-  const uint32_t* w = packed + tile * 32u;
-  const uint32_t word = w[lane], prior = w[(lane + 31u) & 31u];
-  const uint32_t shift = 28u - 4u * slot;  // window of slot s ends 4*(s+1) bits into the word
-  const uint64_t merged = ((uint64_t)prior << 32) | word;
-  const uint32_t cw = (uint32_t)(merged >> shift) & 0xFFFFu;
-  const float v = fp8_to_f32(g_codebook_e4m3[cw]);
-  inner[idx] = __builtin_bit_cast(uint16_t, (_Float16)v);
+  const uint64_t tile = side == 2 ? ((((e * (it / 8u) + tk / 8u) * (ot / 8u) + tn / 8u) * 8u + tk % 8u) * 8u + tn % 8u)
+                                  : (((e * (ot / 8u) + tn / 8u) * it + tk) * 8u + tn % 8u);
+  const uint32_t* tw = packed + tile * 32u;
+  switch (blockIdx.x & 3) {
+    case 0: decode_piece_to_inner<0, 0>(tw, qg, tab, inner, out_f, 16u * tk, 16u * tn); break;
+    case 1: decode_piece_to_inner<1, 2>(tw, qg, tab, inner, out_f, 16u * tk, 16u * tn); break;
+    case 2: decode_piece_to_inner<2, 2>(tw, qg, tab, inner, out_f, 16u * tk, 16u * tn); break;
+    default: decode_piece_to_inner<4, 4>(tw, qg, tab, inner, out_f, 16u * tk, 16u * tn); break;
+  }
 }
 
 // ============================================================== GEMV machinery
@@ -97,29 +130,28 @@ __global__ void trellis_decode_kernel(const uint32_t* __restrict__ packed, int i
 enum InMode { IN_PREP = 0, IN_DIRECT = 1 };
 enum FinMode { FIN_GATE = 0, FIN_VALUES = 1, FIN_COMBINE = 2 };
 
-// Decode mix (codeword pairs per word decoded arithmetically; the rest use the LDS table) and
-// the depth of the per-wave chunk prefetch ring, chosen by measurement on MI355X.
-#ifndef MOE_K4_ALU_PAIRS
-#define MOE_K4_ALU_PAIRS 1
+// Decode GEMV (k4_mfma_kernel): per-word arithmetic pair counts (even, odd
+// words) for single-token units (_1) and for units of up to kMaxRows tokens (_8), chosen by
+// measurement on MI355X
+#ifndef MOE_K4_ALU_EVEN_1
+#define MOE_K4_ALU_EVEN_1 2
 #endif
-#ifndef MOE_K4_PREFETCH
-#define MOE_K4_PREFETCH 3
+#ifndef MOE_K4_ALU_ODD_1
+#define MOE_K4_ALU_ODD_1 2
 #endif
-// MFMA-accumulated decode GEMV (k4_mfma_kernel) and its per-word ALU pair counts (even, odd words)
-#ifndef MOE_K4_MFMA
-#define MOE_K4_MFMA 1
+#ifndef MOE_K4_ALU_EVEN_8
+#define MOE_K4_ALU_EVEN_8 1
 #endif
-#ifndef MOE_K4_ALU_EVEN
-#define MOE_K4_ALU_EVEN 1
+#ifndef MOE_K4_ALU_ODD_8
+#define MOE_K4_ALU_ODD_8 2
 #endif
-#ifndef MOE_K4_ALU_ODD
-#define MOE_K4_ALU_ODD 2
+// waves per block of the MFMA kernel for single-token units and for up to kMaxRows tokens (the
+// latter needs more registers for its A fragments)
+#ifndef MOE_K4_WAVES_1
+#define MOE_K4_WAVES_1 8
 #endif
-#ifndef MOE_K4_MFMA_WAVES
-#define MOE_K4_MFMA_WAVES 8
-#endif
-#ifndef MOE_K4_CHAIN
-#define MOE_K4_CHAIN 0
+#ifndef MOE_K4_WAVES_8
+#define MOE_K4_WAVES_8 8
 #endif
 
 constexpr int kWaves = 16;            // waves per block (one block per CU)
@@ -140,7 +172,6 @@ struct GemvArgs {
   float* partial;              // [W][2][kMaxRows][128]
   int32_t* counter_seg;        // chunks completed per segment
   int32_t* counter_grp;        // segments completed per finish group
-  float* segbuf;               // GATE: reduced segment sums [seg][kMaxRows][128]
   float* yslot;                // COMBINE: bf16-rounded expert outputs [slot][out_f]
   const uint16_t* out_scale[2];
   const uint16_t* in_down;     // GATE
@@ -195,33 +226,65 @@ __device__ __forceinline__ int wave_of_chunk(int64_t c, int64_t n, int nw) {
   return w;
 }
 
+// Partial sums of one segment: the waves overlapping it and, for each, the visit that covers it.
+struct SegWaves {
+  int64_t a;  // first work unit of the segment
+  int wa, wb;
+};
+__device__ __forceinline__ SegWaves seg_waves(int64_t n, int nw, int ups, int seg) {
+  const int64_t a = (int64_t)seg * ups;
+  return SegWaves{a, wave_of_chunk(a, n, nw), wave_of_chunk(a + ups - 1, n, nw)};
+}
+// Load the partial pair of wave w for segment sw, token t, columns 2*lane, +1 (zero if the wave
+// has no work there).
+__device__ __forceinline__ f32x2 load_partial(const float* __restrict__ partial, int64_t n, int nw, const SegWaves& sw,
+                                              int w, int t, bool& ok) {
+  const int64_t s = range_start(n, w, nw);
+  ok = w <= sw.wb && range_start(n, w + 1, nw) > s;
+  const int visit = (s >= sw.a) ? 0 : 1;
+  const int64_t idx = ok ? ((int64_t)w * 2 + visit) * kPartialStride + (int64_t)t * 128 + 2 * lane_id() : 0;
+  return load_coherent2(partial + idx);
+}
+
 // Sum, in wave order, the partials of segment `seg` for token position `t` at columns
 // 2*lane and 2*lane+1.  Work is partitioned in units (a chunk, or a quad of chunks); segment
 // `seg` covers units [seg*ups, (seg+1)*ups) of `n` units split over `nw` waves.  Loads are
-// issued in batches of 8 waves so one memory round trip covers a batch; empty wave ranges
+// issued in batches of 16 waves so one memory round trip covers a batch; empty wave ranges
 // contribute nothing.
 __device__ __forceinline__ void sum_partials(const float* __restrict__ partial, int64_t n, int nw, int ups, int seg,
                                              int t, float& v0, float& v1) {
-  const int64_t a = (int64_t)seg * ups, b = a + ups;
-  const int wa = wave_of_chunk(a, n, nw), wb = wave_of_chunk(b - 1, n, nw);
-  const int lane = lane_id();
+  const SegWaves sw = seg_waves(n, nw, ups, seg);
   v0 = 0.0f;
   v1 = 0.0f;
-  for (int w0 = wa; w0 <= wb; w0 += 8) {
-    f32x2 p[8];
-    bool ok[8];
+  for (int w0 = sw.wa; w0 <= sw.wb; w0 += 16) {
+    f32x2 p[16];
+    bool ok[16];
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-      const int w = w0 + j;
-      const int64_t s = range_start(n, w, nw);
-      ok[j] = w <= wb && range_start(n, w + 1, nw) > s;
-      const int visit = (s >= a) ? 0 : 1;
-      const int64_t idx = ok[j] ? ((int64_t)w * 2 + visit) * kPartialStride + (int64_t)t * 128 + 2 * lane : 0;
-      p[j] = load_coherent2(partial + idx);
+    for (int j = 0; j < 16; j++) p[j] = load_partial(partial, n, nw, sw, w0 + j, t, ok[j]);
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+      if (ok[j]) { v0 += p[j].x; v1 += p[j].y; }
+    }
+  }
+}
+// The same for two segments at once (their loads share round trips).
+__device__ __forceinline__ void sum_partials_pair(const float* __restrict__ partial, int64_t n, int nw, int ups,
+                                                  int seg_a, int seg_b, int t, f32x2& ra, f32x2& rb) {
+  const SegWaves sa = seg_waves(n, nw, ups, seg_a), sb = seg_waves(n, nw, ups, seg_b);
+  ra = f32x2{0.0f, 0.0f};
+  rb = f32x2{0.0f, 0.0f};
+  for (int k = 0; sa.wa + k <= sa.wb || sb.wa + k <= sb.wb; k += 12) {
+    f32x2 pa[12], pb[12];
+    bool oka[12], okb[12];
+#pragma unroll
+    for (int j = 0; j < 12; j++) {
+      pa[j] = load_partial(partial, n, nw, sa, sa.wa + k + j, t, oka[j]);
+      pb[j] = load_partial(partial, n, nw, sb, sb.wa + k + j, t, okb[j]);
     }
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-      if (ok[j]) { v0 += p[j].x; v1 += p[j].y; }
+    for (int j = 0; j < 12; j++) {
+      if (oka[j]) { ra.x += pa[j].x; ra.y += pa[j].y; }
+      if (okb[j]) { rb.x += pb[j].x; rb.y += pb[j].y; }
     }
   }
 }
@@ -234,39 +297,18 @@ __device__ __forceinline__ void complete_visit(const GemvArgs& a, const Plan* __
                                                int ups, int64_t n, int nw, int nproj, int U, int u, int ob, int e,
                                                int ntok) {
   const int lane = lane_id();
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-  if (counter_add(&a.counter_seg[seg], units) + units != ups) return;
-  // this wave completed segment `seg`: reduce its partials once
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-  counter_reset(&a.counter_seg[seg]);
-  const int obs = a.out_f / 128;
   const int col = ob * 128 + 2 * lane;
-  if (FM == FIN_VALUES) {
-    for (int t = 0; t < ntok; t++) {
-      float v0, v1;
-      sum_partials(a.partial, n, nw, ups, seg, t, v0, v1);
-      hadamard128_wave(v0, v1);
-      const int64_t si = (int64_t)e * a.out_f + col;
-      const int slot = P->slot[u][t];
-      const uint32_t packed2 = (uint32_t)f32_to_bf16(v0 * f16_to_f32(a.out_scale[0][si])) |
-                               ((uint32_t)f32_to_bf16(v1 * f16_to_f32(a.out_scale[0][si + 1])) << 16);
-      *reinterpret_cast<uint32_t*>(a.values + (int64_t)slot * a.out_f + col) = packed2;
-    }
-  } else if (FM == FIN_GATE) {
-    for (int t = 0; t < ntok; t++) {
-      float v0, v1;
-      sum_partials(a.partial, n, nw, ups, seg, t, v0, v1);
-      store_coherent2(a.segbuf + ((int64_t)seg * kMaxRows + t) * 128 + 2 * lane, v0, v1);
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    const int grp = u * obs + ob;
-    if (counter_add(&a.counter_grp[grp], 1) + 1 != nproj) return;
-    // gate and up of this column block are both reduced: gate finish
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  if (FM == FIN_GATE) {
+    // gate and up of one column block are the adjacent segments 2*grp and 2*grp+1: one counter
+    // covers both, and the wave that completes them reduces both and runs the gate finish
+    const int grp = seg >> 1;
+    if (counter_add(&a.counter_grp[grp], units) + units != 2 * ups) return;
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     counter_reset(&a.counter_grp[grp]);
     for (int t = 0; t < ntok; t++) {
-      const f32x2 g = load_coherent2(a.segbuf + ((int64_t)(grp * 2 + 0) * kMaxRows + t) * 128 + 2 * lane);
-      const f32x2 uu = load_coherent2(a.segbuf + ((int64_t)(grp * 2 + 1) * kMaxRows + t) * 128 + 2 * lane);
+      f32x2 g, uu;
+      sum_partials_pair(a.partial, n, nw, ups, 2 * grp, 2 * grp + 1, t, g, uu);
       float g0 = g.x, g1 = g.y, u0 = uu.x, u1 = uu.y;
       hadamard128_wave(g0, g1);
       hadamard128_wave(u0, u1);
@@ -278,6 +320,23 @@ __device__ __forceinline__ void complete_visit(const GemvArgs& a, const Plan* __
       hadamard128_wave(h0, h1);
       const int slot = P->slot[u][t];
       *reinterpret_cast<f32x2*>(a.down_xh + (int64_t)slot * a.out_f + col) = f32x2{h0, h1};
+    }
+    return;
+  }
+  if (counter_add(&a.counter_seg[seg], units) + units != ups) return;
+  // this wave completed segment `seg`: reduce its partials once
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  counter_reset(&a.counter_seg[seg]);
+  if (FM == FIN_VALUES) {
+    for (int t = 0; t < ntok; t++) {
+      float v0, v1;
+      sum_partials(a.partial, n, nw, ups, seg, t, v0, v1);
+      hadamard128_wave(v0, v1);
+      const int64_t si = (int64_t)e * a.out_f + col;
+      const int slot = P->slot[u][t];
+      const uint32_t packed2 = (uint32_t)f32_to_bf16(v0 * f16_to_f32(a.out_scale[0][si])) |
+                               ((uint32_t)f32_to_bf16(v1 * f16_to_f32(a.out_scale[0][si + 1])) << 16);
+      *reinterpret_cast<uint32_t*>(a.values + (int64_t)slot * a.out_f + col) = packed2;
     }
   } else {
     // per-slot expert output of this column block: T(H128(inner) * out_scale)
@@ -317,150 +376,17 @@ __device__ __forceinline__ void complete_visit(const GemvArgs& a, const Plan* __
   }
 }
 
-// Partial column order inside a 128-column block: lane L owns 16*(L/8)+L%8 (acc0) and +8 (acc1).
-__device__ __forceinline__ int col_acc0(int lane) { return 16 * (lane >> 3) + (lane & 7); }
-
-template <int IM, int FM, int NT, int ALU, int PF>
-__global__ __launch_bounds__(kThreads) void k4_gemv_kernel(GemvArgs a) {
-  __shared__ __attribute__((aligned(16))) uint8_t tab[65536];
-  __shared__ __attribute__((aligned(16))) float xs[kWaves * NT * 128];
-
-  load_codebook_lds(tab);
-  __syncthreads();
-
-  const Plan* __restrict__ P = a.plan;
-  const int U = P->units;
-  const int it = a.in_f / 16;
-  const int obs = a.out_f / 128;
-  const int nproj = a.nproj;
-  const int64_t nseg = (int64_t)U * obs * nproj;
-  const int64_t n = nseg * it;
-  const int nw = gridDim.x * kWaves;
-  const int wave = blockIdx.x * kWaves + wave_id_in_block();
-  const int lane = lane_id();
-  const int64_t c_begin = range_start(n, wave, nw), c_end = range_start(n, wave + 1, nw);
-  float* xw = xs + wave_id_in_block() * NT * 128;
-  const int src_lane = (lane & 7) == 0 ? lane + 7 : lane - 1;
-
-  int visit = 0;
-  for (int64_t c = c_begin; c < c_end; visit++) {
-    const int seg = (int)(c / it);
-    const int tk0 = (int)(c % it);
-    const int tk1 = (int)min((int64_t)it, (int64_t)tk0 + (c_end - c));
-    const int proj = seg % nproj;
-    const int ob = (seg / nproj) % obs;
-    const int u = seg / (nproj * obs);
-    const int e = P->expert[u];
-    const int ntok = P->ntok[u];
-    const uint8_t* __restrict__ base = a.packed[proj];
-
-    float acc[NT][2];
-#pragma unroll
-    for (int t = 0; t < NT; t++) { acc[t][0] = 0.0f; acc[t][1] = 0.0f; }
-
-    auto chunk_ptr = [&](int tk) {
-      return reinterpret_cast<const u32x4*>(base + chunk_offset(a.side, e, ob, tk, it, obs) + lane * 16);
-    };
-    // Stage x for the 128-row block holding tk in this wave's LDS slice: PREP computes
-    // H128(x * in_scale[e]) from bf16 rows; DIRECT copies already-transformed fp32 rows.
-    auto stage_block = [&](int tk) {
-      const int blk = tk >> 3;
-      if (IM == IN_PREP) {
-        const uint16_t* __restrict__ sc = a.in_scale[proj] + (int64_t)e * a.in_f + blk * 128 + 2 * lane;
-        const float s0 = f16_to_f32(sc[0]), s1 = f16_to_f32(sc[1]);
-#pragma unroll
-        for (int t = 0; t < NT; t++) {
-          if (t < ntok) {
-            const int row = a.x_per_slot ? P->slot[u][t] : P->tok[u][t];
-            const uint16_t* __restrict__ xr = a.x_bf16 + (int64_t)row * a.in_f + blk * 128 + 2 * lane;
-            float v0 = bf16_to_f32(xr[0]) * s0, v1 = bf16_to_f32(xr[1]) * s1;
-            hadamard128_wave(v0, v1);
-            *reinterpret_cast<f32x2*>(xw + t * 128 + 2 * lane) = f32x2{v0, v1};
-          }
-        }
-      } else {
-#pragma unroll
-        for (int t = 0; t < NT; t++) {
-          if (t < ntok) {
-            const int slot = P->slot[u][t];
-            *reinterpret_cast<f32x2*>(xw + t * 128 + 2 * lane) =
-                *reinterpret_cast<const f32x2*>(a.x_f32 + (int64_t)slot * a.in_f + blk * 128 + 2 * lane);
-          }
-        }
-      }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    };
-    auto process = [&](const u32x4 v, int tk) {
-      if (tk == tk0 || (tk & 7) == 0) stage_block(tk);
-      const uint32_t prior0 = (uint32_t)__shfl((int)v.w, src_lane, 64);
-      const uint32_t W[4] = {v.x, v.y, v.z, v.w};
-      const uint32_t Pw[4] = {prior0, v.x, v.y, v.z};
-      const float* xrow = xw + (tk & 7) * 16;
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        // word i covers rows 2i, 2i+1 (slots 0,1 / 4,5) and 2i+8, 2i+9 (slots 2,3 / 6,7)
-        float f[8];
-        decode_word<ALU>(W[i], Pw[i], tab, f);
-#pragma unroll
-        for (int t = 0; t < NT; t++) {
-          if (t < ntok) {
-            const f32x2 xa = *reinterpret_cast<const f32x2*>(xrow + t * 128 + 2 * i);
-            const f32x2 xb = *reinterpret_cast<const f32x2*>(xrow + t * 128 + 2 * i + 8);
-            acc[t][0] = fmaf(xa.x, f[0], acc[t][0]);
-            acc[t][0] = fmaf(xa.y, f[1], acc[t][0]);
-            acc[t][0] = fmaf(xb.x, f[2], acc[t][0]);
-            acc[t][0] = fmaf(xb.y, f[3], acc[t][0]);
-            acc[t][1] = fmaf(xa.x, f[4], acc[t][1]);
-            acc[t][1] = fmaf(xa.y, f[5], acc[t][1]);
-            acc[t][1] = fmaf(xb.x, f[6], acc[t][1]);
-            acc[t][1] = fmaf(xb.y, f[7], acc[t][1]);
-          }
-        }
-      }
-    };
-
-    // software pipeline: a ring of PF chunk loads in flight ahead of the one being decoded
-    u32x4 ring[PF];
-#pragma unroll
-    for (int d = 0; d < PF; d++)
-      if (tk0 + d < tk1) ring[d] = *chunk_ptr(tk0 + d);
-    for (int tk = tk0; tk < tk1; tk += PF) {
-#pragma unroll
-      for (int d = 0; d < PF; d++) {
-        if (tk + d < tk1) {
-          const u32x4 v = ring[d];
-          if (tk + d + PF < tk1) ring[d] = *chunk_ptr(tk + d + PF);
-          process(v, tk + d);
-        }
-      }
-    }
-
-    // partials of this visit
-    float* pw = a.partial + ((int64_t)wave * 2 + visit) * kPartialStride;
-    const int c0 = col_acc0(lane);
-#pragma unroll
-    for (int t = 0; t < NT; t++) {
-      if (t < ntok) {
-        store_coherent(pw + t * 128 + c0, acc[t][0]);
-        store_coherent(pw + t * 128 + c0 + 8, acc[t][1]);
-      }
-    }
-    complete_visit<FM>(a, P, seg, tk1 - tk0, it, n, nw, nproj, U, u, ob, e, ntok);
-    c += tk1 - tk0;
-  }
-}
-
 // ============================================================== MFMA decode GEMV
 //
-// Same work split as k4_gemv_kernel, but in quads of 4 chunks and with the accumulation on the
-// matrix cores (v_mfma_f32_16x16x32_f16), so the vector ALUs only decode.
+// Work split: the (unit, output block, projection, quad) space is flattened and cut into one
+// static contiguous range per wave; a segment is the run of quads of one (unit, output block,
+// projection).  A quad is 4 chunks (64 input rows x 128 output columns).  The accumulation runs on
+// the matrix cores (v_mfma_f32_16x16x32_f16), so the vector ALUs only decode.
 //
 //   * Lane l = 16g + n loads, for each of 4 sets s, the 16 B piece (tile 2s + n/8, word group n%8)
 //     of chunk tk+g: 4 words = all 16 rows of output columns q = n%8 and q+8 of that tile.
-//   * A word's 8 codewords become two fp8 dwords (c0,c1,c4,c5) and (c2,c3,c6,c7) -- by LDS table
-//     lookup or arithmetic decode -- and four f16 pairs.  Two words of a piece form one B
+//   * A word's 8 codewords become four fp16 pairs (c0,c1), (c2,c3), (c4,c5), (c6,c7) -- by LDS
+//     table lookup or arithmetic decode (decode_word_f16).  Two words of a piece form one B
 //     fragment (8 rows x 1 column) per output-column half h and row half rh, so a piece feeds
 //     4 MFMAs; the 4 k-groups of the MFMA are the 4 chunks of the quad.
 //   * A = x split into fp16 rows hi = f16(x) and lo = f16((x - hi) * 2^11) (x to ~22 bits), rows 2t
@@ -469,69 +395,10 @@ __global__ __launch_bounds__(kThreads) void k4_gemv_kernel(GemvArgs a) {
 //   * D[2t] + 2^-11 * D[2t+1] gives token t's fp32 dot products.
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
-__device__ __forceinline__ f16x2 pair_sums(uint32_t v) {  // v = cw_lo | cw_hi << 16
-  const f16x2 ha = __builtin_bit_cast(f16x2, mcg_halves(v & 0xFFFFu));
-  const f16x2 hb = __builtin_bit_cast(f16x2, mcg_halves(v >> 16));
-  f16x2 s;
-  s.x = ha.x + ha.y;
-  s.y = hb.x + hb.y;
-  return s;
-}
-__device__ __forceinline__ uint32_t fp8_pair_into(uint32_t old, f16x2 sums, bool hi_word) {
-  const i16x2 o = __builtin_bit_cast(i16x2, old);
-  return __builtin_bit_cast(uint32_t, hi_word ? __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(o, sums, 1.0f, true)
-                                              : __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(o, sums, 1.0f, false));
-}
-__device__ __forceinline__ uint32_t lds_pair(const uint8_t* tab, uint32_t a, uint32_t b) {
-  return (uint32_t)tab[a] | ((uint32_t)tab[b] << 16);  // bytes [tab[a], 0, tab[b], 0]
-}
-
-// One word -> ea = fp8 bytes (c0, c1, c4, c5), eb = (c2, c3, c6, c7).  ALU pairs are taken in the
-// order (7,3), (6,2), (5,1), (4,0); the others are looked up.
-template <int ALU>
-__device__ __forceinline__ void decode_word_fp8(uint32_t w, uint32_t p, const uint8_t* tab, uint32_t& ea,
-                                                uint32_t& eb) {
-  const uint32_t a4 = __builtin_amdgcn_alignbit(p, w, 4);    // c6 | c2 << 16
-  const uint32_t a8 = __builtin_amdgcn_alignbit(p, w, 8);    // c5 | c1 << 16
-  const uint32_t a12 = __builtin_amdgcn_alignbit(p, w, 12);  // c4 | c0 << 16
-  // eb from pairs (7,3) = w and (6,2) = a4
-  if (ALU >= 2) {
-    uint32_t d = fp8_pair_into(0u, pair_sums(a4), false);   // [c6, c2, -, -]
-    d = fp8_pair_into(d, pair_sums(w), true);                // [c6, c2, c7, c3]
-    eb = __builtin_amdgcn_perm(d, d, 0x02000301u);           // [c2, c3, c6, c7]
-  } else if (ALU == 1) {
-    const uint32_t d = fp8_pair_into(0u, pair_sums(w), true);  // [-, -, c7, c3]
-    const uint32_t v = lds_pair(tab, a4 & 0xFFFFu, a4 >> 16);  // [c6, 0, c2, 0]
-    eb = __builtin_amdgcn_perm(d, v, 0x06000702u);             // [c2, c3, c6, c7]
-  } else {
-    const uint32_t v23 = lds_pair(tab, a4 >> 16, w >> 16);       // [c2, 0, c3, 0]
-    const uint32_t v67 = lds_pair(tab, a4 & 0xFFFFu, w & 0xFFFFu); // [c6, 0, c7, 0]
-    eb = __builtin_amdgcn_perm(v67, v23, 0x06040200u);
-  }
-  // ea from pairs (5,1) = a8 and (4,0) = a12
-  if (ALU >= 4) {
-    uint32_t d = fp8_pair_into(0u, pair_sums(a12), false);  // [c4, c0, -, -]
-    d = fp8_pair_into(d, pair_sums(a8), true);               // [c4, c0, c5, c1]
-    ea = __builtin_amdgcn_perm(d, d, 0x02000301u);           // [c0, c1, c4, c5]
-  } else if (ALU == 3) {
-    const uint32_t d = fp8_pair_into(0u, pair_sums(a8), true);    // [-, -, c5, c1]
-    const uint32_t v = lds_pair(tab, a12 & 0xFFFFu, a12 >> 16);   // [c4, 0, c0, 0]
-    ea = __builtin_amdgcn_perm(d, v, 0x06000702u);
-  } else {
-    const uint32_t v01 = lds_pair(tab, a12 >> 16, a8 >> 16);          // [c0, 0, c1, 0]
-    const uint32_t v45 = lds_pair(tab, a12 & 0xFFFFu, a8 & 0xFFFFu);  // [c4, 0, c5, 0]
-    ea = __builtin_amdgcn_perm(v45, v01, 0x06040200u);
-  }
-}
-
-__device__ __forceinline__ f16x2 fp8x2_to_f16(uint32_t e, bool hi_word) {
-  return hi_word ? __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(e, 1.0f, true)
-                 : __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(e, 1.0f, false);
-}
 __device__ __forceinline__ f16x8 frag(f16x2 a, f16x2 b, f16x2 c, f16x2 d) {
-  f16x8 r;
-  r[0] = a.x; r[1] = a.y; r[2] = b.x; r[3] = b.y; r[4] = c.x; r[5] = c.y; r[6] = d.x; r[7] = d.y;
-  return r;
+  typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+  const f16x4 ab = __builtin_shufflevector(a, b, 0, 1, 2, 3), cd = __builtin_shufflevector(c, d, 0, 1, 2, 3);
+  return __builtin_shufflevector(ab, cd, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
 // block element r (row within a 16-row tile) -> (row half, position inside the 8-wide k group)
@@ -556,11 +423,13 @@ __global__ __launch_bounds__(WV * 64) void k4_mfma_kernel(GemvArgs a) {
   const int64_t nseg = (int64_t)U * obs * nproj;
   const int64_t nq = nseg * ups;
   const int nw = gridDim.x * WV;
-  const int wave = blockIdx.x * WV + wave_id_in_block();
+  const int wave = blockIdx.x * WV + wave_id_uniform();
   const int lane = lane_id();
   const int g = lane >> 4, nn = lane & 15;
   const int64_t q_begin = range_start(nq, wave, nw), q_end = range_start(nq, wave + 1, nw);
-  _Float16* xw = xa + wave_id_in_block() * (2 * 2 * (2 * NT) * 4 * 8);
+  _Float16* xw = xa + wave_id_uniform() * (2 * 2 * (2 * NT) * 4 * 8);
+  // this lane's 16 B inside a chunk: tile 2s + n/8 at +256 s, word group n%8
+  const int lane_off = (nn >> 3) * 128 + (nn & 7) * 16;
   const int src_lane = (lane & 7) == 0 ? lane + 7 : lane - 1;
 
   int visit = 0;
@@ -575,46 +444,66 @@ __global__ __launch_bounds__(WV * 64) void k4_mfma_kernel(GemvArgs a) {
     const int ntok = P->ntok[u];
     const uint8_t* __restrict__ base = a.packed[proj];
 
-    // MFMA chains restart from zero every MOE_K4_CHAIN quads and are folded into an fp32
-    // (round-to-nearest) VALU accumulator, bounding the accumulation error inside the matrix cores
-    f32x4 acc[4][2], tot[4][2];
+    f32x4 acc[4][2];
 #pragma unroll
     for (int s4 = 0; s4 < 4; s4++)
 #pragma unroll
-      for (int h = 0; h < 2; h++) {
-        acc[s4][h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        tot[s4][h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      }
+      for (int h = 0; h < 2; h++) acc[s4][h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    auto piece_ptr = [&](int tq, int s4) {
-      const int tk = 4 * tq + g;
-      return reinterpret_cast<const u32x4*>(base + chunk_offset(a.side, e, ob, tk, it, obs) +
-                                            (2 * s4 + (nn >> 3)) * 128 + (nn & 7) * 16);
+    // the lane's piece of set s4 in quad tq is at quad_ptr(tq) + 256 * s4
+    auto quad_ptr = [&](int tq) {
+      return base + chunk_offset(a.side, e, ob, 4 * tq + g, it, obs) + lane_off;
     };
-    auto stage_block = [&](int blk) {
-      // xh of rows [128*blk, +128) for every token of the unit -> fp16 hi/lo A fragments
-      float v0[NT], v1[NT];
-      if (IM == IN_PREP) {
-        const uint16_t* __restrict__ sc = a.in_scale[proj] + (int64_t)e * a.in_f + blk * 128 + 2 * lane;
-        const float s0 = f16_to_f32(sc[0]), s1 = f16_to_f32(sc[1]);
+    auto load_quad = [&](u32x4(&pc)[4], int tq) {
+      const uint8_t* qp = quad_ptr(tq);
 #pragma unroll
-        for (int t = 0; t < NT; t++) {
-          if (t < ntok) {
-            const int row = a.x_per_slot ? P->slot[u][t] : P->tok[u][t];
-            const uint16_t* __restrict__ xr = a.x_bf16 + (int64_t)row * a.in_f + blk * 128 + 2 * lane;
-            v0[t] = bf16_to_f32(xr[0]) * s0;
-            v1[t] = bf16_to_f32(xr[1]) * s1;
-            hadamard128_wave(v0[t], v1[t]);
-          }
-        }
+      for (int s4 = 0; s4 < 4; s4++) pc[s4] = *reinterpret_cast<const u32x4*>(qp + 256 * s4);
+    };
+    // x of one 128-row block for every token of the unit is fetched one block ahead of its use
+    // (raw words in registers) and turned into A fragments when its block starts.
+    // (unconditional loads -- positions past the unit's tokens re-read its last token -- so the
+    // compiler can count them against the piece loads instead of draining the queue)
+    uint32_t nx[NT], nsc = 0;
+    f32x2 nxd[NT];
+    // source rows of the unit's token positions (positions past ntok repeat the last token),
+    // fixed for the visit and kept in scalar registers
+    const uint16_t* xrow[NT];
+    const float* xrowd[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      const int tt = min(t, ntok - 1);
+      if (IM == IN_PREP) {
+        const int row = __builtin_amdgcn_readfirstlane(a.x_per_slot ? P->slot[u][tt] : P->tok[u][tt]);
+        xrow[t] = a.x_bf16 + (int64_t)row * a.in_f + 2 * lane;
+      } else {
+        const int slot = __builtin_amdgcn_readfirstlane(P->slot[u][tt]);
+        xrowd[t] = a.x_f32 + (int64_t)slot * a.in_f + 2 * lane;
+      }
+    }
+    const uint16_t* scrow = IM == IN_PREP ? a.in_scale[proj] + (int64_t)e * a.in_f + 2 * lane : nullptr;
+    auto fetch_block = [&](int blk) {
+      if (IM == IN_PREP) {
+        nsc = *reinterpret_cast<const uint32_t*>(scrow + blk * 128);
+#pragma unroll
+        for (int t = 0; t < NT; t++) nx[t] = *reinterpret_cast<const uint32_t*>(xrow[t] + blk * 128);
       } else {
 #pragma unroll
-        for (int t = 0; t < NT; t++) {
-          if (t < ntok) {
-            const int slot = P->slot[u][t];
-            const f32x2 xv = *reinterpret_cast<const f32x2*>(a.x_f32 + (int64_t)slot * a.in_f + blk * 128 + 2 * lane);
-            v0[t] = xv.x;
-            v1[t] = xv.y;
+        for (int t = 0; t < NT; t++) nxd[t] = *reinterpret_cast<const f32x2*>(xrowd[t] + blk * 128);
+      }
+    };
+    auto stage_block = [&]() {
+      // fetched block -> xh -> fp16 hi/lo A fragments in the wave's LDS slice
+      float v0[NT], v1[NT];
+#pragma unroll
+      for (int t = 0; t < NT; t++) {
+        if (t < ntok) {
+          if (IM == IN_PREP) {
+            v0[t] = bf16_to_f32((uint16_t)(nx[t] & 0xFFFFu)) * f16_to_f32((uint16_t)(nsc & 0xFFFFu));
+            v1[t] = bf16_to_f32((uint16_t)(nx[t] >> 16)) * f16_to_f32((uint16_t)(nsc >> 16));
+            hadamard128_wave(v0[t], v1[t]);
+          } else {
+            v0[t] = nxd[t].x;
+            v1[t] = nxd[t].y;
           }
         }
       }
@@ -644,12 +533,18 @@ __global__ __launch_bounds__(WV * 64) void k4_mfma_kernel(GemvArgs a) {
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     };
 
-    // each piece's register slot is refilled with the next quad's piece as soon as it is decoded
-    u32x4 cur[4];
-#pragma unroll
-    for (int s4 = 0; s4 < 4; s4++) cur[s4] = *piece_ptr(tq0, s4);
+    // One quad in flight per wave (with enough waves per CU this keeps HBM busy): each piece's
+    // registers are refilled with the next quad's piece once the piece has been decoded.  The
+    // last quad re-reads itself (a cache hit), so the prefetch needs no branch.
+    const int tl = tq1 - 1;
+    u32x4 pc[4];
+    load_quad(pc, tq0);
+    fetch_block(tq0 >> 1);
     for (int tq = tq0; tq < tq1; tq++) {
-      if (tq == tq0 || (tq & 1) == 0) stage_block(tq >> 1);
+      if (tq == tq0 || (tq & 1) == 0) {
+        stage_block();
+        fetch_block(min((tq >> 1) + 1, tl >> 1));
+      }
       f16x8 A[2];
       const int m = nn;
       const bool live = m < 2 * ntok;
@@ -658,43 +553,30 @@ __global__ __launch_bounds__(WV * 64) void k4_mfma_kernel(GemvArgs a) {
         A[rh] = live ? *reinterpret_cast<const f16x8*>(xw + ((((tq & 1) * 2 + rh) * (2 * NT) + m) * 4 + g) * 8)
                      : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
       }
+      const uint8_t* np = quad_ptr(min(tq + 1, tl));
+      // predecessors of the pieces' first words (last word of the lane before, within the tile),
+      // fetched for the whole quad at once
+      uint32_t prior[4];
+#pragma unroll
+      for (int s4 = 0; s4 < 4; s4++) prior[s4] = (uint32_t)__shfl((int)pc[s4].w, src_lane, 64);
 #pragma unroll
       for (int s4 = 0; s4 < 4; s4++) {
-        const u32x4 v = cur[s4];
-        if (tq + 1 < tq1) cur[s4] = *piece_ptr(tq + 1, s4);
-        const uint32_t prior0 = (uint32_t)__shfl((int)v.w, src_lane, 64);
-        uint32_t ea[4], eb[4];
-        decode_word_fp8<ALU_EVEN>(v.x, prior0, tab, ea[0], eb[0]);
-        decode_word_fp8<ALU_ODD>(v.y, v.x, tab, ea[1], eb[1]);
-        decode_word_fp8<ALU_EVEN>(v.z, v.y, tab, ea[2], eb[2]);
-        decode_word_fp8<ALU_ODD>(v.w, v.z, tab, ea[3], eb[3]);
+        const u32x4 v = pc[s4];
 #pragma unroll
         for (int rh = 0; rh < 2; rh++) {
-          const int w0 = 2 * rh, w1 = 2 * rh + 1;
-          // h = 0: slots (0,1),(2,3) ; h = 1: slots (4,5),(6,7) of words w0, w1
-          const f16x8 b0 = frag(fp8x2_to_f16(ea[w0], false), fp8x2_to_f16(eb[w0], false),
-                                fp8x2_to_f16(ea[w1], false), fp8x2_to_f16(eb[w1], false));
-          const f16x8 b1 = frag(fp8x2_to_f16(ea[w0], true), fp8x2_to_f16(eb[w0], true),
-                                fp8x2_to_f16(ea[w1], true), fp8x2_to_f16(eb[w1], true));
+          // words 2rh, 2rh+1 = rows of row half rh; h = 0: slots (0,1),(2,3) ; h = 1: slots (4,5),(6,7)
+          f16x2 q[2][4];  // [word][pair]: (c0,c1), (c2,c3), (c4,c5), (c6,c7)
+          if (rh == 0)
+            decode_pair_words_f16<ALU_EVEN, ALU_ODD>(v.x, v.y, prior[s4], tab, q);
+          else
+            decode_pair_words_f16<ALU_EVEN, ALU_ODD>(v.z, v.w, v.y, tab, q);
+          if (rh == 1) pc[s4] = *reinterpret_cast<const u32x4*>(np + 256 * s4);
+          const f16x8 b0 = frag(q[0][0], q[0][1], q[1][0], q[1][1]);
+          const f16x8 b1 = frag(q[0][2], q[0][3], q[1][2], q[1][3]);
           acc[s4][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[rh], b0, acc[s4][0], 0, 0, 0);
           acc[s4][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[rh], b1, acc[s4][1], 0, 0, 0);
         }
       }
-      if (MOE_K4_CHAIN > 0 && ((tq - tq0 + 1) % (MOE_K4_CHAIN > 0 ? MOE_K4_CHAIN : 1) == 0 || tq + 1 == tq1)) {
-#pragma unroll
-        for (int s4 = 0; s4 < 4; s4++)
-#pragma unroll
-          for (int h = 0; h < 2; h++) {
-            tot[s4][h] += acc[s4][h];
-            acc[s4][h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-          }
-      }
-    }
-    if (MOE_K4_CHAIN == 0) {
-#pragma unroll
-      for (int s4 = 0; s4 < 4; s4++)
-#pragma unroll
-        for (int h = 0; h < 2; h++) tot[s4][h] = acc[s4][h];
     }
 
     // partials of this visit: token t = D rows 2t + 2t+1, held by lanes 16*(t/2) + n, regs 2(t%2), +1
@@ -708,7 +590,7 @@ __global__ __launch_bounds__(WV * 64) void k4_mfma_kernel(GemvArgs a) {
 #pragma unroll
           for (int h = 0; h < 2; h++) {
             const int col = 16 * (2 * s4 + (nn >> 3)) + (nn & 7) + 8 * h;
-            store_coherent(pw + t * 128 + col, fmaf(tot[s4][h][r0 + 1], 1.0f / 2048.0f, tot[s4][h][r0]));
+            store_coherent(pw + t * 128 + col, fmaf(acc[s4][h][r0 + 1], 1.0f / 2048.0f, acc[s4][h][r0]));
           }
       }
     }
@@ -778,7 +660,6 @@ struct Workspace {
   int32_t* counter_grp; // per-group segment counters (self-cleaning)
   int32_t* router_counter;
   float* partial;       // [kMaxWaves][2][kPartialStride]
-  float* segbuf;        // [kMaxWaves segments][kMaxRows][128]
   float* yslot;         // [kMaxUnits][hidden]
   float* down_xh;       // [kMaxUnits][inter]
   float* logits;        // [kMaxRows][256]
@@ -801,7 +682,6 @@ Workspace carve(void* base, int hidden, int inter) {
   w.counter_grp = reinterpret_cast<int32_t*>(take(kCounters * 4));
   w.router_counter = reinterpret_cast<int32_t*>(take(256));
   w.partial = reinterpret_cast<float*>(take((size_t)kMaxWaves * 2 * kPartialStride * 4));
-  w.segbuf = reinterpret_cast<float*>(take((size_t)kMaxWaves * kMaxRows * 128 * 4));
   w.yslot = reinterpret_cast<float*>(take((size_t)kMaxUnits * hidden * 4));
   w.down_xh = reinterpret_cast<float*>(take((size_t)kMaxUnits * inter * 4));
   w.logits = reinterpret_cast<float*>(take((size_t)kMaxRows * 256 * 4));
@@ -823,33 +703,22 @@ int launch_gemv(const GemvArgs& a, int max_ntok, int max_units, hipStream_t stre
   const int64_t nseg_max = (int64_t)max_units * (a.out_f / 128) * a.nproj;
   if (nseg_max > kMaxWaves)
     return fail(MOE_ENOTSUP, "too many (unit, column block) segments: %lld > %d", (long long)nseg_max, kMaxWaves);
-  int blocks = grid_blocks();
-  const int need = (int)((nseg_max + kWaves - 1) / kWaves);
-  if (blocks < need) blocks = need;
-  const dim3 grid(blocks), block(kThreads);
-#if MOE_K4_MFMA
   {
-    constexpr int WV = MOE_K4_MFMA_WAVES;
-    int mblocks = grid_blocks();
+    const int WV = max_ntok <= 1 ? MOE_K4_WAVES_1 : MOE_K4_WAVES_8;
+    // 16 waves per CU (4 per SIMD: the decode's VALU results arrive 16 clocks after issue)
+    int mblocks = grid_blocks() * (WV < 16 ? 16 / WV : 1);
+    // at least one wave per segment, so no wave's range spans more than two segments
     const int mneed = (int)((nseg_max + WV - 1) / WV);
     if (mblocks < mneed) mblocks = mneed;
     if (mblocks * WV > kMaxWaves)
       return fail(MOE_ENOTSUP, "too many waves for the partial buffer (%d)", mblocks * WV);
     if (max_ntok <= 1)
-      hipLaunchKernelGGL((k4_mfma_kernel<IM, FM, 1, MOE_K4_ALU_EVEN, MOE_K4_ALU_ODD, WV>), dim3(mblocks), dim3(WV * 64),
-                         0, stream, a);
-    else
-      hipLaunchKernelGGL((k4_mfma_kernel<IM, FM, kMaxRows, MOE_K4_ALU_EVEN, MOE_K4_ALU_ODD, WV>), dim3(mblocks),
+      hipLaunchKernelGGL((k4_mfma_kernel<IM, FM, 1, MOE_K4_ALU_EVEN_1, MOE_K4_ALU_ODD_1, MOE_K4_WAVES_1>), dim3(mblocks),
                          dim3(WV * 64), 0, stream, a);
+    else
+      hipLaunchKernelGGL((k4_mfma_kernel<IM, FM, kMaxRows, MOE_K4_ALU_EVEN_8, MOE_K4_ALU_ODD_8, MOE_K4_WAVES_8>),
+                         dim3(mblocks), dim3(WV * 64), 0, stream, a);
   }
-  (void)grid;
-  (void)block;
-#else
-  if (max_ntok <= 1)
-    hipLaunchKernelGGL((k4_gemv_kernel<IM, FM, 1, MOE_K4_ALU_PAIRS, MOE_K4_PREFETCH>), grid, block, 0, stream, a);
-  else
-    hipLaunchKernelGGL((k4_gemv_kernel<IM, FM, kMaxRows, MOE_K4_ALU_PAIRS, MOE_K4_PREFETCH>), grid, block, 0, stream, a);
-#endif
   MOE_HIP(hipGetLastError());
   return MOE_OK;
 }
@@ -908,8 +777,8 @@ int moe_trellis_decode_f16(const void* packed, int64_t packed_bytes, int k, int 
           (long long)experts);
   rc = ensure_device_ready();
   if (rc) return rc;
-  const int64_t total = (int64_t)in_f * out_f;
-  hipLaunchKernelGGL(trellis_decode_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+  const int64_t pieces = (int64_t)in_f * out_f / 32;
+  hipLaunchKernelGGL(trellis_decode_kernel, dim3((unsigned)((pieces + 1023) / 1024)), dim3(1024), 0,
                      (hipStream_t)stream, (const uint32_t*)packed, in_f, out_f, side, expert, inner);
   MOE_HIP(hipGetLastError());
   return MOE_OK;
@@ -991,7 +860,6 @@ static int k4_mlp_common(const uint16_t* x, const uint32_t* ids, const float* sc
   g.partial = w.partial;
   g.counter_seg = w.counter_seg;
   g.counter_grp = w.counter_grp;
-  g.segbuf = w.segbuf;
   g.out_scale[0] = out_g; g.out_scale[1] = out_u;
   g.in_down = in_d;
   g.down_xh = w.down_xh;

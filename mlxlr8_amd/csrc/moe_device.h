@@ -72,30 +72,278 @@ __device__ __forceinline__ void load_codebook_lds(uint8_t* lds) {
   for (int i = threadIdx.x; i < 65536 / 16; i += blockDim.x) dst[i] = src[i];
 }
 
-// ---------------------------------------------------------------- K4 word decode
+// ---------------------------------------------------------------- K4 word layout
 // Word w of a tile with its circular predecessor p holds 8 codewords (A.1 direct form):
 //   slot 0..2 straddle p and w, slot 3..7 lie inside w.
 // Slot s sits at tile row (lane%4)*2 + (s&1) + (s&2)*4 and column lane/4 + (s&4)*2.
-// ALU_PAIRS selects how many codeword pairs are decoded arithmetically; the rest are
-// looked up in the LDS table.  Pairs in ALU preference order: (7,3), (6,2), (5,1), (4,0).
-template <int ALU_PAIRS>
-__device__ __forceinline__ void decode_word(uint32_t w, uint32_t p, const uint8_t* tab, float f[8]) {
-  const uint32_t a4 = __builtin_amdgcn_alignbit(p, w, 4);   // (slot6 | slot2 << 16)
-  const uint32_t a8 = __builtin_amdgcn_alignbit(p, w, 8);   // (slot5 | slot1 << 16)
-  const uint32_t a12 = __builtin_amdgcn_alignbit(p, w, 12); // (slot4 | slot0 << 16)
-  const uint32_t pairs[4] = {w, a4, a8, a12};
-  const int lo_slot[4] = {7, 6, 5, 4};
+
+// ---------------------------------------------------------------- K4 word -> fp16 MFMA operands
+// The same word decode, producing the weights as fp16 pairs ready for a B fragment of
+// v_mfma_f32_16x16x32_f16: q01 = (c0, c1), q23 = (c2, c3), q45 = (c4, c5), q67 = (c6, c7), where cs
+// is the codeword of slot s.  Slots 0-3 are column lane/4 and slots 4-7 column lane/4 + 8 of the
+// tile (rows as above), so each pair is two rows of one column.
+//
+// Arithmetic route, per codeword in half H of a register r (about 5 VALU ops):
+//   t = (cw * 0xCBAC mod 2^16) << 16        one SDWA multiply reading the half directly
+//   p = cw * 0x1FED + t = cw * 0xCBAC1FED   one v_mad_u32_u16 selecting the half
+//   m = (p & 0x8FFF8FFF) ^ 0x3B603B60       one v_bitop3
+//   f16(m.lo) + f16(m.hi)                   one SDWA fp16 add written into its half of the pair
+// then E4M3 rounding by a round trip through the hardware fp8 conversions (two per pair).
+// Table route: the E4M3 byte is read from LDS (one address op per codeword), two lookups meet in
+// one register as [b0, 0, b1, 0], a byte permute joins two such pairs and two conversions widen
+// them to fp16.  The split between routes is NALU arithmetic pairs per word (0..4), taken in the
+// order q67, q23, q45, q01.
+template <int H>
+__device__ __forceinline__ uint32_t mcg_product_half(uint32_t r, uint32_t k_hi, uint32_t k_lo) {
+  uint32_t t, p;
+  asm("v_mul_u32_u24_sdwa %0, %1, %2 dst_sel:WORD_1 dst_unused:UNUSED_PAD src0_sel:WORD_%3 src1_sel:DWORD"
+      : "=v"(t)
+      : "v"(r), "s"(k_hi), "n"(H));
+  asm("v_mad_u32_u16 %0, %1, %2, %3 op_sel:[%4,0,0,0]" : "=v"(p) : "v"(r), "s"(k_lo), "v"(t), "n"(H));
+  return p;
+}
+// f16 pair (cw_x, cw_y) for codewords in half HX of rx and half HY of ry, before E4M3 rounding
+template <int HX, int HY>
+__device__ __forceinline__ uint32_t halves_sum_pair(uint32_t rx, uint32_t ry) {
+  const uint32_t k_hi = 0xCBACu, k_lo = 0x1FEDu;
+  const uint32_t mx = (mcg_product_half<HX>(rx, k_hi, k_lo) & 0x8FFF8FFFu) ^ 0x3B603B60u;
+  const uint32_t my = (mcg_product_half<HY>(ry, k_hi, k_lo) & 0x8FFF8FFFu) ^ 0x3B603B60u;
+  uint32_t s;
+  asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1"
+      : "=v"(s)
+      : "v"(mx));
+  asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1"
+      : "+v"(s)
+      : "v"(my));
+  return s;
+}
+// An unconstrained register value: the fp8 conversions below write one half of their destination
+// and keep the other, so the first one into a fresh register is given this instead of a zero
+// (which would cost a copy).
+__device__ __forceinline__ uint32_t scratch_reg() {
+  uint32_t r;
+  asm volatile("" : "=v"(r));
+  return r;
+}
+__device__ __forceinline__ i16x2 as_i16x2(uint32_t v) { return __builtin_bit_cast(i16x2, v); }
+// E4M3 rounding of one or two f16 pairs (round trip through fp8)
+__device__ __forceinline__ f16x2 round_e4m3_pair(uint32_t s) {
+  const uint32_t e = __builtin_bit_cast(
+      uint32_t, __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(as_i16x2(scratch_reg()), __builtin_bit_cast(f16x2, s), 1.0f, false));
+  return __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(e, 1.0f, false);
+}
+__device__ __forceinline__ void round_e4m3_two(uint32_t sa, uint32_t sb, f16x2& fa, f16x2& fb) {
+  i16x2 e = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(as_i16x2(scratch_reg()), __builtin_bit_cast(f16x2, sa), 1.0f, false);
+  e = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(e, __builtin_bit_cast(f16x2, sb), 1.0f, true);
+  fa = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(__builtin_bit_cast(uint32_t, e), 1.0f, false);
+  fb = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(__builtin_bit_cast(uint32_t, e), 1.0f, true);
+}
+template <int H>
+__device__ __forceinline__ uint32_t half_of(uint32_t r) {
+  return H ? (r >> 16) : (r & 0xFFFFu);
+}
+// [tab[x], 0, tab[y], 0]
+template <int HX, int HY>
+__device__ __forceinline__ uint32_t lds_pair_bytes(const uint8_t* tab, uint32_t rx, uint32_t ry) {
+  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+  u16x2 r;
+  r.x = tab[half_of<HX>(rx)];
+  r.y = tab[half_of<HY>(ry)];
+  return __builtin_bit_cast(uint32_t, r);
+}
+__device__ __forceinline__ void widen_two(uint32_t qa, uint32_t qb, f16x2& fa, f16x2& fb) {
+  const uint32_t e = __builtin_amdgcn_perm(qb, qa, 0x06040200u);  // [qa.b0, qa.b2, qb.b0, qb.b2]
+  fa = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(e, 1.0f, false);
+  fb = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(e, 1.0f, true);
+}
+__device__ __forceinline__ f16x2 widen_one(uint32_t q) {
+  return __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(__builtin_amdgcn_perm(q, q, 0x00000200u), 1.0f, false);
+}
+
+template <int NALU>
+__device__ __forceinline__ void decode_word_f16(uint32_t w, uint32_t p, const uint8_t* tab, f16x2& q01, f16x2& q23,
+                                                f16x2& q45, f16x2& q67) {
+  const uint32_t a4 = __builtin_amdgcn_alignbit(p, w, 4);    // c6 | c2 << 16
+  const uint32_t a8 = __builtin_amdgcn_alignbit(p, w, 8);    // c5 | c1 << 16
+  const uint32_t a12 = __builtin_amdgcn_alignbit(p, w, 12);  // c4 | c0 << 16
+  // pairs: q01 = (a12.hi, a8.hi), q23 = (a4.hi, w.hi), q45 = (a12.lo, a8.lo), q67 = (a4.lo, w.lo)
+  if (NALU == 1) q67 = round_e4m3_pair(halves_sum_pair<0, 0>(a4, w));
+  if (NALU >= 2) round_e4m3_two(halves_sum_pair<0, 0>(a4, w), halves_sum_pair<1, 1>(a4, w), q67, q23);
+  if (NALU == 3) q45 = round_e4m3_pair(halves_sum_pair<0, 0>(a12, a8));
+  if (NALU == 4) round_e4m3_two(halves_sum_pair<0, 0>(a12, a8), halves_sum_pair<1, 1>(a12, a8), q45, q01);
+  if (NALU == 0) {
+    widen_two(lds_pair_bytes<0, 0>(tab, a4, w), lds_pair_bytes<1, 1>(tab, a4, w), q67, q23);
+    widen_two(lds_pair_bytes<0, 0>(tab, a12, a8), lds_pair_bytes<1, 1>(tab, a12, a8), q45, q01);
+  } else if (NALU == 1) {
+    widen_two(lds_pair_bytes<1, 1>(tab, a4, w), lds_pair_bytes<0, 0>(tab, a12, a8), q23, q45);
+    q01 = widen_one(lds_pair_bytes<1, 1>(tab, a12, a8));
+  } else if (NALU == 2) {
+    widen_two(lds_pair_bytes<0, 0>(tab, a12, a8), lds_pair_bytes<1, 1>(tab, a12, a8), q45, q01);
+  } else if (NALU == 3) {
+    q01 = widen_one(lds_pair_bytes<1, 1>(tab, a12, a8));
+  }
+}
+
+// ---------------------------------------------------------------- K4 piece -> fp16 MFMA operands
+// Two consecutive words of one lane (w0's predecessor is `prior0`) decoded together, NE arithmetic
+// pairs in w0 and NO in w1.  Every VALU result is needed about 16 clocks after issue, so the
+// arithmetic route runs stage by stage over all of the two words' arithmetic codewords (ordered
+// asm statements): a wave then always has independent work to issue.  q[i][j] receives word i's
+// pair j as in decode_word_f16.
+namespace piece_detail {
+// pair kinds in arithmetic preference order: 0 = (c6,c7) = (a4.lo, w.lo), 1 = (c2,c3) = (a4.hi, w.hi),
+// 2 = (c4,c5) = (a12.lo, a8.lo), 3 = (c0,c1) = (a12.hi, a8.hi); kind k fills q[i][kOut[k]]
+constexpr int kOut[4] = {3, 1, 2, 0};
+}  // namespace piece_detail
+
+template <int H>
+__device__ __forceinline__ uint32_t mul_hi16_shifted(uint32_t r, uint32_t k_hi) {
+  uint32_t t;
+  asm volatile("v_mul_u32_u24_sdwa %0, %1, %2 dst_sel:WORD_1 dst_unused:UNUSED_PAD src0_sel:WORD_%3 src1_sel:DWORD"
+               : "=v"(t)
+               : "v"(r), "s"(k_hi), "n"(H));
+  return t;
+}
+template <int H>
+__device__ __forceinline__ uint32_t mad_lo16(uint32_t r, uint32_t k_lo, uint32_t t) {
+  uint32_t p;
+  asm volatile("v_mad_u32_u16 %0, %1, %2, %3 op_sel:[%4,0,0,0]" : "=v"(p) : "v"(r), "s"(k_lo), "v"(t), "n"(H));
+  return p;
+}
+__device__ __forceinline__ uint32_t add_halves_lo(uint32_t m) {
+  uint32_t s;
+  asm volatile("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1"
+               : "=v"(s)
+               : "v"(m));
+  return s;
+}
+__device__ __forceinline__ void add_halves_hi(uint32_t& s, uint32_t m) {
+  asm volatile("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1"
+               : "+v"(s)
+               : "v"(m));
+}
+
+template <int NE, int NO>
+__device__ __forceinline__ void decode_pair_words_f16(uint32_t w0, uint32_t w1, uint32_t prior0, const uint8_t* tab,
+                                                      f16x2 (&q)[2][4]) {
+  using piece_detail::kOut;
+  const uint32_t w[2] = {w0, w1};
+  const uint32_t pr[2] = {prior0, w0};
+  uint32_t a4[2], a8[2], a12[2];
 #pragma unroll
-  for (int q = 0; q < 4; q++) {
-    const uint32_t v = pairs[q];
-    if (q < ALU_PAIRS) {
-      f32x2 r = decode_pair_alu(v, v >> 16);
-      f[lo_slot[q]] = r.x;
-      f[lo_slot[q] - 4] = r.y;
-    } else {
-      f[lo_slot[q]] = fp8_to_f32(tab[v & 0xFFFFu]);
-      f[lo_slot[q] - 4] = fp8_to_f32(tab[v >> 16]);
-    }
+  for (int i = 0; i < 2; i++) {
+    a4[i] = __builtin_amdgcn_alignbit(pr[i], w[i], 4);
+    a8[i] = __builtin_amdgcn_alignbit(pr[i], w[i], 8);
+    a12[i] = __builtin_amdgcn_alignbit(pr[i], w[i], 12);
+  }
+  auto nalu = [](int i) { return (i & 1) ? NO : NE; };
+  auto xr = [&](int i, int k) { return (k & 2) ? a12[i] : a4[i]; };
+  auto yr = [&](int i, int k) { return (k & 2) ? a8[i] : w[i]; };
+  const uint32_t k_hi = 0xCBACu, k_lo = 0x1FEDu;
+
+  // ---- table route for the pairs with k >= nalu(word): the byte lookups are issued first, and the
+  // scheduling fences keep their use after the arithmetic route, which hides their latency
+  uint32_t bx[2][4], by[2][4];
+#pragma unroll
+  for (int k = 0; k < 4; k++)
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+      if (k >= nalu(i)) {
+        bx[i][k] = tab[(k & 1) ? (xr(i, k) >> 16) : (xr(i, k) & 0xFFFFu)];
+        by[i][k] = tab[(k & 1) ? (yr(i, k) >> 16) : (yr(i, k) & 0xFFFFu)];
+      }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- arithmetic route, stage by stage over all (word, kind) pairs with k < nalu(word)
+  uint32_t tx[2][4], ty[2][4], sm[2][4];
+#pragma unroll
+  for (int k = 0; k < 4; k++)
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+      if (k < nalu(i)) {
+        if (k & 1) {
+          tx[i][k] = mul_hi16_shifted<1>(xr(i, k), k_hi);
+          ty[i][k] = mul_hi16_shifted<1>(yr(i, k), k_hi);
+        } else {
+          tx[i][k] = mul_hi16_shifted<0>(xr(i, k), k_hi);
+          ty[i][k] = mul_hi16_shifted<0>(yr(i, k), k_hi);
+        }
+      }
+#pragma unroll
+  for (int k = 0; k < 4; k++)
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+      if (k < nalu(i)) {
+        if (k & 1) {
+          tx[i][k] = mad_lo16<1>(xr(i, k), k_lo, tx[i][k]);
+          ty[i][k] = mad_lo16<1>(yr(i, k), k_lo, ty[i][k]);
+        } else {
+          tx[i][k] = mad_lo16<0>(xr(i, k), k_lo, tx[i][k]);
+          ty[i][k] = mad_lo16<0>(yr(i, k), k_lo, ty[i][k]);
+        }
+      }
+#pragma unroll
+  for (int k = 0; k < 4; k++)
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+      if (k < nalu(i)) {
+        tx[i][k] = (tx[i][k] & 0x8FFF8FFFu) ^ 0x3B603B60u;
+        ty[i][k] = (ty[i][k] & 0x8FFF8FFFu) ^ 0x3B603B60u;
+      }
+#pragma unroll
+  for (int k = 0; k < 4; k++)
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+      if (k < nalu(i)) sm[i][k] = add_halves_lo(tx[i][k]);
+#pragma unroll
+  for (int k = 0; k < 4; k++)
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+      if (k < nalu(i)) add_halves_hi(sm[i][k], ty[i][k]);
+  // E4M3 rounding: consecutive arithmetic pairs share one fp8 register
+  {
+    int pend_i = -1, pend_k = -1;
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+#pragma unroll
+      for (int i = 0; i < 2; i++)
+        if (k < nalu(i)) {
+          if (pend_i < 0) {
+            pend_i = i;
+            pend_k = k;
+          } else {
+            round_e4m3_two(sm[pend_i][pend_k], sm[i][k], q[pend_i][kOut[pend_k]], q[i][kOut[k]]);
+            pend_i = -1;
+          }
+        }
+    if (pend_i >= 0) q[pend_i][kOut[pend_k]] = round_e4m3_pair(sm[pend_i][pend_k]);
+  }
+
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- table route: [b_x, 0, b_y, 0] per pair, two pairs joined per permute, widened to fp16
+  {
+    uint32_t lb[2][4];
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+#pragma unroll
+      for (int i = 0; i < 2; i++)
+        if (k >= nalu(i)) lb[i][k] = bx[i][k] | (by[i][k] << 16);
+    int pend_i = -1, pend_k = -1;
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+#pragma unroll
+      for (int i = 0; i < 2; i++)
+        if (k >= nalu(i)) {
+          if (pend_i < 0) {
+            pend_i = i;
+            pend_k = k;
+          } else {
+            widen_two(lb[pend_i][pend_k], lb[i][k], q[pend_i][kOut[pend_k]], q[i][kOut[k]]);
+            pend_i = -1;
+          }
+        }
+    if (pend_i >= 0) q[pend_i][kOut[pend_k]] = widen_one(lb[pend_i][pend_k]);
   }
 }
 
@@ -146,5 +394,8 @@ __device__ __forceinline__ float wave_sum(float v) {
 // ---------------------------------------------------------------- small wave helpers
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 __device__ __forceinline__ int wave_id_in_block() { return threadIdx.x >> 6; }
+// The same index as a wave-uniform (scalar) value, so that everything derived from it -- work
+// ranges, loop bounds, segment ids -- lives in scalar registers and loops stay uniform.
+__device__ __forceinline__ int wave_id_uniform() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
 }  // namespace moe

@@ -193,7 +193,9 @@ __global__ __launch_bounds__(64) void route_kernel(const float* __restrict__ log
 
 // Decode batches in one launch: block e computes logit e of every row; the last block to finish
 // routes all rows (one wave per row) and builds the token -> expert dispatch plan.
-template <int R>
+// KI = hidden / 1024 when known at compile time (all loads of a block are then issued before the
+// first multiply, one memory round trip), 0 for any multiple of 1024.
+template <int R, int KI>
 __global__ __launch_bounds__(256) void router_decode_kernel(const uint16_t* __restrict__ x,
                                                             const float* __restrict__ w,
                                                             const float* __restrict__ bias, int rows, int hidden,
@@ -205,17 +207,33 @@ __global__ __launch_bounds__(256) void router_decode_kernel(const uint16_t* __re
   float acc[R];
 #pragma unroll
   for (int r = 0; r < R; r++) acc[r] = 0.0f;
-  for (int k = threadIdx.x * 4; k < hidden; k += 256 * 4) {
-    const f32x4 wv = *reinterpret_cast<const f32x4*>(we + k);
+  auto fma4 = [&](int r, const f32x4& wv, const u32x2& xv) {
+    acc[r] = fmaf(bf16_to_f32((uint16_t)(xv.x & 0xFFFFu)), wv.x, acc[r]);
+    acc[r] = fmaf(bf16_to_f32((uint16_t)(xv.x >> 16)), wv.y, acc[r]);
+    acc[r] = fmaf(bf16_to_f32((uint16_t)(xv.y & 0xFFFFu)), wv.z, acc[r]);
+    acc[r] = fmaf(bf16_to_f32((uint16_t)(xv.y >> 16)), wv.w, acc[r]);
+  };
+  if (KI > 0) {
+    f32x4 wv[KI > 0 ? KI : 1];
+    u32x2 xv[R][KI > 0 ? KI : 1];
 #pragma unroll
-    for (int r = 0; r < R; r++) {
-      if (r < rows) {
-        const u32x2 xv = *reinterpret_cast<const u32x2*>(x + (int64_t)r * hidden + k);
-        acc[r] = fmaf(bf16_to_f32((uint16_t)(xv.x & 0xFFFFu)), wv.x, acc[r]);
-        acc[r] = fmaf(bf16_to_f32((uint16_t)(xv.x >> 16)), wv.y, acc[r]);
-        acc[r] = fmaf(bf16_to_f32((uint16_t)(xv.y & 0xFFFFu)), wv.z, acc[r]);
-        acc[r] = fmaf(bf16_to_f32((uint16_t)(xv.y >> 16)), wv.w, acc[r]);
-      }
+    for (int i = 0; i < KI; i++) wv[i] = *reinterpret_cast<const f32x4*>(we + threadIdx.x * 4 + i * 1024);
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+      for (int i = 0; i < KI; i++)
+        if (r < rows) xv[r][i] = *reinterpret_cast<const u32x2*>(x + (int64_t)r * hidden + threadIdx.x * 4 + i * 1024);
+#pragma unroll
+    for (int i = 0; i < KI; i++)
+#pragma unroll
+      for (int r = 0; r < R; r++)
+        if (r < rows) fma4(r, wv[i], xv[r][i]);
+  } else {
+    for (int k = threadIdx.x * 4; k < hidden; k += 256 * 4) {
+      const f32x4 wv = *reinterpret_cast<const f32x4*>(we + k);
+#pragma unroll
+      for (int r = 0; r < R; r++)
+        if (r < rows) fma4(r, wv, *reinterpret_cast<const u32x2*>(x + (int64_t)r * hidden + k));
     }
   }
   __shared__ float red[R][4];
@@ -269,12 +287,18 @@ int moe_router_fused_plan(const uint16_t* x, const float* w, const float* bias, 
   MOE_ARG(hidden > 0 && hidden % 1024 == 0, "router hidden size must be a positive multiple of 1024");
   MOE_ARG(rows >= 1 && rows <= kMaxRows, "decode routing handles 1..%d rows", kMaxRows);
   const int max_users = rows == 1 ? 1 : kMaxRows;
-  if (rows == 1)
-    hipLaunchKernelGGL(router_decode_kernel<1>, dim3(256), dim3(256), 0, s, x, w, bias, rows, hidden, experts,
-                       max_users, logits, ids, scores, plan, counter);
+#define MOE_ROUTER_LAUNCH(R, KI)                                                                                 \
+  hipLaunchKernelGGL((router_decode_kernel<R, KI>), dim3(256), dim3(256), 0, s, x, w, bias, rows, hidden, experts, \
+                     max_users, logits, ids, scores, plan, counter)
+  if (rows == 1 && hidden == 6144)
+    MOE_ROUTER_LAUNCH(1, 6);
+  else if (rows == 1)
+    MOE_ROUTER_LAUNCH(1, 0);
+  else if (hidden == 6144)
+    MOE_ROUTER_LAUNCH(kMaxRows, 6);
   else
-    hipLaunchKernelGGL(router_decode_kernel<kMaxRows>, dim3(256), dim3(256), 0, s, x, w, bias, rows, hidden, experts,
-                       max_users, logits, ids, scores, plan, counter);
+    MOE_ROUTER_LAUNCH(kMaxRows, 0);
+#undef MOE_ROUTER_LAUNCH
   MOE_HIP(hipGetLastError());
   return MOE_OK;
 }
