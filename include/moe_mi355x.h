@@ -111,6 +111,27 @@ int moe_k4_moe_decode(const uint16_t* x, const uint16_t* residual, int rows, con
                       const uint16_t* out_down, int hidden, int intermediate, uint16_t* out, uint32_t* indices,
                       float* scores, void* workspace, size_t workspace_bytes, moe_stream_t stream);
 
+/* Residual add + RMSNorm of decode rows: h = T(x + residual) (residual may be NULL: h = x),
+ * out = T(w * T(h * rsqrt(mean(h^2) + eps))), T = bf16, x/residual/h_out/out [rows, n], w [n];
+ * h_out may be NULL.  n a multiple of 2048 up to 8192.
+ * Replaces: exlr8/fast_norm.py:20-28 residual_rms_pair (exlr8/metal/residual_rms.metal), and
+ * exlr8/model.py:382-383 (h = x + r; mx.fast.rms_norm(h, post_norm, eps)). */
+int moe_residual_rmsnorm(const uint16_t* x, const uint16_t* residual, const uint16_t* weight, int rows, int n,
+                         float eps, uint16_t* h_out, uint16_t* out, moe_stream_t stream);
+
+/* One decode layer's MoE half with its input norm: h = T(x + attn) (attn may be NULL: h = x),
+ * xn = RMSNorm(h) (norm_w [h] bf16, eps), then the routed MoE block on xn with residual h:
+ * out = T(h + r).  Shapes and side vectors as moe_k4_moe_decode; hidden a multiple of 2048 <= 8192.
+ * Replaces: exlr8/model.py:382-418 (h = x + r; x = rms_norm(h, post_norm); MoE branch), the
+ * layer body of a stack with no attention output. */
+int moe_k4_layer_decode(const uint16_t* x, const uint16_t* attn, const uint16_t* norm_w, float eps, int rows,
+                        const float* router_w, const float* bias, const void* packed_gate, const void* packed_up,
+                        const void* packed_down, int64_t packed_bytes, const uint16_t* in_gate,
+                        const uint16_t* out_gate, const uint16_t* in_up, const uint16_t* out_up,
+                        const uint16_t* in_down, const uint16_t* out_down, int hidden, int intermediate,
+                        uint16_t* out, uint32_t* indices, float* scores, void* workspace, size_t workspace_bytes,
+                        moe_stream_t stream);
+
 /* ---------------------------------------------------------------- joined MXFP4 */
 
 /* Resident joined-MXFP4 experts: gate_up codes [E, 2m, h/2] (e2m1, low nibble = even k) with e8m0

@@ -33,6 +33,9 @@ _SIGNATURES = {
                           + [_I32, _I32, _VP, _VP, _SZ, _VP]),
     "moe_k4_moe_decode": (_I32, [_VP, _VP, _I32, _VP, _VP, _VP, _VP, _VP, _I64] + [_VP] * 6
                           + [_I32, _I32, _VP, _VP, _VP, _VP, _SZ, _VP]),
+    "moe_k4_layer_decode": (_I32, [_VP, _VP, _VP, ctypes.c_float, _I32, _VP, _VP, _VP, _VP, _VP, _I64] + [_VP] * 6
+                            + [_I32, _I32, _VP, _VP, _VP, _VP, _SZ, _VP]),
+    "moe_residual_rmsnorm": (_I32, [_VP, _VP, _VP, _I32, _I32, ctypes.c_float, _VP, _VP, _VP]),
     "moe_workspace_bytes": (_SZ, [_I32, _I32]),
     "moe_profile_events": (_I32, [_VP, _I32]),
     "moe_mxfp4_mlp": (_I32, [_VP, _VP, _I32, _I32, _VP, _VP, _VP, _VP, _I64] + [_VP] * 5

@@ -665,6 +665,8 @@ struct Workspace {
   float* logits;        // [kMaxRows][256]
   uint32_t* ids;        // [kMaxRows][9]
   float* scores;        // [kMaxRows][8]
+  uint16_t* hrow;       // [kMaxRows][hidden] layer residual T(x + attn) (moe_k4_layer_decode)
+  uint16_t* xnrow;      // [kMaxRows][hidden] normalised expert input (moe_k4_layer_decode)
   size_t bytes;
 };
 
@@ -687,6 +689,8 @@ Workspace carve(void* base, int hidden, int inter) {
   w.logits = reinterpret_cast<float*>(take((size_t)kMaxRows * 256 * 4));
   w.ids = reinterpret_cast<uint32_t*>(take((size_t)kMaxRows * 9 * 4));
   w.scores = reinterpret_cast<float*>(take((size_t)kMaxRows * 8 * 4));
+  w.hrow = reinterpret_cast<uint16_t*>(take((size_t)kMaxRows * hidden * 2));
+  w.xnrow = reinterpret_cast<uint16_t*>(take((size_t)kMaxRows * hidden * 2));
   w.bytes = off;
   return w;
 }
@@ -941,6 +945,37 @@ int moe_k4_moe_decode(const uint16_t* x, const uint16_t* residual, int rows, con
   return k4_mlp_common(x, ids, sc, residual, rows, kSlots, packed_gate, packed_up, packed_down, packed_bytes, in_gate,
                        out_gate, in_up, out_up, in_down, out_down, hidden, intermediate, nullptr, out, workspace,
                        workspace_bytes, s, true);
+}
+
+int moe_k4_layer_decode(const uint16_t* x, const uint16_t* attn, const uint16_t* norm_w, float eps, int rows,
+                        const float* router_w, const float* bias, const void* packed_gate, const void* packed_up,
+                        const void* packed_down, int64_t packed_bytes, const uint16_t* in_gate,
+                        const uint16_t* out_gate, const uint16_t* in_up, const uint16_t* out_up,
+                        const uint16_t* in_down, const uint16_t* out_down, int hidden, int intermediate,
+                        uint16_t* out, uint32_t* indices, float* scores, void* workspace, size_t workspace_bytes,
+                        moe_stream_t stream) {
+  MOE_ARG(x && norm_w && router_w && bias && out, "null pointer argument");
+  MOE_ARG(rows >= 1 && rows <= kMaxRows, "rows must be in 1..%d", kMaxRows);
+  MOE_ARG(eps >= 0.0f, "epsilon must be non-negative");
+  MOE_ARG(hidden % 2048 == 0 && hidden <= 8192, "layer width must be a multiple of 2048 up to 8192 (got %d)", hidden);
+  int rc = validate_ws(workspace, workspace_bytes, hidden, intermediate);
+  if (rc) return rc;
+  if ((rc = ensure_device_ready())) return rc;
+  Workspace w = carve(workspace, hidden, intermediate);
+  hipStream_t s = (hipStream_t)stream;
+  uint32_t* ids = indices ? indices : w.ids;
+  float* sc = scores ? scores : w.scores;
+  int64_t experts = 0;
+  if ((rc = check_trellis(packed_bytes, hidden, intermediate, &experts))) return rc;
+  MOE_ARG(experts == 257, "the routed decode block needs 256 routed experts plus the shared expert (got %lld)",
+          (long long)experts);
+  prof_mark(0, s);
+  rc = moe_router_fused_plan(x, router_w, bias, rows, hidden, 257, w.logits, ids, sc, w.plan, w.router_counter, s,
+                             attn, norm_w, eps, w.hrow, w.xnrow);
+  if (rc) return rc;
+  return k4_mlp_common(w.xnrow, ids, sc, w.hrow, rows, kSlots, packed_gate, packed_up, packed_down, packed_bytes,
+                       in_gate, out_gate, in_up, out_up, in_down, out_down, hidden, intermediate, nullptr, out,
+                       workspace, workspace_bytes, s, true);
 }
 
 }  // extern "C"

@@ -19,8 +19,9 @@ int device_cus();
 
 // Router GEMV + route + dispatch plan for decode batches (router.hip).
 int moe_router_fused_plan(const uint16_t* x, const float* w, const float* bias, int rows, int hidden, int experts,
-                          float* logits, uint32_t* ids, float* scores, Plan* plan, int32_t* counter,
-                          hipStream_t stream);
+                          float* logits, uint32_t* ids, float* scores, Plan* plan, int32_t* counter, hipStream_t s,
+                          const uint16_t* attn = nullptr, const uint16_t* norm_w = nullptr, float eps = 0.0f,
+                          uint16_t* h_out = nullptr, uint16_t* xn_out = nullptr);
 
 }  // namespace moe
 

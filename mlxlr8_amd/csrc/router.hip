@@ -195,13 +195,21 @@ __global__ __launch_bounds__(64) void route_kernel(const float* __restrict__ log
 // routes all rows (one wave per row) and builds the token -> expert dispatch plan.
 // KI = hidden / 1024 when known at compile time (all loads of a block are then issued before the
 // first multiply, one memory round trip), 0 for any multiple of 1024.
-template <int R, int KI>
+//
+// NORM (KI > 0 only): the router input is RMSNorm(h), h = T(x + attn) (attn optional), computed
+// in every block from the raw rows (each block holds whole rows, so it reduces the sum of squares
+// itself); block r also stores row r's h (the layer residual) and normalised input for the
+// expert kernels.  Same arithmetic as moe_residual_rmsnorm.
+template <int R, int KI, bool NORM>
 __global__ __launch_bounds__(256) void router_decode_kernel(const uint16_t* __restrict__ x,
                                                             const float* __restrict__ w,
                                                             const float* __restrict__ bias, int rows, int hidden,
                                                             int experts, int max_users, float* logits,
                                                             uint32_t* ids, float* __restrict__ scores, Plan* plan,
-                                                            int32_t* counter) {
+                                                            int32_t* counter, const uint16_t* __restrict__ attn,
+                                                            const uint16_t* __restrict__ norm_w, float eps,
+                                                            uint16_t* __restrict__ h_out,
+                                                            uint16_t* __restrict__ xn_out) {
   const int e = blockIdx.x;
   const float* __restrict__ we = w + (int64_t)e * hidden;
   float acc[R];
@@ -223,6 +231,56 @@ __global__ __launch_bounds__(256) void router_decode_kernel(const uint16_t* __re
 #pragma unroll
       for (int i = 0; i < KI; i++)
         if (r < rows) xv[r][i] = *reinterpret_cast<const u32x2*>(x + (int64_t)r * hidden + threadIdx.x * 4 + i * 1024);
+    if (NORM) {
+      __shared__ float nred[R][4];
+      u32x2 nw[KI > 0 ? KI : 1];
+#pragma unroll
+      for (int i = 0; i < KI; i++) nw[i] = *reinterpret_cast<const u32x2*>(norm_w + threadIdx.x * 4 + i * 1024);
+      auto lo = [](uint32_t v) { return bf16_to_f32((uint16_t)(v & 0xFFFFu)); };
+      auto hi = [](uint32_t v) { return bf16_to_f32((uint16_t)(v >> 16)); };
+      auto pk = [](float a, float b) { return (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16); };
+      float ss[R];
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        ss[r] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < KI; i++)
+          if (r < rows) {
+            u32x2 av = u32x2{0, 0};
+            if (attn) av = *reinterpret_cast<const u32x2*>(attn + (int64_t)r * hidden + threadIdx.x * 4 + i * 1024);
+            const float h0 = round_bf16(lo(xv[r][i].x) + lo(av.x)), h1 = round_bf16(hi(xv[r][i].x) + hi(av.x));
+            const float h2 = round_bf16(lo(xv[r][i].y) + lo(av.y)), h3 = round_bf16(hi(xv[r][i].y) + hi(av.y));
+            ss[r] = fmaf(h0, h0, ss[r]);
+            ss[r] = fmaf(h1, h1, ss[r]);
+            ss[r] = fmaf(h2, h2, ss[r]);
+            ss[r] = fmaf(h3, h3, ss[r]);
+            xv[r][i] = u32x2{pk(h0, h1), pk(h2, h3)};
+          }
+        const float v = wave_sum(ss[r]);
+        if (lane_id() == 63) nred[r][wave_id_in_block()] = v;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        if (r < rows) {
+          const float inv = 1.0f / sqrtf(((nred[r][0] + nred[r][1]) + (nred[r][2] + nred[r][3])) / (float)hidden + eps);
+#pragma unroll
+          for (int i = 0; i < KI; i++) {
+            const u32x2 hv = xv[r][i];
+            const u32x2 xn = u32x2{pk(round_bf16(lo(nw[i].x) * round_bf16(lo(hv.x) * inv)),
+                                      round_bf16(hi(nw[i].x) * round_bf16(hi(hv.x) * inv))),
+                                   pk(round_bf16(lo(nw[i].y) * round_bf16(lo(hv.y) * inv)),
+                                      round_bf16(hi(nw[i].y) * round_bf16(hi(hv.y) * inv)))};
+            if ((int)blockIdx.x == r) {
+              const int64_t off = (int64_t)r * hidden + threadIdx.x * 4 + i * 1024;
+              *reinterpret_cast<u32x2*>(h_out + off) = hv;
+              *reinterpret_cast<u32x2*>(xn_out + off) = xn;
+            }
+            xv[r][i] = xn;
+          }
+        }
+      }
+    }
 #pragma unroll
     for (int i = 0; i < KI; i++)
 #pragma unroll
@@ -281,23 +339,39 @@ int launch_router_logits(const uint16_t* x, const float* w, int rows, int hidden
   return MOE_OK;
 }
 
-// Router GEMV + route + dispatch plan for decode batches (used by moe_k4_moe_decode).
+// Router GEMV + route + dispatch plan for decode batches (used by moe_k4_moe_decode).  With
+// norm_w, x is the raw layer input: the router (and the expert kernels, through xn_out) see
+// RMSNorm(T(x + attn)), and h_out receives T(x + attn).
 int moe_router_fused_plan(const uint16_t* x, const float* w, const float* bias, int rows, int hidden, int experts,
-                          float* logits, uint32_t* ids, float* scores, Plan* plan, int32_t* counter, hipStream_t s) {
+                          float* logits, uint32_t* ids, float* scores, Plan* plan, int32_t* counter, hipStream_t s,
+                          const uint16_t* attn, const uint16_t* norm_w, float eps, uint16_t* h_out,
+                          uint16_t* xn_out) {
   MOE_ARG(hidden > 0 && hidden % 1024 == 0, "router hidden size must be a positive multiple of 1024");
   MOE_ARG(rows >= 1 && rows <= kMaxRows, "decode routing handles 1..%d rows", kMaxRows);
   const int max_users = rows == 1 ? 1 : kMaxRows;
-#define MOE_ROUTER_LAUNCH(R, KI)                                                                                 \
-  hipLaunchKernelGGL((router_decode_kernel<R, KI>), dim3(256), dim3(256), 0, s, x, w, bias, rows, hidden, experts, \
-                     max_users, logits, ids, scores, plan, counter)
-  if (rows == 1 && hidden == 6144)
-    MOE_ROUTER_LAUNCH(1, 6);
+  const uint16_t* xin = x;
+  const bool fused_norm = norm_w && hidden == 6144;
+  if (norm_w && !fused_norm) {
+    // other widths: normalise first, then route the normalised rows
+    int rc = moe_residual_rmsnorm(x, attn, norm_w, rows, hidden, eps, h_out, xn_out, (moe_stream_t)s);
+    if (rc) return rc;
+    xin = xn_out;
+  }
+#define MOE_ROUTER_LAUNCH(R, KI, N)                                                                                 \
+  hipLaunchKernelGGL((router_decode_kernel<R, KI, N>), dim3(256), dim3(256), 0, s, xin, w, bias, rows, hidden,      \
+                     experts, max_users, logits, ids, scores, plan, counter, attn, norm_w, eps, h_out, xn_out)
+  if (fused_norm && rows == 1)
+    MOE_ROUTER_LAUNCH(1, 6, true);
+  else if (fused_norm)
+    MOE_ROUTER_LAUNCH(kMaxRows, 6, true);
+  else if (rows == 1 && hidden == 6144)
+    MOE_ROUTER_LAUNCH(1, 6, false);
   else if (rows == 1)
-    MOE_ROUTER_LAUNCH(1, 0);
+    MOE_ROUTER_LAUNCH(1, 0, false);
   else if (hidden == 6144)
-    MOE_ROUTER_LAUNCH(kMaxRows, 6);
+    MOE_ROUTER_LAUNCH(kMaxRows, 6, false);
   else
-    MOE_ROUTER_LAUNCH(kMaxRows, 0);
+    MOE_ROUTER_LAUNCH(kMaxRows, 0, false);
 #undef MOE_ROUTER_LAUNCH
   MOE_HIP(hipGetLastError());
   return MOE_OK;

@@ -84,6 +84,47 @@ class ExpertLayer:
         call.run = run
         return call
 
+    def prepare_layer_decode(self, x, norm_weight, router_weight, bias, attn=None, eps=1e-5):
+        """Like prepare_decode for a whole decode layer's MoE half: h = T(x + attn), the routed
+        block runs on rms_norm(h, norm_weight) with residual h (one C call per run).  `x` is bound
+        by reference, so a stack can feed one layer's `.out` to the next layer's `x`."""
+        h = self.hidden
+        rows = x.numel() // h
+        if rows > 8 or self.experts != 257 or x.dtype != BF16:
+            raise ValueError("prepare_layer_decode needs <= 8 bf16 rows and 256 routed + 1 shared experts")
+        if not x.is_contiguous():
+            raise ValueError("the layer input must be contiguous (it is bound by address)")
+        require_cuda(x, norm_weight, router_weight, bias)
+        call = SimpleNamespace()
+        call.x = x
+        call.attn = attn.reshape(rows, h).to(BF16).contiguous() if attn is not None else None
+        call.norm = norm_weight.to(BF16).contiguous()
+        call.w = router_weight.to(torch.float32).contiguous()
+        call.bias = bias.to(torch.float32).contiguous()
+        call.out = torch.empty((rows, h), dtype=BF16, device=x.device)
+        call.ids = torch.empty((rows, 9), dtype=torch.int32, device=x.device)
+        call.scores = torch.empty((rows, 8), dtype=torch.float32, device=x.device)
+        ws = workspace(x.device, h, self.intermediate)
+        args = (ptr(x), ptr(call.attn) if call.attn is not None else None, ptr(call.norm), float(eps), rows,
+                ptr(call.w), ptr(call.bias), *_weights(self.packed, self.scales), h, self.intermediate,
+                ptr(call.out), ptr(call.ids), ptr(call.scores), ptr(ws), ws.numel(), stream(x.device))
+        fn = lib().moe_k4_layer_decode
+
+        def run():
+            check(fn(*args))
+            return call.out
+
+        call.run = run
+        return call
+
+    def layer_decode(self, x, norm_weight, router_weight, bias, attn=None, eps=1e-5):
+        """One-shot form of prepare_layer_decode: returns (out, indices [rows,9], scores [rows,8])."""
+        h = self.hidden
+        xr = x.reshape(x.numel() // h, h).to(BF16).contiguous()
+        call = self.prepare_layer_decode(xr, norm_weight, router_weight, bias, attn, eps)
+        call.run()
+        return call.out.reshape(x.shape), call.ids, call.scores
+
     def decode_block_routes(self, x, residual, router_weight, bias):
         h = self.hidden
         rows = x.numel() // h

@@ -71,3 +71,32 @@ class MoEBlock:
         if self._expert_finish is None:
             self._expert_finish = compiled_expert_mlp_finish(self.experts)
         return self._expert_finish(x, indices, scores, h)
+
+
+class DecoderMoELayer:
+    """A decoder layer's post-attention half: h = x + attn_out; out = h + MoE(rms_norm(h))
+    (exlr8/model.py:376-418 with the fused residual/RMS pair of exlr8/fast_norm.py), for decode
+    rows on the K4 experts.  One library call per layer."""
+
+    def __init__(self, args, post_norm, router_weight, bias, experts, eps=1e-5):
+        if not (_fast_router_args(args) and getattr(experts, "k", None) == 4):
+            raise NotImplementedError("the fused decode layer is built for the GLM-5.3 K4 configuration")
+        self.args, self.norm, self.gate, self.bias, self.experts, self.eps = (args, post_norm, router_weight, bias,
+                                                                               experts, eps)
+
+    def __call__(self, x, attn=None):
+        out, ids, scores = self.experts.layer_decode(x, self.norm, self.gate, self.bias, attn, self.eps)
+        return out, ids[..., :8]
+
+
+class DecoderMoEStack:
+    """Consecutive decoder MoE layers with no attention output between them (each layer:
+    h <- h + MoE(rms_norm(h))): the 20-layer K4 decode stack."""
+
+    def __init__(self, layers):
+        self.layers = list(layers)
+
+    def __call__(self, x):
+        for layer in self.layers:
+            x, _ = layer(x)
+        return x
