@@ -166,6 +166,31 @@ size_t moe_mxfp4_workspace_bytes(int hidden, int intermediate);
  * runs on.  No counterpart in the reference (its benchmarks time whole model steps). */
 int moe_profile_events(void** events, int count);
 
+/* ---------------------------------------------------------------- prefill (sorted work order) */
+
+/* Sorted work order of flat expert ids [n] (values < experts <= 1024): order [n] (sorted position
+ * -> flat index, stable within an expert), counts/starts [experts], and the block table
+ * table [3][capacity] = (expert, first sorted position, length <= block_rows), *num_blocks rows used;
+ * capacity >= n / block_rows + experts.  Ids outside [0, experts) are skipped (no position).
+ * Replaces: exlr8/fast_prefill.py:19-46 _segment_table / _plan (argsort + counts + block table). */
+int moe_segment_table(const uint32_t* ids, int n, int experts, int block_rows, int32_t* order, int32_t* counts,
+                      int32_t* starts, int32_t* table, int capacity, int32_t* num_blocks, moe_stream_t stream);
+
+/* Prefill chunk through the joined-MXFP4 experts: router GEMV + route for `rows` rows, sorted
+ * work order, grouped gate_up GEMM + gate finish, grouped down GEMM + value finish, weighted
+ * combine with the shared expert and the residual.  Weights/side vectors as moe_mxfp4_mlp
+ * (hidden a multiple of 1024, intermediate of 128); indices/scores optional outputs.
+ * Workspace: moe_mxfp4_prefill_workspace_bytes(rows, hidden, intermediate, experts) (no zeroing).
+ * Replaces: exlr8/joined_mxfp4.py:90-134,148-163 (JoinedMXFP4._inner with gather_qmm sorted RHS,
+ * finish) for prefill rows, with the router of exlr8/model.py:111-132. */
+int moe_mxfp4_prefill(const uint16_t* x, const uint16_t* residual, int rows, const float* router_w,
+                      const float* bias, const uint8_t* gate_up_codes, const uint8_t* gate_up_scales,
+                      const uint8_t* down_codes, const uint8_t* down_scales, int64_t experts, const uint16_t* unit,
+                      const uint16_t* out_gate, const uint16_t* out_up, const uint16_t* in_down,
+                      const uint16_t* out_down, int hidden, int intermediate, uint16_t* out, uint32_t* indices,
+                      float* scores, void* workspace, size_t workspace_bytes, moe_stream_t stream);
+size_t moe_mxfp4_prefill_workspace_bytes(int rows, int hidden, int intermediate, int64_t experts);
+
 /* ---------------------------------------------------------------- workspace */
 
 /* Bytes of workspace needed by the decode entry points above for the given shape on the

@@ -1,0 +1,712 @@
+// Joined-MXFP4 expert path for prefill chunks on gfx950: sorted-by-expert grouped GEMMs on the
+// scaled MX MFMA (v_mfma_scale_f32_16x16x128_f8f6f4, activations fp8 x weights fp4).
+//
+// Reference semantics (paths relative to the reference root):
+//   sorted work order: argsort of the flat expert ids, per-expert counts/starts and a block table
+//     (expert, first, length)                                   exlr8/fast_prefill.py:19-46
+//   xh = H128(x * unit) per token                                exlr8/joined_mxfp4.py:96
+//   gu = xh @ W_gate_up[e]^T, grouped by expert (gather_qmm)     exlr8/joined_mxfp4.py:98-113
+//   hidden = H128(swiglu_T(H(g)*og, H(u)*ou) * in_down)         exlr8/metal/joined_gate_finish.metal
+//   v = hidden @ W_down[e]^T                                      exlr8/joined_mxfp4.py:121-134
+//   value = T(H128(v) * out_down); out = T(T(sum_i value_i*score_i) + shared) + residual
+//                                                                 exlr8/model.py:415-418
+//
+// MI355X design:
+//   * Activations are split as x = hi + lo1 + lo2 with hi = f16(x) and the remainder in two fp8
+//     (e4m3) terms, each with an e8m0 scale per 32 values (~20 significant bits in all: the bf16
+//     casts of gate/up and of the values then flip as rarely as with fp32 activations).  hi runs on
+//     the fp16 matrix cores (v_mfma_f32_16x16x32_f16) against the weights widened to fp16 in
+//     registers (v_cvt_scalef32_pk_f16_fp4 applies the block scale; exact for e8m0 scales
+//     114..140); lo1 and lo2 run on the scaled MX matrix cores (v_mfma_scale_f32_16x16x128_f8f6f4,
+//     fp8 x MXFP4) with the resident codes and both block scales.  The scaled MX instruction keeps
+//     only ~15 bits across its 128-product sums, ample for the < 2^-11 remainder but not for the
+//     whole value; all terms go into one fp32 accumulator.
+//   * Operand layout of the 16x16x128 scaled MFMA (measured on gfx950): lane l holds row/column
+//     l%16; fp8 A bytes 0-15 are k = 16(l/16)+j and bytes 16-31 are k = 64+16(l/16)+j-16; fp4 B
+//     nibble j (low nibble first) is k = 32(l/16)+j; lane l's scale byte scales k-block l/16.  The
+//     fp16 MFMAs of a 128-wide k step reuse the lane's 32 widened weights: MFMA q (q = 0..3) maps
+//     its k-group kg = l/16 to k = 32 kg + 8q + i, and the staged hi activations are read to match.
+//   * A work item is (block of <= 128 sorted rows of one expert, output block): the weights of the
+//     output block are streamed once per item with 16 B loads per lane; the item's activation
+//     terms for one 128-wide k step are staged in LDS (double buffered) and shared by the 8 waves.
+//   * The gate finish (both 128-column halves of an intermediate block are in one item) and the
+//     down finish (H128 over the item's 128 output columns) run in the GEMM epilogues through LDS;
+//     the gate epilogue writes the down GEMM's fp8 terms directly.
+#include <hip/hip_runtime.h>
+
+#include "moe_device.h"
+#include "moe_host.h"
+
+namespace moe {
+namespace {
+
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ f16x8 pack_f16x8(f16x2 a, f16x2 b, f16x2 c, f16x2 d) {
+  typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+  const f16x4 ab = __builtin_shufflevector(a, b, 0, 1, 2, 3), cd = __builtin_shufflevector(c, d, 0, 1, 2, 3);
+  return __builtin_shufflevector(ab, cd, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+constexpr int kPfItemRows = 128; // sorted rows per GEMM work item (8 M-tiles of 16)
+constexpr int kPfWaves = 8;      // waves per GEMM block
+constexpr int kPfThreads = kPfWaves * 64;
+constexpr int kPfRowBytes = 528; // LDS row stride of a staged k step: 256 B hi + 2 x 128 B lo + pad
+constexpr int kPfLo = 2;         // fp8 remainder terms
+constexpr int kPfMaxExperts = 1024;
+
+// ---------------------------------------------------------------- sorted work order
+// One block of 1024 threads.  Counting sort of the flat ids (stable: slots of one expert keep
+// their order), per-expert counts and starts, and the block table of `block_rows` rows.
+__global__ __launch_bounds__(1024) void segment_table_kernel(const uint32_t* __restrict__ ids, int n, int experts,
+                                                             int block_rows, int32_t* __restrict__ order,
+                                                             int32_t* __restrict__ counts,
+                                                             int32_t* __restrict__ starts, int32_t* __restrict__ blk,
+                                                             int cap, int32_t* __restrict__ nblk) {
+  __shared__ int32_t cnt[kPfMaxExperts], st[kPfMaxExperts], fill[kPfMaxExperts], bst[kPfMaxExperts];
+  __shared__ int32_t wsum[16];
+  const int tid = threadIdx.x, lane = lane_id(), wv = wave_id_in_block();
+  for (int e = tid; e < experts; e += 1024) { cnt[e] = 0; fill[e] = 0; }
+  __syncthreads();
+  // ids outside [0, experts) are skipped (they get no position; callers pass valid ids)
+  for (int i = tid; i < n; i += 1024) {
+    const uint32_t e = ids[i];
+    if (e < (uint32_t)experts) atomicAdd(&cnt[e], 1);
+  }
+  __syncthreads();
+  // exclusive scans of the counts and of the per-expert block counts (experts <= 1024: one per thread)
+  {
+    const int c = tid < experts ? cnt[tid] : 0;
+    const int b = tid < experts ? (c + block_rows - 1) / block_rows : 0;
+    int ic = c, ib = b;  // inclusive wave scans
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int oc = __shfl_up(ic, d, 64), ob = __shfl_up(ib, d, 64);
+      if (lane >= d) { ic += oc; ib += ob; }
+    }
+    if (lane == 63) wsum[wv] = ic;
+    __syncthreads();
+    int offc = 0;
+    for (int w = 0; w < wv; w++) offc += wsum[w];
+    __syncthreads();
+    if (lane == 63) wsum[wv] = ib;
+    __syncthreads();
+    int offb = 0;
+    for (int w = 0; w < wv; w++) offb += wsum[w];
+    if (tid < experts) {
+      st[tid] = offc + ic - c;
+      bst[tid] = offb + ib - b;
+      counts[tid] = c;
+      starts[tid] = offc + ic - c;
+    }
+    if (tid == 1023) *nblk = offb + ib;
+  }
+  __syncthreads();
+  // stable placement: chunks of 1024 slots in order, waves of a chunk in order; inside a wave the
+  // rank of a slot among equal ids comes from matching the id bit by bit with ballots
+  for (int c0 = 0; c0 < n; c0 += 1024) {
+    for (int w = 0; w < 16; w++) {
+      if (wv == w) {
+        const int i = c0 + tid;
+        const uint32_t e = i < n ? ids[i] : 0xFFFFFFFFu;
+        const bool valid = e < (uint32_t)experts;
+        uint64_t same = __ballot(1);
+#pragma unroll
+        for (int bit = 0; bit < 32; bit++) {
+          const bool on = (e >> bit) & 1u;
+          const uint64_t bal = __ballot(on);
+          same &= on ? bal : ~bal;
+        }
+        const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+        const int rank = __popcll(same & below);
+        if (valid) {
+          const int pos = st[e] + fill[e] + rank;
+          order[pos] = i;
+        }
+        __builtin_amdgcn_wave_barrier();
+        if (valid && rank == 0) fill[e] += __popcll(same);
+      }
+      __syncthreads();
+    }
+  }
+  // block table rows (expert, first, length)
+  for (int e = tid; e < experts; e += 1024) {
+    const int c = cnt[e];
+    for (int f = 0, b = bst[e]; f < c; f += block_rows, b++) {
+      if (b < cap) {
+        blk[b] = e;
+        blk[cap + b] = st[e] + f;
+        blk[2 * cap + b] = min(block_rows, c - f);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------- fp8 terms of activations
+// 32 values held as 2 per lane by 16 lanes (one DPP row): max magnitude of the row.
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_f32<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp_f32<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp_f32<0x124>(v));  // row_ror:4
+  v = fmaxf(v, dpp_f32<0x128>(v));  // row_ror:8
+  return v;
+}
+// Split (v0, v1) of a 32-value group (the 16 lanes of a DPP row) into hi = f16 pair (returned as
+// bits) and the remainder as kPfLo fp8 terms: lo[t] holds the term's two codes (bytes 0, 1) and
+// scale[t] the group's e8m0 scale of term t (each term rounds the previous remainder).
+__device__ __forceinline__ uint32_t hi_lo_terms(float v0, float v1, uint32_t (&lo)[kPfLo], uint32_t (&scale)[kPfLo]) {
+  const _Float16 h0 = (_Float16)v0, h1 = (_Float16)v1;
+  float r0 = v0 - (float)h0, r1 = v1 - (float)h1;  // exact
+#pragma unroll
+  for (int t = 0; t < kPfLo; t++) {
+    const float amax = row16_max(fmaxf(fabsf(r0), fabsf(r1)));
+    // scale 2^s with amax / 2^s in [128, 256): the e4m3 range (448) is never exceeded
+    int s = 0;
+    if (amax > 0.0f) s = (int)((__float_as_uint(amax) >> 23) & 0xFF) - 127 - 7;
+    s = max(-127, min(127, s));
+    const i16x2 old = {0, 0};
+    const uint32_t codes =
+        __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pk_fp8_f32(__builtin_amdgcn_ldexpf(r0, -s),
+                                                                     __builtin_amdgcn_ldexpf(r1, -s),
+                                                                     __builtin_bit_cast(int, old), false)) &
+        0xFFFFu;
+    lo[t] = codes;
+    scale[t] = (uint32_t)(s + 127);
+    const f32x2 d = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(codes, 1.0f, false);
+    r0 -= __builtin_amdgcn_ldexpf(d.x, s);  // exact: the code is r0's rounding at this scale
+    r1 -= __builtin_amdgcn_ldexpf(d.y, s);
+  }
+  return (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+}
+
+// xh = H128(x * unit) of every token -> hi/lo terms.  One wave per (token, 128-block).
+// xh_hi: [rows][K] fp16, xq: [kPfLo][rows][K] fp8 remainder terms, xs: [kPfLo][rows][K/32] e8m0.
+__global__ __launch_bounds__(256) void prep_terms_kernel(const uint16_t* __restrict__ x,
+                                                         const uint16_t* __restrict__ unit, int rows, int K,
+                                                         uint16_t* __restrict__ xh_hi, uint8_t* __restrict__ xq,
+                                                         uint8_t* __restrict__ xs) {
+  const int64_t wid = (int64_t)blockIdx.x * 4 + wave_id_uniform();
+  const int blocks = K / 128;
+  if (wid >= (int64_t)rows * blocks) return;
+  const int t = (int)(wid / blocks), b = (int)(wid % blocks);
+  const int lane = lane_id();
+  const int k0 = b * 128 + 2 * lane;
+  const uint32_t xv = *reinterpret_cast<const uint32_t*>(x + (int64_t)t * K + k0);
+  const uint32_t uv = *reinterpret_cast<const uint32_t*>(unit + k0);
+  float v0 = bf16_to_f32((uint16_t)(xv & 0xFFFFu)) * f16_to_f32((uint16_t)(uv & 0xFFFFu));
+  float v1 = bf16_to_f32((uint16_t)(xv >> 16)) * f16_to_f32((uint16_t)(uv >> 16));
+  hadamard128_wave(v0, v1);
+  uint32_t lo[kPfLo], sc[kPfLo];
+  const uint32_t hi = hi_lo_terms(v0, v1, lo, sc);
+  *reinterpret_cast<uint32_t*>(xh_hi + (int64_t)t * K + k0) = hi;
+#pragma unroll
+  for (int tt = 0; tt < kPfLo; tt++) {
+    *reinterpret_cast<uint16_t*>(xq + ((int64_t)tt * rows + t) * K + k0) = (uint16_t)lo[tt];
+    if ((lane & 15) == 0) xs[((int64_t)tt * rows + t) * (K / 32) + b * 4 + lane / 16] = (uint8_t)sc[tt];
+  }
+}
+
+// ---------------------------------------------------------------- grouped GEMM machinery
+struct PfGemm {
+  // weights (MXFP4): codes [E][N][K/2], scales [E][N][K/32]
+  const uint8_t* codes;
+  const uint8_t* wscales;
+  int K, N;
+  // activation terms: ahi [arows][K] fp16, aq [kPfLo][arows][K] fp8 remainder terms,
+  // as [kPfLo][arows][K/32] e8m0;
+  // the row of sorted position p is rowmap ? rowmap[p] / rowdiv : p
+  const uint16_t* ahi;
+  const uint8_t* aq;
+  const uint8_t* as;
+  int64_t arows;
+  const int32_t* rowmap;
+  int rowdiv;
+  // plan
+  const int32_t* blk;  // [3][cap]
+  int cap;
+  const int32_t* nblk;
+  const int32_t* order;  // sorted position -> slot
+  // gate epilogue (N = 2m): hidden terms hhi [n][m] fp16, hq [kPfLo][n][m] fp8, hs [kPfLo][n][m/32]
+  const uint16_t* out_gate;
+  const uint16_t* out_up;
+  const uint16_t* in_down;
+  int m;
+  uint16_t* hhi;
+  uint8_t* hq;
+  uint8_t* hs;
+  int64_t nslots;
+  // down epilogue: values [slots][N] bf16
+  const uint16_t* out_down;
+  uint16_t* values;
+};
+
+// Staging of one 128-wide k step of the item's activations: per row [256 B hi][128 B lo1][128 B lo2]
+// at stride kPfRowBytes, and the row's 4 scales of each remainder term.
+template <int MT>
+struct PfStage {
+  static constexpr int kBytes = MT * 16 * kPfRowBytes;
+  static constexpr int kScaleBytes = MT * 16 * 4 * kPfLo;
+};
+
+template <int MT>
+__device__ __forceinline__ void stage_k(const PfGemm& a, int ks, const int64_t* rowidx, uint8_t* buf, uint8_t* sbuf) {
+  // 16 B chunks per row: 16 of hi, 8 per remainder term
+  constexpr int kPer = 16 + 8 * kPfLo;
+  constexpr int kChunks = MT * 16 * kPer;
+  for (int c = threadIdx.x; c < kChunks; c += kPfThreads) {
+    const int r = c / kPer, ch = c % kPer;
+    i32x4 v;
+    if (ch < 16) {
+      v = *reinterpret_cast<const i32x4*>(a.ahi + rowidx[r] * a.K + ks * 128 + ch * 8);
+    } else {
+      const int t = (ch - 16) / 8, cc = (ch - 16) % 8;
+      v = *reinterpret_cast<const i32x4*>(a.aq + (t * a.arows + rowidx[r]) * a.K + ks * 128 + cc * 16);
+    }
+    *reinterpret_cast<i32x4*>(buf + r * kPfRowBytes + ch * 16) = v;
+  }
+  for (int c = threadIdx.x; c < MT * 16 * kPfLo; c += kPfThreads) {
+    const int r = c / kPfLo, t = c % kPfLo;
+    *reinterpret_cast<uint32_t*>(sbuf + (r * kPfLo + t) * 4) =
+        *reinterpret_cast<const uint32_t*>(a.as + (t * a.arows + rowidx[r]) * (a.K / 32) + ks * 4);
+  }
+}
+
+// The item's rows: sorted positions [first, first + len), clamped into the item for the padding
+// rows of the last M-tile (their results are discarded).
+template <int MT>
+__device__ __forceinline__ void item_rows(const PfGemm& a, int first, int len, int64_t* rowidx) {
+  for (int r = threadIdx.x; r < MT * 16; r += kPfThreads) {
+    const int p = first + min(r, len - 1);
+    rowidx[r] = a.rowmap ? (int64_t)(a.rowmap[p] / a.rowdiv) : (int64_t)p;
+  }
+}
+
+// One wave's NT column tiles (cols[j] .. +16) over all K for the item's MT M-tiles.
+template <int MT, int NT>
+__device__ __forceinline__ void gemm_item(const PfGemm& a, int e, const int (&cols)[NT], const int64_t* rowidx,
+                                          uint8_t* abuf, uint8_t* sbuf, f32x4 (&acc)[MT][NT]) {
+  const int lane = lane_id(), nn = lane & 15, g = lane >> 4;
+  const int ksteps = a.K / 128;
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+    for (int j = 0; j < NT; j++) acc[mt][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  const uint8_t* wrow[NT];
+  const uint8_t* srow[NT];
+#pragma unroll
+  for (int j = 0; j < NT; j++) {
+    const int64_t row = (int64_t)e * a.N + cols[j] + nn;
+    wrow[j] = a.codes + row * (a.K / 2) + g * 16;
+    srow[j] = a.wscales + row * (a.K / 32) + g;
+  }
+  constexpr int kStage = PfStage<MT>::kBytes, kSStage = PfStage<MT>::kScaleBytes;
+  stage_k<MT>(a, 0, rowidx, abuf, sbuf);
+  i32x4 bw[NT];
+  uint32_t bs[NT];
+#pragma unroll
+  for (int j = 0; j < NT; j++) {
+    bw[j] = *reinterpret_cast<const i32x4*>(wrow[j]);
+    bs[j] = srow[j][0];
+  }
+  __syncthreads();
+  for (int ks = 0; ks < ksteps; ks++) {
+    const int cur = ks & 1;
+    // next step's activations into the other buffer, next step's weights into registers
+    if (ks + 1 < ksteps) stage_k<MT>(a, ks + 1, rowidx, abuf + (cur ^ 1) * kStage, sbuf + (cur ^ 1) * kSStage);
+    i32x4 nbw[NT];
+    uint32_t nbs[NT];
+    const int kn = min(ks + 1, ksteps - 1);
+#pragma unroll
+    for (int j = 0; j < NT; j++) {
+      nbw[j] = *reinterpret_cast<const i32x4*>(wrow[j] + kn * 64);
+      nbs[j] = srow[j][kn * 4];
+    }
+    const uint8_t* ab = abuf + cur * kStage;
+    const uint8_t* sb = sbuf + cur * kSStage;
+    // the weights widened to fp16 with their block scale: bf[j][b] = codes of byte b
+    f16x2 bf[NT][16];
+#pragma unroll
+    for (int j = 0; j < NT; j++) {
+      const float wsc = __builtin_amdgcn_ldexpf(1.0f, (int)bs[j] - 127);
+      const uint32_t words[4] = {(uint32_t)bw[j].x, (uint32_t)bw[j].y, (uint32_t)bw[j].z, (uint32_t)bw[j].w};
+#pragma unroll
+      for (int wd = 0; wd < 4; wd++) {
+        bf[j][4 * wd + 0] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(words[wd], wsc, 0);
+        bf[j][4 * wd + 1] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(words[wd], wsc, 1);
+        bf[j][4 * wd + 2] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(words[wd], wsc, 2);
+        bf[j][4 * wd + 3] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(words[wd], wsc, 3);
+      }
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) {
+      const uint8_t* rp = ab + (mt * 16 + nn) * kPfRowBytes;
+      // hi: 4 fp16 MFMAs, q-th reads k = 32 g + 8 q + i
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const f16x8 ah = *reinterpret_cast<const f16x8*>(rp + (32 * g + 8 * q) * 2);
+#pragma unroll
+        for (int j = 0; j < NT; j++) {
+          const f16x8 bh = pack_f16x8(bf[j][4 * q], bf[j][4 * q + 1], bf[j][4 * q + 2], bf[j][4 * q + 3]);
+          acc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, acc[mt][j], 0, 0, 0);
+        }
+      }
+      // remainder terms: one scaled MX MFMA each on the resident codes
+#pragma unroll
+      for (int t = 0; t < kPfLo; t++) {
+        const i32x4 l0 = *reinterpret_cast<const i32x4*>(rp + 256 + 128 * t + 16 * g);
+        const i32x4 l1 = *reinterpret_cast<const i32x4*>(rp + 256 + 128 * t + 64 + 16 * g);
+        const i32x8 al = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
+        const int asc = sb[((mt * 16 + nn) * kPfLo + t) * 4 + g];
+#pragma unroll
+        for (int j = 0; j < NT; j++) {
+          const i32x8 bv = {bw[j].x, bw[j].y, bw[j].z, bw[j].w, 0, 0, 0, 0};
+          acc[mt][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(al, bv, acc[mt][j], 0, 4, 0, asc, 0,
+                                                                        (int)bs[j]);
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NT; j++) {
+      bw[j] = nbw[j];
+      bs[j] = nbs[j];
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------- gate/up GEMM + gate finish
+// Item = (plan block b, intermediate block c): columns gate [128c, +128) and up [m + 128c, +128);
+// wave w owns gate tile 16w and up tile 16w.
+template <int MT>
+__device__ void gateup_item(const PfGemm& a, int e, int first, int len, int c, uint8_t* abuf, uint8_t* sbuf,
+                            int64_t* rowidx, float* ex) {
+  const int w = wave_id_uniform(), lane = lane_id(), nn = lane & 15, g = lane >> 4;
+  item_rows<MT>(a, first, len, rowidx);
+  __syncthreads();
+  const int cols[2] = {128 * c + 16 * w, a.m + 128 * c + 16 * w};
+  f32x4 acc[MT][2];
+  gemm_item<MT, 2>(a, e, cols, rowidx, abuf, sbuf, acc);
+  // epilogue per M-tile: gate/up tiles -> LDS [16][2][128] -> per row: H128, scale, SwiGLU, in_down, H128
+  const int64_t si = (int64_t)e * a.m + 128 * c + 2 * lane;
+  const float og0 = f16_to_f32(a.out_gate[si]), og1 = f16_to_f32(a.out_gate[si + 1]);
+  const float ou0 = f16_to_f32(a.out_up[si]), ou1 = f16_to_f32(a.out_up[si + 1]);
+  const float id0 = f16_to_f32(a.in_down[si]), id1 = f16_to_f32(a.in_down[si + 1]);
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int r = 4 * g + i;
+      ex[(r * 2 + 0) * 128 + 16 * w + nn] = acc[mt][0][i];
+      ex[(r * 2 + 1) * 128 + 16 * w + nn] = acc[mt][1][i];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int rr = 0; rr < 2; rr++) {
+      const int r = 2 * w + rr;  // 8 waves x 2 rows
+      const int pr = mt * 16 + r;
+      if (pr < len) {
+        float g0 = ex[(r * 2) * 128 + 2 * lane], g1 = ex[(r * 2) * 128 + 2 * lane + 1];
+        float u0 = ex[(r * 2 + 1) * 128 + 2 * lane], u1 = ex[(r * 2 + 1) * 128 + 2 * lane + 1];
+        hadamard128_wave(g0, g1);
+        hadamard128_wave(u0, u1);
+        float h0 = swiglu_bf16(g0 * og0, u0 * ou0) * id0;
+        float h1 = swiglu_bf16(g1 * og1, u1 * ou1) * id1;
+        hadamard128_wave(h0, h1);
+        uint32_t lo[kPfLo], sc[kPfLo];
+        const uint32_t hi = hi_lo_terms(h0, h1, lo, sc);
+        const int64_t p = first + pr;
+        *reinterpret_cast<uint32_t*>(a.hhi + p * a.m + 128 * c + 2 * lane) = hi;
+#pragma unroll
+        for (int t = 0; t < kPfLo; t++) {
+          *reinterpret_cast<uint16_t*>(a.hq + (t * a.nslots + p) * a.m + 128 * c + 2 * lane) = (uint16_t)lo[t];
+          if (nn == 0) a.hs[(t * a.nslots + p) * (a.m / 32) + 4 * c + g] = (uint8_t)sc[t];
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------- down GEMM + value finish
+// Item = (plan block b, output block ob): columns [128 ob, +128); wave w owns tile 16w.
+template <int MT>
+__device__ void down_item(const PfGemm& a, int e, int first, int len, int ob, uint8_t* abuf, uint8_t* sbuf,
+                          int64_t* rowidx, float* ex) {
+  const int w = wave_id_uniform(), lane = lane_id(), nn = lane & 15, g = lane >> 4;
+  item_rows<MT>(a, first, len, rowidx);
+  __syncthreads();
+  const int cols[1] = {128 * ob + 16 * w};
+  f32x4 acc[MT][1];
+  gemm_item<MT, 1>(a, e, cols, rowidx, abuf, sbuf, acc);
+  const int64_t si = (int64_t)e * a.N + 128 * ob + 2 * lane;
+  const float od0 = f16_to_f32(a.out_down[si]), od1 = f16_to_f32(a.out_down[si + 1]);
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) ex[(4 * g + i) * 128 + 16 * w + nn] = acc[mt][0][i];
+    __syncthreads();
+#pragma unroll
+    for (int rr = 0; rr < 2; rr++) {
+      const int r = 2 * w + rr;
+      const int pr = mt * 16 + r;
+      if (pr < len) {
+        float v0 = ex[r * 128 + 2 * lane], v1 = ex[r * 128 + 2 * lane + 1];
+        hadamard128_wave(v0, v1);
+        const int slot = a.order[first + pr];
+        const uint32_t pk = (uint32_t)f32_to_bf16(v0 * od0) | ((uint32_t)f32_to_bf16(v1 * od1) << 16);
+        *reinterpret_cast<uint32_t*>(a.values + (int64_t)slot * a.N + 128 * ob + 2 * lane) = pk;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// Grid: (plan blocks) x (output blocks per item).  LDS: double-buffered activation stage for
+// MT = 8, scale stage, row map, epilogue exchange.
+template <bool GATE>
+__global__ __launch_bounds__(kPfThreads) void pf_gemm_kernel(PfGemm a) {
+  __shared__ __attribute__((aligned(16))) uint8_t abuf[2 * PfStage<8>::kBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t sbuf[2 * PfStage<8>::kScaleBytes];
+  __shared__ int64_t rowidx[8 * 16];
+  // the epilogue exchange [16][2][128] f32 reuses the activation stage (free after the k loop)
+  static_assert(2 * PfStage<8>::kBytes >= 16 * 2 * 128 * 4, "exchange buffer must fit in the stage");
+  float* ex = reinterpret_cast<float*>(abuf);
+  const int outblocks = GATE ? a.m / 128 : a.N / 128;
+  const int b = blockIdx.x / outblocks, ob = blockIdx.x % outblocks;
+  if (b >= *a.nblk) return;
+  const int e = a.blk[b], first = a.blk[a.cap + b], len = a.blk[2 * a.cap + b];
+  const int mt = (len + 15) / 16;
+#define PF_CASE(M)                                                                          \
+  case M:                                                                                   \
+    if (GATE)                                                                               \
+      gateup_item<M>(a, e, first, len, ob, abuf, sbuf, rowidx, ex);                         \
+    else                                                                                    \
+      down_item<M>(a, e, first, len, ob, abuf, sbuf, rowidx, ex);                           \
+    break;
+  switch (mt) {
+    PF_CASE(1)
+    PF_CASE(2)
+    PF_CASE(3)
+    PF_CASE(4)
+    PF_CASE(5)
+    PF_CASE(6)
+    PF_CASE(7)
+    PF_CASE(8)
+    default: break;
+  }
+#undef PF_CASE
+}
+
+// ---------------------------------------------------------------- combine
+// out[t] = T(T(sum_{i<8} value[9t+i] * score[t,i]) + value[9t+8]) + residual[t], the routed sum
+// in the reference's order (value_0*s_0, then each next product added to the running sum).
+// One block of 256 threads per row, 8 columns per thread per pass.
+__global__ __launch_bounds__(256) void pf_combine_kernel(const uint16_t* __restrict__ values,
+                                                         const float* __restrict__ scores,
+                                                         const uint16_t* __restrict__ residual, int h,
+                                                         uint16_t* __restrict__ out) {
+  const int64_t r = blockIdx.x;
+  float sc[8];
+#pragma unroll
+  for (int j = 0; j < 8; j++) sc[j] = scores[r * 8 + j];
+  for (int c = threadIdx.x * 8; c < h; c += 256 * 8) {
+    u32x4 y[9];
+#pragma unroll
+    for (int j = 0; j < 9; j++) y[j] = *reinterpret_cast<const u32x4*>(values + (r * 9 + j) * h + c);
+    const u32x4 rv = *reinterpret_cast<const u32x4*>(residual + r * h + c);
+    u32x4 o;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      float res2[2];
+#pragma unroll
+      for (int hh = 0; hh < 2; hh++) {
+        auto val = [&](int j) { return bf16_to_f32((uint16_t)(hh ? (y[j][q] >> 16) : (y[j][q] & 0xFFFFu))); };
+        float tot = val(0) * sc[0] + 0.0f;
+#pragma unroll
+        for (int j = 1; j < 8; j++) tot = (val(j) * sc[j] + 0.0f) + tot;
+        const float comb = round_bf16(round_bf16(tot) + val(8));
+        const float resv = bf16_to_f32((uint16_t)(hh ? (rv[q] >> 16) : (rv[q] & 0xFFFFu)));
+        res2[hh] = resv + comb;
+      }
+      o[q] = (uint32_t)f32_to_bf16(res2[0]) | ((uint32_t)f32_to_bf16(res2[1]) << 16);
+    }
+    *reinterpret_cast<u32x4*>(out + r * h + c) = o;
+  }
+}
+
+// ---------------------------------------------------------------- workspace
+struct PfWorkspace {
+  float* logits;      // [rows][256]
+  uint32_t* ids;      // [rows][9]
+  float* scores;      // [rows][8]
+  int32_t* order;     // [n]
+  int32_t* counts;    // [E]
+  int32_t* starts;    // [E]
+  int32_t* blk;       // [3][cap]
+  int32_t* nblk;
+  uint16_t* xhi;      // [rows][h] fp16
+  uint8_t* xq;        // [kPfLo][rows][h] fp8 remainder terms
+  uint8_t* xs;        // [kPfLo][rows][h/32]
+  uint16_t* hhi;      // [n][m] fp16
+  uint8_t* hq;        // [kPfLo][n][m] fp8 remainder terms
+  uint8_t* hs;        // [kPfLo][n][m/32]
+  uint16_t* values;   // [n][h]
+  int cap;
+  size_t bytes;
+};
+
+int pf_cap(int64_t n, int64_t experts) { return (int)(n / kPfItemRows + experts + 1); }
+
+PfWorkspace pf_carve(void* base, int rows, int h, int m, int64_t experts) {
+  PfWorkspace w{};
+  const int64_t n = (int64_t)rows * kSlots;
+  w.cap = pf_cap(n, experts);
+  size_t off = 0;
+  char* p = static_cast<char*>(base);
+  auto take = [&](size_t bytes) { char* r = p ? p + off : nullptr; off += (bytes + 255) & ~(size_t)255; return r; };
+  w.logits = reinterpret_cast<float*>(take((size_t)rows * 256 * 4));
+  w.ids = reinterpret_cast<uint32_t*>(take((size_t)n * 4));
+  w.scores = reinterpret_cast<float*>(take((size_t)rows * 8 * 4));
+  w.order = reinterpret_cast<int32_t*>(take((size_t)n * 4));
+  w.counts = reinterpret_cast<int32_t*>(take((size_t)experts * 4));
+  w.starts = reinterpret_cast<int32_t*>(take((size_t)experts * 4));
+  w.blk = reinterpret_cast<int32_t*>(take((size_t)3 * w.cap * 4));
+  w.nblk = reinterpret_cast<int32_t*>(take(4));
+  w.xhi = reinterpret_cast<uint16_t*>(take((size_t)rows * h * 2));
+  w.xq = reinterpret_cast<uint8_t*>(take((size_t)kPfLo * rows * h));
+  w.xs = reinterpret_cast<uint8_t*>(take((size_t)kPfLo * rows * (h / 32)));
+  w.hhi = reinterpret_cast<uint16_t*>(take((size_t)n * m * 2));
+  w.hq = reinterpret_cast<uint8_t*>(take((size_t)kPfLo * n * m));
+  w.hs = reinterpret_cast<uint8_t*>(take((size_t)kPfLo * n * (m / 32)));
+  w.values = reinterpret_cast<uint16_t*>(take((size_t)n * h * 2));
+  w.bytes = off;
+  return w;
+}
+
+int launch_segment_table(const uint32_t* ids, int n, int experts, int block_rows, int32_t* order, int32_t* counts,
+                         int32_t* starts, int32_t* blk, int cap, int32_t* nblk, hipStream_t s) {
+  hipLaunchKernelGGL(segment_table_kernel, dim3(1), dim3(1024), 0, s, ids, n, experts, block_rows, order, counts,
+                     starts, blk, cap, nblk);
+  MOE_HIP(hipGetLastError());
+  return MOE_OK;
+}
+
+}  // namespace
+}  // namespace moe
+
+using namespace moe;
+
+extern "C" {
+
+int moe_segment_table(const uint32_t* ids, int n, int experts, int block_rows, int32_t* order, int32_t* counts,
+                      int32_t* starts, int32_t* table, int capacity, int32_t* num_blocks, moe_stream_t stream) {
+  MOE_ARG((ids && order) || n == 0, "null ids/order with n > 0");
+  MOE_ARG(counts && starts && table && num_blocks, "null pointer argument");
+  MOE_ARG(n >= 0, "n must be non-negative");
+  MOE_ARG(experts >= 1 && experts <= kPfMaxExperts, "experts must be in 1..%d", kPfMaxExperts);
+  MOE_ARG(block_rows >= 1, "block_rows must be positive");
+  MOE_ARG(capacity >= (int64_t)n / block_rows + experts,
+          "table capacity must be at least n / block_rows + experts (%lld)", (long long)n / block_rows + experts);
+  int rc = ensure_device_ready();
+  if (rc) return rc;
+  return launch_segment_table(ids, n, experts, block_rows, order, counts, starts, table, capacity, num_blocks,
+                              (hipStream_t)stream);
+}
+
+size_t moe_mxfp4_prefill_workspace_bytes(int rows, int hidden, int intermediate, int64_t experts) {
+  if (rows <= 0 || hidden <= 0 || intermediate <= 0 || experts <= 0) return 0;
+  return pf_carve(nullptr, rows, hidden, intermediate, experts).bytes;
+}
+
+int moe_mxfp4_prefill(const uint16_t* x, const uint16_t* residual, int rows, const float* router_w,
+                      const float* bias, const uint8_t* gate_up_codes, const uint8_t* gate_up_scales,
+                      const uint8_t* down_codes, const uint8_t* down_scales, int64_t experts, const uint16_t* unit,
+                      const uint16_t* out_gate, const uint16_t* out_up, const uint16_t* in_down,
+                      const uint16_t* out_down, int hidden, int intermediate, uint16_t* out, uint32_t* indices,
+                      float* scores, void* workspace, size_t workspace_bytes, moe_stream_t stream) {
+  MOE_ARG(x && residual && router_w && bias && gate_up_codes && gate_up_scales && down_codes && down_scales && unit &&
+              out_gate && out_up && in_down && out_down && out,
+          "null pointer argument");
+  MOE_ARG(rows >= 1, "rows must be positive");
+  MOE_ARG(experts == 257, "the routed block needs 256 routed experts plus the shared expert (got %lld)",
+          (long long)experts);
+  MOE_ARG(hidden % 1024 == 0 && hidden > 0, "hidden must be a positive multiple of 1024 (got %d)", hidden);
+  MOE_ARG(intermediate % 128 == 0 && intermediate > 0, "intermediate must be a positive multiple of 128 (got %d)",
+          intermediate);
+  MOE_ARG(workspace != nullptr, "workspace must not be NULL");
+  const PfWorkspace w = pf_carve(workspace, rows, hidden, intermediate, experts);
+  if (workspace_bytes < w.bytes)
+    return fail(MOE_EWORKSPACE, "workspace too small: %zu < %zu bytes", workspace_bytes, w.bytes);
+  int rc = ensure_device_ready();
+  if (rc) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  const int n = rows * kSlots;
+  uint32_t* ids = indices ? indices : w.ids;
+  float* sc = scores ? scores : w.scores;
+  // routing: router GEMV, then top-8 + shared slot per row
+  if ((rc = moe_router_logits(x, router_w, rows, hidden, 256, w.logits, stream))) return rc;
+  if ((rc = moe_route_f32(w.logits, bias, rows, ids, sc, stream))) return rc;
+  // sorted work order in blocks of <= kPfItemRows rows
+  if ((rc = launch_segment_table(ids, n, (int)experts, kPfItemRows, w.order, w.counts, w.starts, w.blk, w.cap,
+                                 w.nblk, s)))
+    return rc;
+  // activation terms
+  const int64_t pwaves = (int64_t)rows * (hidden / 128);
+  hipLaunchKernelGGL(prep_terms_kernel, dim3((unsigned)((pwaves + 3) / 4)), dim3(256), 0, s, x, unit, rows, hidden,
+                     w.xhi, w.xq, w.xs);
+  MOE_HIP(hipGetLastError());
+  // gate/up GEMM + gate finish -> hidden terms
+  PfGemm g{};
+  g.codes = gate_up_codes;
+  g.wscales = gate_up_scales;
+  g.K = hidden;
+  g.N = 2 * intermediate;
+  g.ahi = w.xhi;
+  g.aq = w.xq;
+  g.as = w.xs;
+  g.arows = rows;
+  g.rowmap = w.order;
+  g.rowdiv = kSlots;
+  g.blk = w.blk;
+  g.cap = w.cap;
+  g.nblk = w.nblk;
+  g.order = w.order;
+  g.out_gate = out_gate;
+  g.out_up = out_up;
+  g.in_down = in_down;
+  g.m = intermediate;
+  g.hhi = w.hhi;
+  g.hq = w.hq;
+  g.hs = w.hs;
+  g.nslots = n;
+  hipLaunchKernelGGL(pf_gemm_kernel<true>, dim3((unsigned)(w.cap * (intermediate / 128))), dim3(kPfThreads), 0, s, g);
+  MOE_HIP(hipGetLastError());
+  // down GEMM + value finish -> per-slot values
+  PfGemm d{};
+  d.codes = down_codes;
+  d.wscales = down_scales;
+  d.K = intermediate;
+  d.N = hidden;
+  d.ahi = w.hhi;
+  d.aq = w.hq;
+  d.as = w.hs;
+  d.arows = n;
+  d.rowmap = nullptr;
+  d.rowdiv = 1;
+  d.blk = w.blk;
+  d.cap = w.cap;
+  d.nblk = w.nblk;
+  d.order = w.order;
+  d.m = intermediate;
+  d.out_down = out_down;
+  d.values = w.values;
+  hipLaunchKernelGGL(pf_gemm_kernel<false>, dim3((unsigned)(w.cap * (hidden / 128))), dim3(kPfThreads), 0, s, d);
+  MOE_HIP(hipGetLastError());
+  hipLaunchKernelGGL(pf_combine_kernel, dim3(rows), dim3(256), 0, s, w.values, sc, residual, hidden, out);
+  MOE_HIP(hipGetLastError());
+  return MOE_OK;
+}
+
+}  // extern "C"

@@ -85,3 +85,27 @@ class JoinedMXFP4:
                                              *self._args(), h, self.intermediate, ptr(out[r0:r1]), ptr(ws), ws.numel(),
                                              st))
         return out.reshape(residual.shape)
+
+    def prefill(self, x, residual, router_weight, bias):
+        """A prefill chunk through the routed block: routing, sorted grouped GEMMs on the MX
+        matrix cores, combine (exlr8/joined_mxfp4.py:90-134,148-163 with exlr8/model.py:111-132).
+        Returns (out [rows, h] bf16, indices [rows, 9] int32, scores [rows, 8] f32)."""
+        h = self.hidden
+        if x.dtype != BF16:
+            raise ValueError("this build computes bf16 activations")
+        if self.experts != 257:
+            raise ValueError("the routed block needs 256 routed experts plus the shared expert")
+        require_cuda(x, residual, router_weight, bias)
+        rows = x.numel() // h
+        xr = x.reshape(rows, h).contiguous()
+        res = residual.reshape(rows, h).to(BF16).contiguous()
+        w = router_weight.to(torch.float32).contiguous()
+        b = bias.to(torch.float32).contiguous()
+        out = torch.empty((rows, h), dtype=BF16, device=x.device)
+        ids = torch.empty((rows, 9), dtype=torch.int32, device=x.device)
+        scores = torch.empty((rows, 8), dtype=torch.float32, device=x.device)
+        nbytes = lib().moe_mxfp4_prefill_workspace_bytes(rows, h, self.intermediate, self.experts)
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+        check(lib().moe_mxfp4_prefill(ptr(xr), ptr(res), rows, ptr(w), ptr(b), *self._args(), h, self.intermediate,
+                                      ptr(out), ptr(ids), ptr(scores), ptr(ws), nbytes, stream(x.device)))
+        return out.reshape(residual.shape), ids, scores
