@@ -283,8 +283,59 @@ __device__ __forceinline__ void item_rows(const PfGemm& a, int first, int len, i
   }
 }
 
-// One wave's NT column tiles (cols[j] .. +16) over all K for the item's MT M-tiles.
+// One k step of the MFMAs: activations from the staged buffer, weights from (bw, bs).
 template <int MT, int NT>
+__device__ __forceinline__ void gemm_step(const uint8_t* ab, const uint8_t* sb, const i32x4 (&bw)[NT],
+                                          const uint32_t (&bs)[NT], f32x4 (&acc)[MT][NT]) {
+  const int lane = lane_id(), nn = lane & 15, g = lane >> 4;
+  // the weights widened to fp16 with their block scale: bf[j][b] = codes of byte b
+  f16x2 bf[NT][16];
+#pragma unroll
+  for (int j = 0; j < NT; j++) {
+    const float wsc = __builtin_amdgcn_ldexpf(1.0f, (int)bs[j] - 127);
+    const uint32_t words[4] = {(uint32_t)bw[j].x, (uint32_t)bw[j].y, (uint32_t)bw[j].z, (uint32_t)bw[j].w};
+#pragma unroll
+    for (int wd = 0; wd < 4; wd++) {
+      bf[j][4 * wd + 0] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(words[wd], wsc, 0);
+      bf[j][4 * wd + 1] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(words[wd], wsc, 1);
+      bf[j][4 * wd + 2] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(words[wd], wsc, 2);
+      bf[j][4 * wd + 3] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(words[wd], wsc, 3);
+    }
+  }
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++) {
+    const uint8_t* rp = ab + (mt * 16 + nn) * kPfRowBytes;
+    // hi: 4 fp16 MFMAs, q-th reads k = 32 g + 8 q + i
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const f16x8 ah = *reinterpret_cast<const f16x8*>(rp + (32 * g + 8 * q) * 2);
+#pragma unroll
+      for (int j = 0; j < NT; j++) {
+        const f16x8 bh = pack_f16x8(bf[j][4 * q], bf[j][4 * q + 1], bf[j][4 * q + 2], bf[j][4 * q + 3]);
+        acc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, acc[mt][j], 0, 0, 0);
+      }
+    }
+    // remainder terms: one scaled MX MFMA each on the resident codes
+#pragma unroll
+    for (int t = 0; t < kPfLo; t++) {
+      const i32x4 l0 = *reinterpret_cast<const i32x4*>(rp + 256 + 128 * t + 16 * g);
+      const i32x4 l1 = *reinterpret_cast<const i32x4*>(rp + 256 + 128 * t + 64 + 16 * g);
+      const i32x8 al = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
+      const int asc = sb[((mt * 16 + nn) * kPfLo + t) * 4 + g];
+#pragma unroll
+      for (int j = 0; j < NT; j++) {
+        const i32x8 bv = {bw[j].x, bw[j].y, bw[j].z, bw[j].w, 0, 0, 0, 0};
+        acc[mt][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(al, bv, acc[mt][j], 0, 4, 0, asc, 0,
+                                                                      (int)bs[j]);
+      }
+    }
+  }
+}
+
+// One wave's NT column tiles (cols[j] .. +16) over all K for the item's MT M-tiles.  The weights
+// are prefetched two k steps ahead in two register sets (even and odd steps; K/128 is even), the
+// activations one step ahead in the other LDS buffer.
+template <int MT, int NT, int MTMAX>
 __device__ __forceinline__ void gemm_item(const PfGemm& a, int e, const int (&cols)[NT], const int64_t* rowidx,
                                           uint8_t* abuf, uint8_t* sbuf, f32x4 (&acc)[MT][NT]) {
   const int lane = lane_id(), nn = lane & 15, g = lane >> 4;
@@ -301,77 +352,30 @@ __device__ __forceinline__ void gemm_item(const PfGemm& a, int e, const int (&co
     wrow[j] = a.codes + row * (a.K / 2) + g * 16;
     srow[j] = a.wscales + row * (a.K / 32) + g;
   }
-  constexpr int kStage = PfStage<MT>::kBytes, kSStage = PfStage<MT>::kScaleBytes;
+  constexpr int kStage = PfStage<MTMAX>::kBytes, kSStage = PfStage<MTMAX>::kScaleBytes;
+  auto load_w = [&](i32x4 (&bw)[NT], uint32_t (&bs)[NT], int ks) {
+#pragma unroll
+    for (int j = 0; j < NT; j++) {
+      bw[j] = *reinterpret_cast<const i32x4*>(wrow[j] + ks * 64);
+      bs[j] = srow[j][ks * 4];
+    }
+  };
   stage_k<MT>(a, 0, rowidx, abuf, sbuf);
-  i32x4 bw[NT];
-  uint32_t bs[NT];
-#pragma unroll
-  for (int j = 0; j < NT; j++) {
-    bw[j] = *reinterpret_cast<const i32x4*>(wrow[j]);
-    bs[j] = srow[j][0];
-  }
+  i32x4 b0[NT], b1[NT];
+  uint32_t s0[NT], s1[NT];
+  load_w(b0, s0, 0);
+  load_w(b1, s1, min(1, ksteps - 1));
   __syncthreads();
-  for (int ks = 0; ks < ksteps; ks++) {
-    const int cur = ks & 1;
-    // next step's activations into the other buffer, next step's weights into registers
-    if (ks + 1 < ksteps) stage_k<MT>(a, ks + 1, rowidx, abuf + (cur ^ 1) * kStage, sbuf + (cur ^ 1) * kSStage);
-    i32x4 nbw[NT];
-    uint32_t nbs[NT];
-    const int kn = min(ks + 1, ksteps - 1);
-#pragma unroll
-    for (int j = 0; j < NT; j++) {
-      nbw[j] = *reinterpret_cast<const i32x4*>(wrow[j] + kn * 64);
-      nbs[j] = srow[j][kn * 4];
-    }
-    const uint8_t* ab = abuf + cur * kStage;
-    const uint8_t* sb = sbuf + cur * kSStage;
-    // the weights widened to fp16 with their block scale: bf[j][b] = codes of byte b
-    f16x2 bf[NT][16];
-#pragma unroll
-    for (int j = 0; j < NT; j++) {
-      const float wsc = __builtin_amdgcn_ldexpf(1.0f, (int)bs[j] - 127);
-      const uint32_t words[4] = {(uint32_t)bw[j].x, (uint32_t)bw[j].y, (uint32_t)bw[j].z, (uint32_t)bw[j].w};
-#pragma unroll
-      for (int wd = 0; wd < 4; wd++) {
-        bf[j][4 * wd + 0] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(words[wd], wsc, 0);
-        bf[j][4 * wd + 1] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(words[wd], wsc, 1);
-        bf[j][4 * wd + 2] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(words[wd], wsc, 2);
-        bf[j][4 * wd + 3] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(words[wd], wsc, 3);
-      }
-    }
-#pragma unroll
-    for (int mt = 0; mt < MT; mt++) {
-      const uint8_t* rp = ab + (mt * 16 + nn) * kPfRowBytes;
-      // hi: 4 fp16 MFMAs, q-th reads k = 32 g + 8 q + i
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const f16x8 ah = *reinterpret_cast<const f16x8*>(rp + (32 * g + 8 * q) * 2);
-#pragma unroll
-        for (int j = 0; j < NT; j++) {
-          const f16x8 bh = pack_f16x8(bf[j][4 * q], bf[j][4 * q + 1], bf[j][4 * q + 2], bf[j][4 * q + 3]);
-          acc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, acc[mt][j], 0, 0, 0);
-        }
-      }
-      // remainder terms: one scaled MX MFMA each on the resident codes
-#pragma unroll
-      for (int t = 0; t < kPfLo; t++) {
-        const i32x4 l0 = *reinterpret_cast<const i32x4*>(rp + 256 + 128 * t + 16 * g);
-        const i32x4 l1 = *reinterpret_cast<const i32x4*>(rp + 256 + 128 * t + 64 + 16 * g);
-        const i32x8 al = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
-        const int asc = sb[((mt * 16 + nn) * kPfLo + t) * 4 + g];
-#pragma unroll
-        for (int j = 0; j < NT; j++) {
-          const i32x8 bv = {bw[j].x, bw[j].y, bw[j].z, bw[j].w, 0, 0, 0, 0};
-          acc[mt][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(al, bv, acc[mt][j], 0, 4, 0, asc, 0,
-                                                                        (int)bs[j]);
-        }
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < NT; j++) {
-      bw[j] = nbw[j];
-      bs[j] = nbs[j];
-    }
+  for (int ks = 0; ks < ksteps; ks += 2) {
+    // even step ks (buffer 0): stage ks+1, compute, refill set 0 with ks+2
+    stage_k<MT>(a, ks + 1, rowidx, abuf + kStage, sbuf + kSStage);
+    gemm_step<MT, NT>(abuf, sbuf, b0, s0, acc);
+    load_w(b0, s0, min(ks + 2, ksteps - 1));
+    __syncthreads();
+    // odd step ks+1 (buffer 1): stage ks+2, compute, refill set 1 with ks+3
+    if (ks + 2 < ksteps) stage_k<MT>(a, ks + 2, rowidx, abuf, sbuf);
+    gemm_step<MT, NT>(abuf + kStage, sbuf + kSStage, b1, s1, acc);
+    load_w(b1, s1, min(ks + 3, ksteps - 1));
     __syncthreads();
   }
 }
@@ -379,7 +383,7 @@ __device__ __forceinline__ void gemm_item(const PfGemm& a, int e, const int (&co
 // ---------------------------------------------------------------- gate/up GEMM + gate finish
 // Item = (plan block b, intermediate block c): columns gate [128c, +128) and up [m + 128c, +128);
 // wave w owns gate tile 16w and up tile 16w.
-template <int MT>
+template <int MT, int MTMAX>
 __device__ void gateup_item(const PfGemm& a, int e, int first, int len, int c, uint8_t* abuf, uint8_t* sbuf,
                             int64_t* rowidx, float* ex) {
   const int w = wave_id_uniform(), lane = lane_id(), nn = lane & 15, g = lane >> 4;
@@ -387,7 +391,7 @@ __device__ void gateup_item(const PfGemm& a, int e, int first, int len, int c, u
   __syncthreads();
   const int cols[2] = {128 * c + 16 * w, a.m + 128 * c + 16 * w};
   f32x4 acc[MT][2];
-  gemm_item<MT, 2>(a, e, cols, rowidx, abuf, sbuf, acc);
+  gemm_item<MT, 2, MTMAX>(a, e, cols, rowidx, abuf, sbuf, acc);
   // epilogue per M-tile: gate/up tiles -> LDS [16][2][128] -> per row: H128, scale, SwiGLU, in_down, H128
   const int64_t si = (int64_t)e * a.m + 128 * c + 2 * lane;
   const float og0 = f16_to_f32(a.out_gate[si]), og1 = f16_to_f32(a.out_gate[si + 1]);
@@ -431,7 +435,7 @@ __device__ void gateup_item(const PfGemm& a, int e, int first, int len, int c, u
 
 // ---------------------------------------------------------------- down GEMM + value finish
 // Item = (plan block b, output block ob): columns [128 ob, +128); wave w owns tile 16w.
-template <int MT>
+template <int MT, int MTMAX>
 __device__ void down_item(const PfGemm& a, int e, int first, int len, int ob, uint8_t* abuf, uint8_t* sbuf,
                           int64_t* rowidx, float* ex) {
   const int w = wave_id_uniform(), lane = lane_id(), nn = lane & 15, g = lane >> 4;
@@ -439,7 +443,7 @@ __device__ void down_item(const PfGemm& a, int e, int first, int len, int ob, ui
   __syncthreads();
   const int cols[1] = {128 * ob + 16 * w};
   f32x4 acc[MT][1];
-  gemm_item<MT, 1>(a, e, cols, rowidx, abuf, sbuf, acc);
+  gemm_item<MT, 1, MTMAX>(a, e, cols, rowidx, abuf, sbuf, acc);
   const int64_t si = (int64_t)e * a.N + 128 * ob + 2 * lane;
   const float od0 = f16_to_f32(a.out_down[si]), od1 = f16_to_f32(a.out_down[si + 1]);
 #pragma unroll
@@ -463,27 +467,36 @@ __device__ void down_item(const PfGemm& a, int e, int first, int len, int ob, ui
   }
 }
 
-// Grid: (plan blocks) x (output blocks per item).  LDS: double-buffered activation stage for
-// MT = 8, scale stage, row map, epilogue exchange.
-template <bool GATE>
+// Grid: (plan blocks) x (output blocks per item).  Items of MTMIN..MTMAX M-tiles only (the others
+// exit at once): the small class needs little LDS, so several blocks share a CU.  Dynamic LDS:
+// double-buffered activation stage, scale stage, row map (the epilogue exchange reuses the stage).
+template <int MTMIN, int MTMAX>
+constexpr size_t pf_lds_bytes() {
+  return 2 * PfStage<MTMAX>::kBytes + 2 * PfStage<MTMAX>::kScaleBytes + MTMAX * 16 * sizeof(int64_t);
+}
+
+template <bool GATE, int MTMIN, int MTMAX>
 __global__ __launch_bounds__(kPfThreads) void pf_gemm_kernel(PfGemm a) {
-  __shared__ __attribute__((aligned(16))) uint8_t abuf[2 * PfStage<8>::kBytes];
-  __shared__ __attribute__((aligned(16))) uint8_t sbuf[2 * PfStage<8>::kScaleBytes];
-  __shared__ int64_t rowidx[8 * 16];
-  // the epilogue exchange [16][2][128] f32 reuses the activation stage (free after the k loop)
-  static_assert(2 * PfStage<8>::kBytes >= 16 * 2 * 128 * 4, "exchange buffer must fit in the stage");
+  extern __shared__ __attribute__((aligned(16))) uint8_t pf_lds[];
+  uint8_t* abuf = pf_lds;
+  uint8_t* sbuf = abuf + 2 * PfStage<MTMAX>::kBytes;
+  int64_t* rowidx = reinterpret_cast<int64_t*>(sbuf + 2 * PfStage<MTMAX>::kScaleBytes);
+  static_assert(2 * PfStage<1>::kBytes >= 16 * 2 * 128 * 4, "the epilogue exchange must fit in the stage");
   float* ex = reinterpret_cast<float*>(abuf);
   const int outblocks = GATE ? a.m / 128 : a.N / 128;
   const int b = blockIdx.x / outblocks, ob = blockIdx.x % outblocks;
   if (b >= *a.nblk) return;
   const int e = a.blk[b], first = a.blk[a.cap + b], len = a.blk[2 * a.cap + b];
   const int mt = (len + 15) / 16;
+  if (mt < MTMIN || mt > MTMAX) return;
 #define PF_CASE(M)                                                                          \
   case M:                                                                                   \
-    if (GATE)                                                                               \
-      gateup_item<M>(a, e, first, len, ob, abuf, sbuf, rowidx, ex);                         \
-    else                                                                                    \
-      down_item<M>(a, e, first, len, ob, abuf, sbuf, rowidx, ex);                           \
+    if (M >= MTMIN && M <= MTMAX) {                                                         \
+      if (GATE)                                                                             \
+        gateup_item<(M <= MTMAX ? M : 1), MTMAX>(a, e, first, len, ob, abuf, sbuf, rowidx, ex); \
+      else                                                                                  \
+        down_item<(M <= MTMAX ? M : 1), MTMAX>(a, e, first, len, ob, abuf, sbuf, rowidx, ex);   \
+    }                                                                                       \
     break;
   switch (mt) {
     PF_CASE(1)
@@ -497,6 +510,20 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm_kernel(PfGemm a) {
     default: break;
   }
 #undef PF_CASE
+}
+
+template <bool GATE>
+int launch_pf_gemm(const PfGemm& a, int outblocks, hipStream_t s) {
+  const dim3 grid((unsigned)(a.cap * outblocks)), block(kPfThreads);
+  constexpr size_t small_lds = pf_lds_bytes<1, 2>(), large_lds = pf_lds_bytes<3, 8>();
+  // dynamic LDS beyond 64 KB must be allowed explicitly (idempotent; cheap)
+  MOE_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&pf_gemm_kernel<GATE, 3, 8>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)large_lds));
+  hipLaunchKernelGGL((pf_gemm_kernel<GATE, 1, 2>), grid, block, small_lds, s, a);
+  MOE_HIP(hipGetLastError());
+  hipLaunchKernelGGL((pf_gemm_kernel<GATE, 3, 8>), grid, block, large_lds, s, a);
+  MOE_HIP(hipGetLastError());
+  return MOE_OK;
 }
 
 // ---------------------------------------------------------------- combine
@@ -633,7 +660,7 @@ int moe_mxfp4_prefill(const uint16_t* x, const uint16_t* residual, int rows, con
   MOE_ARG(experts == 257, "the routed block needs 256 routed experts plus the shared expert (got %lld)",
           (long long)experts);
   MOE_ARG(hidden % 1024 == 0 && hidden > 0, "hidden must be a positive multiple of 1024 (got %d)", hidden);
-  MOE_ARG(intermediate % 128 == 0 && intermediate > 0, "intermediate must be a positive multiple of 128 (got %d)",
+  MOE_ARG(intermediate % 256 == 0 && intermediate > 0, "intermediate must be a positive multiple of 256 (got %d)",
           intermediate);
   MOE_ARG(workspace != nullptr, "workspace must not be NULL");
   const PfWorkspace w = pf_carve(workspace, rows, hidden, intermediate, experts);
@@ -681,8 +708,7 @@ int moe_mxfp4_prefill(const uint16_t* x, const uint16_t* residual, int rows, con
   g.hq = w.hq;
   g.hs = w.hs;
   g.nslots = n;
-  hipLaunchKernelGGL(pf_gemm_kernel<true>, dim3((unsigned)(w.cap * (intermediate / 128))), dim3(kPfThreads), 0, s, g);
-  MOE_HIP(hipGetLastError());
+  if ((rc = launch_pf_gemm<true>(g, intermediate / 128, s))) return rc;
   // down GEMM + value finish -> per-slot values
   PfGemm d{};
   d.codes = down_codes;
@@ -702,8 +728,7 @@ int moe_mxfp4_prefill(const uint16_t* x, const uint16_t* residual, int rows, con
   d.m = intermediate;
   d.out_down = out_down;
   d.values = w.values;
-  hipLaunchKernelGGL(pf_gemm_kernel<false>, dim3((unsigned)(w.cap * (hidden / 128))), dim3(kPfThreads), 0, s, d);
-  MOE_HIP(hipGetLastError());
+  if ((rc = launch_pf_gemm<false>(d, hidden / 128, s))) return rc;
   hipLaunchKernelGGL(pf_combine_kernel, dim3(rows), dim3(256), 0, s, w.values, sc, residual, hidden, out);
   MOE_HIP(hipGetLastError());
   return MOE_OK;

@@ -57,42 +57,38 @@ __global__ __launch_bounds__(256) void router_logits_small(const uint16_t* __res
 }
 
 // ---------------------------------------------------------------- logits, prefill batches
-// 64 rows x 64 experts per block, K staged through LDS in fp32, 4x4 outputs per thread.
-__global__ __launch_bounds__(256) void router_logits_tiled(const uint16_t* __restrict__ x,
-                                                           const float* __restrict__ w, int rows, int hidden,
-                                                           int experts, float* __restrict__ logits) {
-  __shared__ float xs[32][64 + 1];
-  __shared__ float ws[32][64 + 1];
-  const int r0 = blockIdx.y * 64, e0 = blockIdx.x * 64;
-  const int tr = threadIdx.x / 16, te = threadIdx.x % 16;
-  float acc[4][4] = {};
-  for (int k0 = 0; k0 < hidden; k0 += 32) {
-    for (int i = threadIdx.x; i < 64 * 32; i += 256) {
-      const int rr = i / 32, kk = i % 32;
-      const int gr = r0 + rr, ge = e0 + rr;
-      xs[kk][rr] = gr < rows ? bf16_to_f32(x[(int64_t)gr * hidden + k0 + kk]) : 0.0f;
-      ws[kk][rr] = ge < experts ? w[(int64_t)ge * hidden + k0 + kk] : 0.0f;
-    }
-    __syncthreads();
+// 16 rows x 16 experts per block on the fp32 matrix cores (v_mfma_f32_16x16x4_f32); the 4 waves
+// split K and their tiles are summed in LDS in wave order.  Lane l = 16 kk + r loads 4 consecutive
+// k of row r of x and of expert r of w; MFMA j takes element j, so its k-group kk covers k0+4kk+j.
+__global__ __launch_bounds__(256) void router_logits_mfma(const uint16_t* __restrict__ x,
+                                                          const float* __restrict__ w, int rows, int hidden,
+                                                          int experts, float* __restrict__ logits) {
+  __shared__ f32x4 red[4][64];
+  const int r0 = blockIdx.y * 16, e0 = blockIdx.x * 16;
+  const int wv = wave_id_uniform(), lane = lane_id(), r = lane & 15, kk = lane >> 4;
+  const int kq = hidden / 4;
+  const uint16_t* __restrict__ xr = x + (int64_t)min(r0 + r, rows - 1) * hidden + wv * kq + 4 * kk;
+  const float* __restrict__ wr = w + (int64_t)min(e0 + r, experts - 1) * hidden + wv * kq + 4 * kk;
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll 4
-    for (int kk = 0; kk < 32; kk++) {
-      float xv[4], wv[4];
+  for (int k = 0; k < kq; k += 16) {
+    const u32x2 xv = *reinterpret_cast<const u32x2*>(xr + k);
+    const f32x4 wvv = *reinterpret_cast<const f32x4*>(wr + k);
+    const float xa[4] = {bf16_to_f32((uint16_t)(xv.x & 0xFFFFu)), bf16_to_f32((uint16_t)(xv.x >> 16)),
+                         bf16_to_f32((uint16_t)(xv.y & 0xFFFFu)), bf16_to_f32((uint16_t)(xv.y >> 16))};
 #pragma unroll
-      for (int i = 0; i < 4; i++) { xv[i] = xs[kk][tr * 4 + i]; wv[i] = ws[kk][te * 4 + i]; }
-#pragma unroll
-      for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = fmaf(xv[i], wv[j], acc[i][j]);
-    }
-    __syncthreads();
+    for (int j = 0; j < 4; j++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[j], wvv[j], acc, 0, 0, 0);
   }
+  red[wv][lane] = acc;
+  __syncthreads();
+  if (wv == 0) {
+    const f32x4 t = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
 #pragma unroll
-  for (int i = 0; i < 4; i++)
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const int gr = r0 + tr * 4 + i, ge = e0 + te * 4 + j;
-      if (gr < rows && ge < experts) logits[(int64_t)gr * experts + ge] = acc[i][j];
+    for (int i = 0; i < 4; i++) {
+      const int row = r0 + 4 * kk + i, e = e0 + r;  // D[4 kk + i][r]
+      if (row < rows && e < experts) logits[(int64_t)row * experts + e] = t[i];
     }
+  }
 }
 
 // ---------------------------------------------------------------- selection
@@ -332,8 +328,8 @@ int launch_router_logits(const uint16_t* x, const float* w, int rows, int hidden
     hipLaunchKernelGGL(router_logits_small<kMaxRows>, dim3(experts), dim3(256), 0, s, x, w, rows, hidden, experts,
                        logits);
   } else {
-    dim3 grid((experts + 63) / 64, (rows + 63) / 64);
-    hipLaunchKernelGGL(router_logits_tiled, grid, dim3(256), 0, s, x, w, rows, hidden, experts, logits);
+    dim3 grid((experts + 15) / 16, (rows + 15) / 16);
+    hipLaunchKernelGGL(router_logits_mfma, grid, dim3(256), 0, s, x, w, rows, hidden, experts, logits);
   }
   MOE_HIP(hipGetLastError());
   return MOE_OK;

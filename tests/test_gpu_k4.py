@@ -71,7 +71,7 @@ def test_route_bit_exact(cuda, orc, rows, case):
     np.testing.assert_array_equal(ids[:, :8], chosen)
 
 
-@pytest.mark.parametrize("rows", [1, 8, 512])
+@pytest.mark.parametrize("rows", [1, 8, 37, 512])
 def test_router_logits(cuda, orc, rows):
     from mlxlr8_amd.fast_router import router_logits
     say(f"case: router logits rows={rows}")
