@@ -1,9 +1,9 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X MoE expert path: one GLM-5.3-style K4 trellis MoE layer, batch-1 decode.
 
-    python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu]
+    python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu] [--config 0..4]
 
-One step = one token through the whole layer (router GEMV, bias-corrected top-8, eight routed
+Default (--config 0): one step = one token through the whole layer (router GEMV, bias-corrected top-8, eight routed
 experts plus the shared expert as K4-trellis decode GEMVs with SwiGLU, weighted combine and
 residual).  Inputs and weights are resident in HBM before timing starts.  Weights of several
 independently seeded layers are rotated (and tokens vary) so consecutive steps stream
@@ -12,6 +12,13 @@ different expert bytes instead of re-reading the 256 MB last-level cache.
 Prints ONE JSON line.  `value` is tokens/s; `us_per_token`, achieved algorithmic HBM GB/s and
 the roofline of the dominant kernel (the fused gate/up decode GEMV, timed with HIP events on
 its own stream) are reported beside it, with the CPU oracle timed on this host's cores.
+
+The other workloads of the same path are measured with --config N (same JSON shape, whole-step
+timing with HIP events):
+  1  joined-MXFP4 layer, batch-1 decode (router + MXFP4 gate_up/down GEMVs + combine)
+  2  8-token speculative-verify batch through the K4 layer (correlated rows, experts deduplicated)
+  3  512-token prefill chunk through the joined-MXFP4 layer (Zipf-skewed routing, grouped GEMMs)
+  4  20 consecutive K4 layers (RMSNorm'd residual each), batch-1 decode
 """
 import argparse
 import json
@@ -45,6 +52,9 @@ def parse():
     p.add_argument("--seed", type=int, default=2026)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--config", type=int, default=0, choices=range(5),
+                   help="workload: 0 K4 b=1 (default), 1 MXFP4 b=1, 2 K4 8-token verify, 3 MXFP4 512-token "
+                        "prefill, 4 20-layer K4 stack")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="also run a plain 1 GiB device copy (reference point for rocprofv3 FETCH/WRITE_SIZE)")
     return p.parse_args()
@@ -98,6 +108,9 @@ def main():
         print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported (this path has no "
               "multi-GPU collectives; see DESIGN.md for how it would shard)", file=sys.stderr)
         sys.exit(2)
+    if args.config != 0:
+        print(json.dumps(OTHER[args.config](args)), flush=True)
+        return
     import torch
     from mlxlr8_amd import synth
     from mlxlr8_amd._lib import lib
@@ -127,32 +140,39 @@ def main():
         step(i)
     torch.cuda.synchronize()
 
-    # timed region: every step also records per-kernel HIP events on the launch stream
-    import ctypes
+    # timed region: K steps, nothing else on the stream
     n = args.steps
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(n)]
-    L = lib()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start.record()
+    for i in range(n):
+        step(args.warmup + i)
+    end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per_step_ms = start.elapsed_time(end) / n
+    us_tok = per_step_ms * 1e3
+
+    # per-kernel durations: a second pass that records HIP events on the launch stream between the
+    # layer's kernels (the events add gaps, so this pass is not the headline time)
+    import ctypes
+    ne = min(n, 100)
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(ne)]
+    L = lib()
     # torch creates an event's HIP handle on its first record(): record each once first
     for row in evs:
         for e in row:
             e.record()
     handles = [(ctypes.c_void_p * 4)(*[ctypes.c_void_p(e.cuda_event) for e in row]) for row in evs]
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    start.record()
-    for i in range(n):
+    for i in range(ne):
         L.moe_profile_events(handles[i], 4)
-        step(args.warmup + i)
-    end.record()
+        step(args.warmup + n + i)
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms = start.elapsed_time(end)
-    per_step_ms = ms / n
-    us_tok = per_step_ms * 1e3
-    router_us = sum(evs[i][0].elapsed_time(evs[i][1]) for i in range(n)) / n * 1e3
-    gateup_us = sum(evs[i][1].elapsed_time(evs[i][2]) for i in range(n)) / n * 1e3
-    down_us = sum(evs[i][2].elapsed_time(evs[i][3]) for i in range(n)) / n * 1e3
+    router_us = sum(evs[i][0].elapsed_time(evs[i][1]) for i in range(ne)) / ne * 1e3
+    gateup_us = sum(evs[i][1].elapsed_time(evs[i][2]) for i in range(ne)) / ne * 1e3
+    down_us = sum(evs[i][2].elapsed_time(evs[i][3]) for i in range(ne)) / ne * 1e3
     achieved = BYTES_GATEUP / (gateup_us * 1e-6) / 1e9
     hbm = BYTES_TOKEN / (us_tok * 1e-6) / 1e9
     traffic = traffic_from_profiles()
@@ -181,7 +201,7 @@ def main():
         "hbm_frac": round(hbm / HBM_PEAK_GBPS, 4),
         "bytes_per_token": BYTES_TOKEN,
         "kernels_us": {"router": round(router_us, 2), "gate_up": round(gateup_us, 2), "down": round(down_us, 2)},
-        "roofline": {"kernel": "k4_gemv_kernel<prep,gate> (fused gate/up decode GEMV, 9 experts)",
+        "roofline": {"kernel": "k4_mfma_kernel<0,0,1,...> (fused gate/up decode GEMV, 9 experts)",
                      "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "algorithmic_bytes": BYTES_GATEUP},
@@ -197,6 +217,148 @@ def main():
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(raw[0], w, bias, xs, rs, args.cpu_seconds)
     print(json.dumps(result), flush=True)
+
+
+def _time_steps(step, steps, warmup):
+    """HIP events around `steps` calls of step(i) after `warmup` untimed ones; ms per step."""
+    import torch
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        step(warmup + i)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def _line(args, value, unit, ms, dtype, workload, extra, algo_bytes, kernel):
+    gbps = algo_bytes / (ms * 1e-3) / 1e9
+    out = {
+        "metric": METRIC, "value": round(value, 2), "unit": unit, "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": dtype, "data": "synthetic",
+        "config": dict({"workload": workload, "parallelism": "none (1 GPU)", "seed": args.seed}, **extra),
+        "roofline": {"kernel": kernel, "bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "algorithmic_bytes": int(algo_bytes)},
+    }
+    return out
+
+
+MX_EXPERT_BYTES = 2 * M * H // 2 + 2 * M * H // 32 + H * M // 2 + H * M // 32   # 20,054,016
+
+
+def _mx_layers(dev, seed, n):
+    from mlxlr8_amd import synth
+    from mlxlr8_amd.joined_mxfp4 import JoinedMXFP4
+    out = []
+    for i in range(n):
+        L = synth.mxfp4_layer(dev, seed + 31 * i)
+        side = L["side"]
+        out.append(JoinedMXFP4(L["weights"], L["unit"], {"gate": (None, side["out_gate"]), "up": (None, side["out_up"]),
+                                                         "down": (side["in_down"], side["out_down"])}, H, M))
+    return out
+
+
+def bench_mxfp4_decode(args):
+    import torch
+    from mlxlr8_amd import synth
+    dev = torch.device("cuda:0")
+    layers = _mx_layers(dev, args.seed, min(args.layers, 3))
+    w, bias = synth.router(dev, args.seed)
+    toks = [synth.activations(dev, args.seed + 1000 + t, 1) for t in range(args.tokens)]
+    calls = [[l.prepare_decode(x, r, w, bias) for (x, r) in toks] for l in layers]
+    ms = _time_steps(lambda i: calls[i % len(calls)][i % len(toks)].run(), args.steps, args.warmup)
+    algo = 9 * MX_EXPERT_BYTES + 256 * H * 4 + 9 * (3 * M + H) * 2 + H * 2 + 256 * 4 + 3 * H * 2
+    return dict(_line(args, 1e3 / ms, "tokens/s", ms, "f32",
+                      "GLM-5.3-style joined-MXFP4 MoE layer, batch-1 decode: hidden 6144, 256 routed + 1 shared, "
+                      "top-8, intermediate 2048 (e2m1 + e8m0 per 32), bf16 activations, fp32 accumulate",
+                      {"global_batch": 1, "seq_len": 1, "layers_rotated": len(layers)}, algo,
+                      "whole step: router + mx_gemv gate_up + mx_gemv down/combine"),
+                us_per_token=round(ms * 1e3, 2))
+
+
+def bench_k4_verify(args):
+    import torch
+    from mlxlr8_amd import synth
+    from mlxlr8_amd.experts import ExpertLayer
+    dev = torch.device("cuda:0")
+    layers = [ExpertLayer(**{k: v for k, v in synth.k4_layer(dev, args.seed + 17 * i).items()}, hidden=H,
+                          intermediate=M) for i in range(min(args.layers, 3))]
+    w, bias = synth.router(dev, args.seed)
+    batches = [synth.activations(dev, args.seed + 2000 + t, 8, correlated=True) for t in range(4)]
+    calls = [[l.prepare_decode(x, r, w, bias) for (x, r) in batches] for l in layers]
+    for c in calls[0]:
+        c.run()
+    torch.cuda.synchronize()
+    uniq = [len(set(c.ids.cpu().numpy().ravel().tolist())) for c in calls[0]]
+    U = sum(uniq) / len(uniq)
+    ms = _time_steps(lambda i: calls[i % len(calls)][i % len(batches)].run(), args.steps, args.warmup)
+    algo = U * (3 * TRELLIS + 3 * (H + M) * 2) + 256 * H * 4 + 256 * 4 + 8 * 3 * H * 2
+    return dict(_line(args, 8e3 / ms, "tokens/s", ms, "f32",
+                      "8-token speculative-verify batch through the K4-trellis MoE layer (correlated rows, "
+                      "distinct experts streamed once)",
+                      {"global_batch": 8, "seq_len": 1, "distinct_experts": U, "layers_rotated": len(layers)},
+                      algo, "whole step: router + k4_mfma_kernel gate/up + down/combine"),
+                us_per_step=round(ms * 1e3, 2))
+
+
+def bench_prefill(args):
+    import torch
+    from mlxlr8_amd import synth
+    dev = torch.device("cuda:0")
+    layers = _mx_layers(dev, args.seed, 2)
+    w, bias = synth.router(dev, args.seed + 1, zipf=True)
+    x, res = synth.activations(dev, args.seed + 3000, 512)
+    _, ids, _ = layers[0].prefill(x, res, w, bias)
+    torch.cuda.synchronize()
+    touched = len(set(ids.cpu().numpy().ravel().tolist()))
+    steps = max(1, min(args.steps, 40))
+    ms = _time_steps(lambda i: layers[i % 2].prefill(x, res, w, bias), steps, min(args.warmup, 5))
+    algo = touched * MX_EXPERT_BYTES + 256 * H * 4 + 3 * 512 * H * 2
+    out = _line(args, 512e3 / ms, "tokens/s", ms, "f32",
+                "512-token prefill chunk through the joined-MXFP4 MoE layer (Zipf(1.1)-skewed routing, "
+                "sort-by-expert grouped GEMMs on the MX matrix cores, weighted combine)",
+                {"global_batch": 512, "seq_len": 512, "touched_experts": touched}, algo,
+                "whole step: router + sort + grouped gate_up/down GEMMs + combine")
+    out["steps"] = steps
+    flops = 512 * 9 * 3 * 2 * H * M
+    out["mfma_util_fp4_peak"] = round(flops / (ms * 1e-3) / 10.1e15, 4)
+    return out
+
+
+def bench_stack(args):
+    import torch
+    from mlxlr8_amd import synth
+    from mlxlr8_amd.experts import ExpertLayer
+    dev = torch.device("cuda:0")
+    n = 20
+    calls, x = [], synth.activations(dev, args.seed + 4000, 1)[0].contiguous()
+    for i in range(n):
+        lay = ExpertLayer(**synth.k4_layer(dev, args.seed + 101 * i), hidden=H, intermediate=M)
+        w, bias = synth.router(dev, args.seed + 101 * i, zipf=True)
+        g = torch.Generator(device=dev)
+        g.manual_seed(args.seed + 7 * i)
+        norm = (0.5 + torch.rand(H, generator=g, device=dev)).to(torch.bfloat16)
+        c = lay.prepare_layer_decode(x, norm, w, bias)
+        calls.append(c)
+        x = c.out
+    steps = max(1, min(args.steps, 50))
+    ms = _time_steps(lambda i: [c.run() for c in calls], steps, min(args.warmup, 5))
+    algo = n * (BYTES_TOKEN + H * 2)
+    out = _line(args, 1e3 / ms, "tokens/s", ms, "f32",
+                "20 consecutive GLM-5.3-style K4-trellis MoE layers (independent seeded weights, Zipf-skewed "
+                "router biases, RMSNorm'd residual per layer), batch-1 decode",
+                {"global_batch": 1, "seq_len": 1, "layers": n}, algo, "whole step: 20 x (router+norm, gate/up, down)")
+    out["steps"] = steps
+    out["us_per_token_stack"] = round(ms * 1e3, 2)
+    return out
+
+
+OTHER = {1: bench_mxfp4_decode, 2: bench_k4_verify, 3: bench_prefill, 4: bench_stack}
 
 
 if __name__ == "__main__":

@@ -155,7 +155,19 @@ int moe_mxfp4_mlp_finish(const uint16_t* x, const uint32_t* ids, const float* sc
                          const uint16_t* in_down, const uint16_t* out_down, int hidden, int intermediate,
                          uint16_t* out, void* workspace, size_t workspace_bytes, moe_stream_t stream);
 
-/* Workspace bytes for the two MXFP4 entry points above. */
+/* Router GEMV + route (as moe_k4_moe_decode) + joined-MXFP4 MLP + combine for 1..8 decode rows in
+ * one call; indices [rows, 9] and scores [rows, 8] may be NULL (kept in the workspace).
+ * Replaces: exlr8/fast_router.py:27-37 compiled_finish with the joined-MXFP4 experts
+ *           (exlr8/joined_mxfp4.py:148-163 JoinedMXFP4.finish; exlr8/model.py:406-418). */
+int moe_mxfp4_moe_decode(const uint16_t* x, const uint16_t* residual, int rows, const float* router_w,
+                         const float* bias, const uint8_t* gate_up_codes, const uint8_t* gate_up_scales,
+                         const uint8_t* down_codes, const uint8_t* down_scales, int64_t experts,
+                         const uint16_t* unit, const uint16_t* out_gate, const uint16_t* out_up,
+                         const uint16_t* in_down, const uint16_t* out_down, int hidden, int intermediate,
+                         uint16_t* out, uint32_t* indices, float* scores, void* workspace, size_t workspace_bytes,
+                         moe_stream_t stream);
+
+/* Workspace bytes for the three MXFP4 decode entry points above. */
 size_t moe_mxfp4_workspace_bytes(int hidden, int intermediate);
 
 /* ---------------------------------------------------------------- profiling */

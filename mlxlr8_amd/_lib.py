@@ -42,6 +42,8 @@ _SIGNATURES = {
                       + [_I32, _I32, _VP, _VP, _SZ, _VP]),
     "moe_mxfp4_mlp_finish": (_I32, [_VP, _VP, _VP, _VP, _I32, _VP, _VP, _VP, _VP, _I64] + [_VP] * 5
                              + [_I32, _I32, _VP, _VP, _SZ, _VP]),
+    "moe_mxfp4_moe_decode": (_I32, [_VP, _VP, _I32, _VP, _VP, _VP, _VP, _VP, _VP, _I64] + [_VP] * 5
+                             + [_I32, _I32, _VP, _VP, _VP, _VP, _SZ, _VP]),
     "moe_mxfp4_workspace_bytes": (_SZ, [_I32, _I32]),
     "moe_segment_table": (_I32, [_VP, _I32, _I32, _I32, _VP, _VP, _VP, _VP, _I32, _VP, _VP]),
     "moe_mxfp4_prefill": (_I32, [_VP, _VP, _I32, _VP, _VP, _VP, _VP, _VP, _VP, _I64] + [_VP] * 5

@@ -254,6 +254,11 @@ struct MxWorkspace {
   int32_t* counter_grp;  // [72 * 16] / [48]
   float* rowout;         // [72][max(2m, h)]
   float* hidden;         // [72][m]
+  Plan* plan;            // decode block: router plan (unused by the MXFP4 kernels)
+  int32_t* router_counter;
+  float* logits;         // [8][256]
+  uint32_t* ids;         // [8][9]
+  float* scores;         // [8][8]
   size_t bytes;
 };
 
@@ -267,6 +272,11 @@ MxWorkspace mx_carve(void* base, int h, int m) {
   w.counter_grp = reinterpret_cast<int32_t*>(take((size_t)kMaxUnits * (rowmax / 128) * 4));
   w.rowout = reinterpret_cast<float*>(take((size_t)kMaxUnits * rowmax * 4));
   w.hidden = reinterpret_cast<float*>(take((size_t)kMaxUnits * m * 4));
+  w.plan = reinterpret_cast<Plan*>(take(sizeof(Plan)));
+  w.router_counter = reinterpret_cast<int32_t*>(take(256));
+  w.logits = reinterpret_cast<float*>(take((size_t)kMaxRows * 256 * 4));
+  w.ids = reinterpret_cast<uint32_t*>(take((size_t)kMaxRows * kSlots * 4));
+  w.scores = reinterpret_cast<float*>(take((size_t)kMaxRows * 8 * 4));
   w.bytes = off;
   return w;
 }
@@ -361,6 +371,34 @@ int moe_mxfp4_mlp_finish(const uint16_t* x, const uint32_t* ids, const float* sc
   return mx_common(x, ids, scores, residual, rows, kSlots, gate_up_codes, gate_up_scales, down_codes, down_scales,
                    experts, unit, out_gate, out_up, in_down, out_down, hidden, intermediate, nullptr, out, workspace,
                    workspace_bytes, (hipStream_t)stream);
+}
+
+// Router GEMV + route + joined-MXFP4 MLP + combine for decode rows in one call.
+int moe_mxfp4_moe_decode(const uint16_t* x, const uint16_t* residual, int rows, const float* router_w,
+                         const float* bias, const uint8_t* gate_up_codes, const uint8_t* gate_up_scales,
+                         const uint8_t* down_codes, const uint8_t* down_scales, int64_t experts,
+                         const uint16_t* unit, const uint16_t* out_gate, const uint16_t* out_up,
+                         const uint16_t* in_down, const uint16_t* out_down, int hidden, int intermediate,
+                         uint16_t* out, uint32_t* indices, float* scores, void* workspace, size_t workspace_bytes,
+                         moe_stream_t stream) {
+  MOE_ARG(x && residual && router_w && bias && out && workspace, "null pointer argument");
+  MOE_ARG(rows >= 1 && rows <= kMaxRows, "rows must be in 1..%d", kMaxRows);
+  MOE_ARG(experts == 257, "the routed decode block needs 256 routed experts plus the shared expert (got %lld)",
+          (long long)experts);
+  MOE_ARG(hidden > 0 && intermediate > 0, "hidden and intermediate must be positive");
+  MxWorkspace w = mx_carve(nullptr, hidden, intermediate);
+  if (workspace_bytes < w.bytes) return fail(MOE_EWORKSPACE, "workspace too small: %zu < %zu", workspace_bytes, w.bytes);
+  int rc = ensure_device_ready();
+  if (rc) return rc;
+  w = mx_carve(workspace, hidden, intermediate);
+  const hipStream_t s = (hipStream_t)stream;
+  uint32_t* ids = indices ? indices : w.ids;
+  float* sc = scores ? scores : w.scores;
+  rc = moe_router_fused_plan(x, router_w, bias, rows, hidden, 257, w.logits, ids, sc, w.plan, w.router_counter, s);
+  if (rc) return rc;
+  return mx_common(x, ids, sc, residual, rows, kSlots, gate_up_codes, gate_up_scales, down_codes, down_scales, experts,
+                   unit, out_gate, out_up, in_down, out_down, hidden, intermediate, nullptr, out, workspace,
+                   workspace_bytes, s);
 }
 
 }  // extern "C"

@@ -5,6 +5,8 @@ Gate and up of every expert are one ``[2m, h]`` MXFP4 matrix (e2m1 codes, one e8
 slots share ``xh = H128(x * unit)``.  ``slots`` returns per-slot expert values and ``finish``
 the combined layer output; both run in ``libmoe_mi355x.so``.
 """
+from types import SimpleNamespace
+
 import torch
 
 from ._lib import check, lib, ptr, require_cuda, stream, workspace
@@ -85,6 +87,42 @@ class JoinedMXFP4:
                                              *self._args(), h, self.intermediate, ptr(out[r0:r1]), ptr(ws), ws.numel(),
                                              st))
         return out.reshape(residual.shape)
+
+    def prepare_decode(self, x, residual, router_weight, bias):
+        """Bind device buffers once and return a callable that enqueues router GEMV + route +
+        MXFP4 MLP + combine for <= 8 decode rows in one C call (exlr8/fast_router.py:27-37 with the
+        joined experts); results land in `.out`, `.ids`, `.scores`."""
+        h = self.hidden
+        rows = x.numel() // h
+        if rows < 1 or rows > 8 or self.experts != 257 or x.dtype != BF16:
+            raise ValueError("prepare_decode needs 1..8 bf16 rows and 256 routed + 1 shared experts")
+        require_cuda(x, residual, router_weight, bias)
+        call = SimpleNamespace()
+        call.x = x.reshape(rows, h).contiguous()
+        call.residual = residual.reshape(rows, h).to(BF16).contiguous()
+        call.w = router_weight.to(torch.float32).contiguous()
+        call.bias = bias.to(torch.float32).contiguous()
+        call.out = torch.empty((rows, h), dtype=BF16, device=x.device)
+        call.ids = torch.empty((rows, 9), dtype=torch.int32, device=x.device)
+        call.scores = torch.empty((rows, 8), dtype=torch.float32, device=x.device)
+        ws = workspace(x.device, h, self.intermediate, "mxfp4")
+        args = (ptr(call.x), ptr(call.residual), rows, ptr(call.w), ptr(call.bias), *self._args(), h,
+                self.intermediate, ptr(call.out), ptr(call.ids), ptr(call.scores), ptr(ws), ws.numel(),
+                stream(x.device))
+        fn = lib().moe_mxfp4_moe_decode
+
+        def run():
+            check(fn(*args))
+            return call.out
+
+        call.run = run
+        return call
+
+    def decode_block(self, x, residual, router_weight, bias):
+        """One-shot form of prepare_decode: returns (out, indices [rows, 9], scores [rows, 8])."""
+        call = self.prepare_decode(x, residual, router_weight, bias)
+        call.run()
+        return call.out.reshape(residual.shape), call.ids, call.scores
 
     def prefill(self, x, residual, router_weight, bias):
         """A prefill chunk through the routed block: routing, sorted grouped GEMMs on the MX

@@ -91,3 +91,33 @@ def test_mxfp4_config1_full_layer(cuda, orc):
     err = rel_l2(bits_to_f32(bf16_bits(out)), bits_to_f32(want))
     say(f"  rel_l2={err:.3e}")
     assert err <= 1e-3
+
+
+def test_mxfp4_decode_block_one_call(cuda, orc):
+    """Router + route + MXFP4 MLP + combine in one library call, rows 1 and 8 (config 1 path)."""
+    from mlxlr8_amd import synth
+    say("case: mxfp4 decode block (one call) rows=1,8")
+    joined, host = _layer(cuda, 257, 515)
+    w, bias = synth.router(cuda, 515)
+    for rows in (1, 8):
+        x, res = synth.activations(cuda, 516 + rows, rows)
+        out, ids, scores = joined.decode_block(x, res, w, bias)
+        torch.cuda.synchronize()
+        logits = orc.router_logits(bf16_bits(x), w.cpu().numpy())
+        oids, _ = orc.route(logits, bias.cpu().numpy())
+        got_ids = ids.cpu().numpy().astype(np.uint32)
+        mism = (got_ids != oids).any(axis=1)
+        if mism.any():
+            sig = 1 / (1 + np.exp(-logits.astype(np.float64)))
+            choice = sig + bias.cpu().numpy()
+            for r in np.where(mism)[0]:
+                srt = np.sort(choice[r])[::-1]
+                assert srt[7] - srt[8] < 1e-5, f"row {r}: routing differs without a near tie"
+        want, _ = _oracle(orc, host, x, got_ids, scores.cpu().numpy(), bf16_bits(res))
+        got = bits_to_f32(bf16_bits(out))
+        r = bits_to_f32(bf16_bits(res))
+        err, err_moe = rel_l2(got, bits_to_f32(want)), rel_l2(got - r, bits_to_f32(want) - r)
+        say(f"  rows={rows} rel_l2={err:.3e} moe-part={err_moe:.3e} routing mismatches={int(mism.sum())}")
+        assert err <= 1e-3 and err_moe <= 1e-2
+        again, _, _ = joined.decode_block(x, res, w, bias)
+        assert torch.equal(out.view(torch.int16), again.view(torch.int16))
