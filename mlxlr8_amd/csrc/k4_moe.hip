@@ -189,7 +189,19 @@ __device__ __forceinline__ uint64_t chunk_offset(int side, uint64_t e, uint32_t 
   return (((e * obs + ob) * it + tk) << 10);
 }
 
-__device__ __forceinline__ int64_t range_start(int64_t n, int w, int nw) { return n * w / nw; }
+// Static split of n work units over nw waves: every wave takes `base` units and the first `rem`
+// waves one more, so a wave's range start is a multiply-add (no division in the finish path).
+struct Split {
+  int base, rem;
+  __device__ __forceinline__ int start(int w) const { return w * base + min(w, rem); }
+  __device__ __forceinline__ bool nonempty(int w) const { return base > 0 || w < rem; }
+  // the wave whose range holds unit c
+  __device__ __forceinline__ int wave_of(int c) const {
+    const int big = rem * (base + 1);
+    return c < big ? c / (base + 1) : rem + (c - big) / base;
+  }
+};
+__device__ __forceinline__ Split make_split(int n, int nw) { return Split{n / nw, n % nw}; }
 
 // Cross-wave hand-off of partial sums inside one launch.  The XCDs' L2 caches are not coherent
 // with each other, and an agent-scope release would write back a whole L2.  Partials are
@@ -219,29 +231,21 @@ __device__ __forceinline__ void counter_reset(int32_t* c) {
   if (lane_id() == 0) __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
-__device__ __forceinline__ int wave_of_chunk(int64_t c, int64_t n, int nw) {
-  int w = (int)((c * nw) / n);
-  while (w + 1 < nw && range_start(n, w + 1, nw) <= c) w++;
-  while (w > 0 && range_start(n, w, nw) > c) w--;
-  return w;
-}
-
 // Partial sums of one segment: the waves overlapping it and, for each, the visit that covers it.
 struct SegWaves {
-  int64_t a;  // first work unit of the segment
+  int a;  // first work unit of the segment
   int wa, wb;
 };
-__device__ __forceinline__ SegWaves seg_waves(int64_t n, int nw, int ups, int seg) {
-  const int64_t a = (int64_t)seg * ups;
-  return SegWaves{a, wave_of_chunk(a, n, nw), wave_of_chunk(a + ups - 1, n, nw)};
+__device__ __forceinline__ SegWaves seg_waves(const Split& sp, int ups, int seg) {
+  const int a = seg * ups;
+  return SegWaves{a, sp.wave_of(a), sp.wave_of(a + ups - 1)};
 }
 // Load the partial pair of wave w for segment sw, token t, columns 2*lane, +1 (zero if the wave
 // has no work there).
-__device__ __forceinline__ f32x2 load_partial(const float* __restrict__ partial, int64_t n, int nw, const SegWaves& sw,
+__device__ __forceinline__ f32x2 load_partial(const float* __restrict__ partial, const Split& sp, const SegWaves& sw,
                                               int w, int t, bool& ok) {
-  const int64_t s = range_start(n, w, nw);
-  ok = w <= sw.wb && range_start(n, w + 1, nw) > s;
-  const int visit = (s >= sw.a) ? 0 : 1;
+  ok = w <= sw.wb && sp.nonempty(w);
+  const int visit = (sp.start(w) >= sw.a) ? 0 : 1;
   const int64_t idx = ok ? ((int64_t)w * 2 + visit) * kPartialStride + (int64_t)t * 128 + 2 * lane_id() : 0;
   return load_coherent2(partial + idx);
 }
@@ -251,16 +255,16 @@ __device__ __forceinline__ f32x2 load_partial(const float* __restrict__ partial,
 // `seg` covers units [seg*ups, (seg+1)*ups) of `n` units split over `nw` waves.  Loads are
 // issued in batches of 16 waves so one memory round trip covers a batch; empty wave ranges
 // contribute nothing.
-__device__ __forceinline__ void sum_partials(const float* __restrict__ partial, int64_t n, int nw, int ups, int seg,
+__device__ __forceinline__ void sum_partials(const float* __restrict__ partial, const Split& sp, int ups, int seg,
                                              int t, float& v0, float& v1) {
-  const SegWaves sw = seg_waves(n, nw, ups, seg);
+  const SegWaves sw = seg_waves(sp, ups, seg);
   v0 = 0.0f;
   v1 = 0.0f;
   for (int w0 = sw.wa; w0 <= sw.wb; w0 += 16) {
     f32x2 p[16];
     bool ok[16];
 #pragma unroll
-    for (int j = 0; j < 16; j++) p[j] = load_partial(partial, n, nw, sw, w0 + j, t, ok[j]);
+    for (int j = 0; j < 16; j++) p[j] = load_partial(partial, sp, sw, w0 + j, t, ok[j]);
 #pragma unroll
     for (int j = 0; j < 16; j++) {
       if (ok[j]) { v0 += p[j].x; v1 += p[j].y; }
@@ -268,9 +272,9 @@ __device__ __forceinline__ void sum_partials(const float* __restrict__ partial, 
   }
 }
 // The same for two segments at once (their loads share round trips).
-__device__ __forceinline__ void sum_partials_pair(const float* __restrict__ partial, int64_t n, int nw, int ups,
+__device__ __forceinline__ void sum_partials_pair(const float* __restrict__ partial, const Split& sp, int ups,
                                                   int seg_a, int seg_b, int t, f32x2& ra, f32x2& rb) {
-  const SegWaves sa = seg_waves(n, nw, ups, seg_a), sb = seg_waves(n, nw, ups, seg_b);
+  const SegWaves sa = seg_waves(sp, ups, seg_a), sb = seg_waves(sp, ups, seg_b);
   ra = f32x2{0.0f, 0.0f};
   rb = f32x2{0.0f, 0.0f};
   for (int k = 0; sa.wa + k <= sa.wb || sb.wa + k <= sb.wb; k += 12) {
@@ -278,8 +282,8 @@ __device__ __forceinline__ void sum_partials_pair(const float* __restrict__ part
     bool oka[12], okb[12];
 #pragma unroll
     for (int j = 0; j < 12; j++) {
-      pa[j] = load_partial(partial, n, nw, sa, sa.wa + k + j, t, oka[j]);
-      pb[j] = load_partial(partial, n, nw, sb, sb.wa + k + j, t, okb[j]);
+      pa[j] = load_partial(partial, sp, sa, sa.wa + k + j, t, oka[j]);
+      pb[j] = load_partial(partial, sp, sb, sb.wa + k + j, t, okb[j]);
     }
 #pragma unroll
     for (int j = 0; j < 12; j++) {
@@ -294,11 +298,11 @@ __device__ __forceinline__ void sum_partials_pair(const float* __restrict__ part
 // segment unlocks (gate finish, per-slot values, or the column-block combine).
 template <int FM>
 __device__ __forceinline__ void complete_visit(const GemvArgs& a, const Plan* __restrict__ P, int seg, int units,
-                                               int ups, int64_t n, int nw, int nproj, int U, int u, int ob, int e,
+                                               int ups, const Split& sp, int nproj, int U, int u, int ob, int e,
                                                int ntok) {
   const int lane = lane_id();
   const int col = ob * 128 + 2 * lane;
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  release_stores();
   if (FM == FIN_GATE) {
     // gate and up of one column block are the adjacent segments 2*grp and 2*grp+1: one counter
     // covers both, and the wave that completes them reduces both and runs the gate finish
@@ -306,17 +310,23 @@ __device__ __forceinline__ void complete_visit(const GemvArgs& a, const Plan* __
     if (counter_add(&a.counter_grp[grp], units) + units != 2 * ups) return;
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     counter_reset(&a.counter_grp[grp]);
+    // side vectors issued with the first partial loads (one round trip)
+    const int64_t si = (int64_t)e * a.out_f + col;
+    const uint32_t og = *reinterpret_cast<const uint32_t*>(a.out_scale[0] + si);
+    const uint32_t ou = *reinterpret_cast<const uint32_t*>(a.out_scale[1] + si);
+    const uint32_t idn = *reinterpret_cast<const uint32_t*>(a.in_down + si);
+    auto lo = [](uint32_t v) { return f16_to_f32((uint16_t)(v & 0xFFFFu)); };
+    auto hi = [](uint32_t v) { return f16_to_f32((uint16_t)(v >> 16)); };
     for (int t = 0; t < ntok; t++) {
       f32x2 g, uu;
-      sum_partials_pair(a.partial, n, nw, ups, 2 * grp, 2 * grp + 1, t, g, uu);
+      sum_partials_pair(a.partial, sp, ups, 2 * grp, 2 * grp + 1, t, g, uu);
       float g0 = g.x, g1 = g.y, u0 = uu.x, u1 = uu.y;
       hadamard128_wave(g0, g1);
       hadamard128_wave(u0, u1);
-      const int64_t si = (int64_t)e * a.out_f + col;
-      float h0 = swiglu_bf16(g0 * f16_to_f32(a.out_scale[0][si]), u0 * f16_to_f32(a.out_scale[1][si]));
-      float h1 = swiglu_bf16(g1 * f16_to_f32(a.out_scale[0][si + 1]), u1 * f16_to_f32(a.out_scale[1][si + 1]));
-      h0 *= f16_to_f32(a.in_down[si]);
-      h1 *= f16_to_f32(a.in_down[si + 1]);
+      float h0 = swiglu_bf16(g0 * lo(og), u0 * lo(ou));
+      float h1 = swiglu_bf16(g1 * hi(og), u1 * hi(ou));
+      h0 *= lo(idn);
+      h1 *= hi(idn);
       hadamard128_wave(h0, h1);
       const int slot = P->slot[u][t];
       *reinterpret_cast<f32x2*>(a.down_xh + (int64_t)slot * a.out_f + col) = f32x2{h0, h1};
@@ -327,29 +337,28 @@ __device__ __forceinline__ void complete_visit(const GemvArgs& a, const Plan* __
   // this wave completed segment `seg`: reduce its partials once
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
   counter_reset(&a.counter_seg[seg]);
+  const int64_t si = (int64_t)e * a.out_f + col;
+  const uint32_t osc = *reinterpret_cast<const uint32_t*>(a.out_scale[0] + si);  // with the partial loads
+  const float os0 = f16_to_f32((uint16_t)(osc & 0xFFFFu)), os1 = f16_to_f32((uint16_t)(osc >> 16));
   if (FM == FIN_VALUES) {
     for (int t = 0; t < ntok; t++) {
       float v0, v1;
-      sum_partials(a.partial, n, nw, ups, seg, t, v0, v1);
+      sum_partials(a.partial, sp, ups, seg, t, v0, v1);
       hadamard128_wave(v0, v1);
-      const int64_t si = (int64_t)e * a.out_f + col;
       const int slot = P->slot[u][t];
-      const uint32_t packed2 = (uint32_t)f32_to_bf16(v0 * f16_to_f32(a.out_scale[0][si])) |
-                               ((uint32_t)f32_to_bf16(v1 * f16_to_f32(a.out_scale[0][si + 1])) << 16);
+      const uint32_t packed2 = (uint32_t)f32_to_bf16(v0 * os0) | ((uint32_t)f32_to_bf16(v1 * os1) << 16);
       *reinterpret_cast<uint32_t*>(a.values + (int64_t)slot * a.out_f + col) = packed2;
     }
   } else {
     // per-slot expert output of this column block: T(H128(inner) * out_scale)
     for (int t = 0; t < ntok; t++) {
       float v0, v1;
-      sum_partials(a.partial, n, nw, ups, seg, t, v0, v1);
+      sum_partials(a.partial, sp, ups, seg, t, v0, v1);
       hadamard128_wave(v0, v1);
-      const int64_t si = (int64_t)e * a.out_f + col;
       const int slot = P->slot[u][t];
-      store_coherent2(a.yslot + (int64_t)slot * a.out_f + col, round_bf16(v0 * f16_to_f32(a.out_scale[0][si])),
-                      round_bf16(v1 * f16_to_f32(a.out_scale[0][si + 1])));
+      store_coherent2(a.yslot + (int64_t)slot * a.out_f + col, round_bf16(v0 * os0), round_bf16(v1 * os1));
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    release_stores();
     if (counter_add(&a.counter_grp[ob], 1) + 1 != U) return;
     // every unit of this column block is done: weighted routed sum, shared, residual
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
@@ -426,17 +435,19 @@ __global__ __launch_bounds__(WV * 64) void k4_mfma_kernel(GemvArgs a) {
   const int wave = blockIdx.x * WV + wave_id_uniform();
   const int lane = lane_id();
   const int g = lane >> 4, nn = lane & 15;
-  const int64_t q_begin = range_start(nq, wave, nw), q_end = range_start(nq, wave + 1, nw);
+  // quad counts fit 32 bits (<= 72 units x 64 column blocks x 2 projections x 1024 quads)
+  const Split sp = make_split((int)nq, nw);
+  const int q_begin = sp.start(wave), q_end = sp.start(wave + 1);
   _Float16* xw = xa + wave_id_uniform() * (2 * 2 * (2 * NT) * 4 * 8);
   // this lane's 16 B inside a chunk: tile 2s + n/8 at +256 s, word group n%8
   const int lane_off = (nn >> 3) * 128 + (nn & 7) * 16;
   const int src_lane = (lane & 7) == 0 ? lane + 7 : lane - 1;
 
   int visit = 0;
-  for (int64_t c = q_begin; c < q_end; visit++) {
-    const int seg = (int)(c / ups);
-    const int tq0 = (int)(c % ups);
-    const int tq1 = (int)min((int64_t)ups, (int64_t)tq0 + (q_end - c));
+  for (int c = q_begin; c < q_end; visit++) {
+    const int seg = c / ups;
+    const int tq0 = c % ups;
+    const int tq1 = min(ups, tq0 + (q_end - c));
     const int proj = seg % nproj;
     const int ob = (seg / nproj) % obs;
     const int u = seg / (nproj * obs);
@@ -594,7 +605,7 @@ __global__ __launch_bounds__(WV * 64) void k4_mfma_kernel(GemvArgs a) {
           }
       }
     }
-    complete_visit<FM>(a, P, seg, tq1 - tq0, ups, nq, nw, nproj, U, u, ob, e, ntok);
+    complete_visit<FM>(a, P, seg, tq1 - tq0, ups, sp, nproj, U, u, ob, e, ntok);
     c += tq1 - tq0;
   }
 }

@@ -396,6 +396,14 @@ __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 __device__ __forceinline__ int wave_id_in_block() { return threadIdx.x >> 6; }
 // The same index as a wave-uniform (scalar) value, so that everything derived from it -- work
 // ranges, loop bounds, segment ids -- lives in scalar registers and loops stay uniform.
+// Publication of write-through stores to other CUs: wait until every earlier store of this wave
+// is acknowledged (gfx9 counts stores in vmcnt; a workgroup-scope release emits no wait), then
+// act as a compiler barrier.  Used before the counter atomic that hands the stored data over.
+__device__ __forceinline__ void release_stores() {
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), expcnt and lgkmcnt not waited on
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+}
+
 __device__ __forceinline__ int wave_id_uniform() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
 }  // namespace moe

@@ -172,7 +172,7 @@ __global__ __launch_bounds__(kMxThreads) void mx_gemv_kernel(MxArgs a) {
     const int nb = n >> 7;
     const int run = (int)(r + 1 - run_start);
     run_start = r + 1;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    release_stores();
     const int cb = s * (N / 128) + nb;
     if (cnt_add(&a.counter_blk[cb], run) + run != 128) continue;
     // 128-row block (s, nb) complete
@@ -218,7 +218,7 @@ __global__ __launch_bounds__(kMxThreads) void mx_gemv_kernel(MxArgs a) {
                           ((uint64_t)__float_as_uint(round_bf16(v1 * f16_to_f32(a.out_down[si + 1]))) << 32);
       __hip_atomic_store(reinterpret_cast<uint64_t*>(a.rowout + (int64_t)s * N + col), pk, __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_SYSTEM);
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+      release_stores();
       if (cnt_add(&a.counter_grp[nb], 1) + 1 != a.slots) continue;
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
       cnt_reset(&a.counter_grp[nb]);

@@ -306,7 +306,7 @@ __global__ __launch_bounds__(256) void router_decode_kernel(const uint16_t* __re
     const float lg = (red[r][0] + red[r][1]) + (red[r][2] + red[r][3]);
     __hip_atomic_store(logits + (int64_t)r * 256 + e, lg, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  release_stores();
   __syncthreads();
   if (threadIdx.x == 0)
     last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) == (int)gridDim.x - 1;
