@@ -106,6 +106,34 @@ __global__ __launch_bounds__(kMxThreads) void mx_gemv_kernel(MxArgs a) {
   const int s0 = (int)(r0 / N);
   const int s1 = (int)((r1 - 1) / N);  // s1 <= s0 + 1 (host guarantees rows per block <= N)
   const int lane = lane_id(), wv = wave_id_in_block();
+  // this wave's rows (row indices fit 32 bits: at most 72 slots x 6144 rows)
+  const int w0 = (int)(r0 + (r1 - r0) * wv / kMxWaves), w1 = (int)(r0 + (r1 - r0) * (wv + 1) / kMxWaves);
+
+  // Weight rows are streamed through a ring of D rows per wave (issued D rows ahead, so D row
+  // loads are in flight while a row is reduced); the first D are issued before the activations
+  // are staged.  Loads past the range re-read its last row, so the ring needs no branch.
+  constexpr int D = KC == 3 ? 2 : 6;
+  u32x4 wr[D][KC];
+  uint32_t sr[D][KC];
+  // experts of the block's (at most two) slots, read once (no scalar-load round trip per row)
+  const int e_s0 = slot_expert(a, s0), e_s1 = slot_expert(a, s1);
+  auto expert_of = [&](int s) { return s == s0 ? e_s0 : e_s1; };
+  auto issue = [&](int j, int r) {
+    const int rr = min(r, w1 - 1);
+    const int s = rr / N, n = rr - s * N;
+    const int e = expert_of(s);
+    const uint8_t* crow = a.codes + ((int64_t)e * N + n) * (K / 2);
+    const uint8_t* srow = a.scales + ((int64_t)e * N + n) * (K / 32);
+#pragma unroll
+    for (int i = 0; i < KC; i++) {
+      wr[j][i] = *reinterpret_cast<const u32x4*>(crow + 1024 * i + 16 * lane);
+      sr[j][i] = srow[64 * i + lane];
+    }
+  };
+  if (w0 < w1) {
+#pragma unroll
+    for (int j = 0; j < D; j++) issue(j, w0 + j);
+  }
 
   // ---- stage the activation rows of the (at most two) slots this block touches
   for (int q = 0; q <= s1 - s0; q++) {
@@ -130,116 +158,138 @@ __global__ __launch_bounds__(kMxThreads) void mx_gemv_kernel(MxArgs a) {
   }
   __syncthreads();
 
-  // ---- this wave's rows
-  const int64_t w0 = r0 + (r1 - r0) * wv / kMxWaves, w1 = r0 + (r1 - r0) * (wv + 1) / kMxWaves;
   float x[KC * 32];
   int cur = -1;
-  int64_t run_start = w0;
-  for (int64_t r = w0; r < w1; r++) {
-    const int s = (int)(r / N);
-    const int n = (int)(r % N);
-    if (s != cur) {
-      cur = s;
-      const float* src = xs[s - s0];
-      // lane holds k = 2048*i + 32*lane + j (static register indices)
+  int run_start = w0, buf_start = w0;
+  float rbuf = 0.0f;
+  for (int rb = w0; rb < w1; rb += D) {
 #pragma unroll
-      for (int i = 0; i < KC; i++)
+    for (int j = 0; j < D; j++) {
+      const int r = rb + j;
+      if (r >= w1) break;
+      const int s = r / N;
+      const int n = r - s * N;
+      if (s != cur) {
+        cur = s;
+        const float* src = xs[s - s0];
+        // lane holds k = 2048*i + 32*lane + j (static register indices)
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-          const f32x4 v = *reinterpret_cast<const f32x4*>(src + 2048 * i + 32 * lane + 4 * j);
-          x[32 * i + 4 * j] = v.x; x[32 * i + 4 * j + 1] = v.y; x[32 * i + 4 * j + 2] = v.z; x[32 * i + 4 * j + 3] = v.w;
-        }
-    }
-    const int e = slot_expert(a, s);
-    const uint8_t* crow = a.codes + ((int64_t)e * N + n) * (K / 2);
-    const uint8_t* srow = a.scales + ((int64_t)e * N + n) * (K / 32);
-    float acc = 0.0f;
+        for (int i = 0; i < KC; i++)
 #pragma unroll
-    for (int i = 0; i < KC; i++) {
-      const u32x4 w = *reinterpret_cast<const u32x4*>(crow + 1024 * i + 16 * lane);
-      const float sc = e8m0_to_f32(srow[64 * i + lane]);
-      acc = dot8_fp4(w.x, sc, x + 32 * i, acc);
-      acc = dot8_fp4(w.y, sc, x + 32 * i + 8, acc);
-      acc = dot8_fp4(w.z, sc, x + 32 * i + 16, acc);
-      acc = dot8_fp4(w.w, sc, x + 32 * i + 24, acc);
-    }
-    acc = wave_sum(acc);
-    if (lane == 63) st_wt(a.rowout + (int64_t)s * N + n, acc);
+          for (int jj = 0; jj < 8; jj++) {
+            const f32x4 v = *reinterpret_cast<const f32x4*>(src + 2048 * i + 32 * lane + 4 * jj);
+            x[32 * i + 4 * jj] = v.x; x[32 * i + 4 * jj + 1] = v.y; x[32 * i + 4 * jj + 2] = v.z;
+            x[32 * i + 4 * jj + 3] = v.w;
+          }
+      }
+      const int e = expert_of(s);
+      float acc = 0.0f;
+#pragma unroll
+      for (int i = 0; i < KC; i++) {
+        const u32x4 w = wr[j][i];
+        const float sc = e8m0_to_f32(sr[j][i]);
+        acc = dot8_fp4(w.x, sc, x + 32 * i, acc);
+        acc = dot8_fp4(w.y, sc, x + 32 * i + 8, acc);
+        acc = dot8_fp4(w.z, sc, x + 32 * i + 16, acc);
+        acc = dot8_fp4(w.w, sc, x + 32 * i + 24, acc);
+      }
+      issue(j, r + D);
+      acc = wave_sum(acc);
+      // row sums are gathered in one register (row r - buf_start in that lane) and stored with one
+      // coalesced write-through store per 64 rows or block end: a store per row would put a
+      // write acknowledgement in front of every later wait on the load ring
+      const float tot = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc), 63));
+      if (lane == r - buf_start) rbuf = tot;
 
-    // close a run at the end of a 128-row block or of the wave's range
-    const bool block_end = ((n & 127) == 127) || (r + 1 == w1);
-    if (!block_end) continue;
-    const int nb = n >> 7;
-    const int run = (int)(r + 1 - run_start);
-    run_start = r + 1;
-    release_stores();
-    const int cb = s * (N / 128) + nb;
-    if (cnt_add(&a.counter_blk[cb], run) + run != 128) continue;
-    // 128-row block (s, nb) complete
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    cnt_reset(&a.counter_blk[cb]);
-    if (MODE == MX_GATEUP) {
-      const int m = N / 2;
-      const int b = nb % (m / 128);
-      const int grp = s * (m / 128) + b;
-      if (cnt_add(&a.counter_grp[grp], 1) + 1 != 2) continue;
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-      cnt_reset(&a.counter_grp[grp]);
-      const int col = b * 128 + 2 * lane;
-      f32x2 g = ld_wt2(a.rowout + (int64_t)s * N + col);
-      f32x2 u = ld_wt2(a.rowout + (int64_t)s * N + m + col);
-      float g0 = g.x, g1 = g.y, u0 = u.x, u1 = u.y;
-      hadamard128_wave(g0, g1);
-      hadamard128_wave(u0, u1);
-      const int64_t si = (int64_t)e * m + col;
-      float h0 = swiglu_bf16(g0 * f16_to_f32(a.out_gate[si]), u0 * f16_to_f32(a.out_up[si]));
-      float h1 = swiglu_bf16(g1 * f16_to_f32(a.out_gate[si + 1]), u1 * f16_to_f32(a.out_up[si + 1]));
-      h0 *= f16_to_f32(a.in_down[si]);
-      h1 *= f16_to_f32(a.in_down[si + 1]);
-      hadamard128_wave(h0, h1);
-      *reinterpret_cast<f32x2*>(a.hidden + (int64_t)s * m + col) = f32x2{h0, h1};
-    } else if (MODE == MX_DOWN_VALUES) {
-      const int col = nb * 128 + 2 * lane;
-      f32x2 v = ld_wt2(a.rowout + (int64_t)s * N + col);
-      float v0 = v.x, v1 = v.y;
-      hadamard128_wave(v0, v1);
-      const int64_t si = (int64_t)e * N + col;
-      const uint32_t pk = (uint32_t)f32_to_bf16(v0 * f16_to_f32(a.out_down[si])) |
-                          ((uint32_t)f32_to_bf16(v1 * f16_to_f32(a.out_down[si + 1])) << 16);
-      *reinterpret_cast<uint32_t*>(a.values + (int64_t)s * N + col) = pk;
-    } else {
-      // per-slot bf16 value of this block, then the block's combine once every slot is done
-      const int col = nb * 128 + 2 * lane;
-      f32x2 v = ld_wt2(a.rowout + (int64_t)s * N + col);
-      float v0 = v.x, v1 = v.y;
-      hadamard128_wave(v0, v1);
-      const int64_t si = (int64_t)e * N + col;
-      const uint64_t pk = (uint64_t)__float_as_uint(round_bf16(v0 * f16_to_f32(a.out_down[si]))) |
-                          ((uint64_t)__float_as_uint(round_bf16(v1 * f16_to_f32(a.out_down[si + 1]))) << 32);
-      __hip_atomic_store(reinterpret_cast<uint64_t*>(a.rowout + (int64_t)s * N + col), pk, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_SYSTEM);
+      // close a run at the end of a 128-row block or of the wave's range
+      const bool block_end = ((n & 127) == 127) || (r + 1 == w1);
+      if (block_end || r - buf_start == 63) {
+        if (lane <= r - buf_start) st_wt(a.rowout + buf_start + lane, rbuf);  // rowout index of row r is r
+        buf_start = r + 1;
+      }
+      if (!block_end) continue;
+      const int nb = n >> 7;
+      const int run = r + 1 - run_start;
+      run_start = r + 1;
       release_stores();
-      if (cnt_add(&a.counter_grp[nb], 1) + 1 != a.slots) continue;
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-      cnt_reset(&a.counter_grp[nb]);
-      const int rows = a.slots / kSlots;
-      for (int rr = 0; rr < rows; rr++) {
-        f32x2 y[kSlots];
+      if (MODE == MX_GATEUP) {
+        // gate rows [0, m) and up rows [m, 2m): the 256 rows of column block b share one counter
+        const int m = N / 2;
+        const int b = nb % (m / 128);
+        const int grp = s * (m / 128) + b;
+        const int col = b * 128 + 2 * lane;
+        const int64_t si = (int64_t)e * m + col;
+        const uint32_t og = *reinterpret_cast<const uint32_t*>(a.out_gate + si);
+        const uint32_t ou = *reinterpret_cast<const uint32_t*>(a.out_up + si);
+        const uint32_t idn = *reinterpret_cast<const uint32_t*>(a.in_down + si);
+        if (cnt_add(&a.counter_grp[grp], run) + run != 256) continue;
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        cnt_reset(&a.counter_grp[grp]);
+        f32x2 g = ld_wt2(a.rowout + (int64_t)s * N + col);
+        f32x2 u = ld_wt2(a.rowout + (int64_t)s * N + m + col);
+        float g0 = g.x, g1 = g.y, u0 = u.x, u1 = u.y;
+        hadamard128_wave(g0, g1);
+        hadamard128_wave(u0, u1);
+        auto lo = [](uint32_t v) { return f16_to_f32((uint16_t)(v & 0xFFFFu)); };
+        auto hi = [](uint32_t v) { return f16_to_f32((uint16_t)(v >> 16)); };
+        float h0 = swiglu_bf16(g0 * lo(og), u0 * lo(ou));
+        float h1 = swiglu_bf16(g1 * hi(og), u1 * hi(ou));
+        h0 *= lo(idn);
+        h1 *= hi(idn);
+        hadamard128_wave(h0, h1);
+        *reinterpret_cast<f32x2*>(a.hidden + (int64_t)s * m + col) = f32x2{h0, h1};
+      } else if (MODE == MX_DOWN_VALUES) {
+        const int cb = s * (N / 128) + nb;
+        if (cnt_add(&a.counter_blk[cb], run) + run != 128) continue;
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        cnt_reset(&a.counter_blk[cb]);
+        const int col = nb * 128 + 2 * lane;
+        f32x2 v = ld_wt2(a.rowout + (int64_t)s * N + col);
+        float v0 = v.x, v1 = v.y;
+        hadamard128_wave(v0, v1);
+        const int64_t si = (int64_t)e * N + col;
+        const uint32_t pk = (uint32_t)f32_to_bf16(v0 * f16_to_f32(a.out_down[si])) |
+                            ((uint32_t)f32_to_bf16(v1 * f16_to_f32(a.out_down[si + 1])) << 16);
+        *reinterpret_cast<uint32_t*>(a.values + (int64_t)s * N + col) = pk;
+      } else {
+        // per-slot bf16 value of this block, then the block's combine once every slot is done
+        const int cb = s * (N / 128) + nb;
+        if (cnt_add(&a.counter_blk[cb], run) + run != 128) continue;
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        cnt_reset(&a.counter_blk[cb]);
+        const int col = nb * 128 + 2 * lane;
+        f32x2 v = ld_wt2(a.rowout + (int64_t)s * N + col);
+        float v0 = v.x, v1 = v.y;
+        hadamard128_wave(v0, v1);
+        const int64_t si = (int64_t)e * N + col;
+        const uint64_t pk = (uint64_t)__float_as_uint(round_bf16(v0 * f16_to_f32(a.out_down[si]))) |
+                            ((uint64_t)__float_as_uint(round_bf16(v1 * f16_to_f32(a.out_down[si + 1]))) << 32);
+        __hip_atomic_store(reinterpret_cast<uint64_t*>(a.rowout + (int64_t)s * N + col), pk, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_SYSTEM);
+        release_stores();
+        if (cnt_add(&a.counter_grp[nb], 1) + 1 != a.slots) continue;
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        cnt_reset(&a.counter_grp[nb]);
+        const int rows = a.slots / kSlots;
+        for (int rr = 0; rr < rows; rr++) {
+          f32x2 y[kSlots];
 #pragma unroll
-        for (int j = 0; j < kSlots; j++) y[j] = ld_wt2(a.rowout + (int64_t)(rr * kSlots + j) * N + col);
-        float t0 = y[0].x * a.scores[rr * 8] + 0.0f, t1 = y[0].y * a.scores[rr * 8] + 0.0f;
+          for (int j = 0; j < kSlots; j++) y[j] = ld_wt2(a.rowout + (int64_t)(rr * kSlots + j) * N + col);
+          const int64_t o = (int64_t)rr * N + col;
+          const uint32_t res = *reinterpret_cast<const uint32_t*>(a.residual + o);
+          float t0 = y[0].x * a.scores[rr * 8] + 0.0f, t1 = y[0].y * a.scores[rr * 8] + 0.0f;
 #pragma unroll
-        for (int j = 1; j < 8; j++) {
-          const float sc = a.scores[rr * 8 + j];
-          t0 = (y[j].x * sc + 0.0f) + t0;
-          t1 = (y[j].y * sc + 0.0f) + t1;
+          for (int j = 1; j < 8; j++) {
+            const float sc = a.scores[rr * 8 + j];
+            t0 = (y[j].x * sc + 0.0f) + t0;
+            t1 = (y[j].y * sc + 0.0f) + t1;
+          }
+          const float c0 = round_bf16(round_bf16(t0) + y[8].x);
+          const float c1 = round_bf16(round_bf16(t1) + y[8].y);
+          const uint32_t pk2 = (uint32_t)f32_to_bf16(bf16_to_f32((uint16_t)(res & 0xFFFFu)) + c0) |
+                               ((uint32_t)f32_to_bf16(bf16_to_f32((uint16_t)(res >> 16)) + c1) << 16);
+          *reinterpret_cast<uint32_t*>(a.out + o) = pk2;
         }
-        const float c0 = round_bf16(round_bf16(t0) + y[8].x);
-        const float c1 = round_bf16(round_bf16(t1) + y[8].y);
-        const int64_t o = (int64_t)rr * N + col;
-        const uint32_t pk2 = (uint32_t)f32_to_bf16(bf16_to_f32(a.residual[o]) + c0) |
-                             ((uint32_t)f32_to_bf16(bf16_to_f32(a.residual[o + 1]) + c1) << 16);
-        *reinterpret_cast<uint32_t*>(a.out + o) = pk2;
       }
     }
   }
