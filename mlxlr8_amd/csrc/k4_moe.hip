@@ -29,6 +29,7 @@
 #include "moe_device.h"
 #include "moe_host.h"
 #include "moe_plan.h"
+#include "route.h"
 
 namespace moe {
 

@@ -404,6 +404,8 @@ __device__ __forceinline__ void release_stores() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
 }
 
+// A value every lane holds equally (e.g. read from LDS), made wave-uniform for the compiler.
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 __device__ __forceinline__ int wave_id_uniform() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
 }  // namespace moe

@@ -72,25 +72,29 @@ __device__ inline void build_plan_parallel(const int32_t* sid, int rows, int slo
   const int n = rows * slots;
   const int s = threadIdx.x;
   int pos = 0, start = s, total = 0, e = 0;
+  // no early exits: the LDS reads of the loops are independent and issue back to back
   if (s < n) {
     e = sid[s];
+#pragma unroll 4
     for (int q = 0; q < n; q++) {
-      if (sid[q] != e) continue;
-      if (q < s) pos++;
-      total++;
+      const int m = sid[q] == e ? 1 : 0;
+      pos += q < s ? m : 0;
+      total += m;
     }
     const int want = (pos / max_users) * max_users;
     int seen = 0;
+#pragma unroll 4
     for (int q = 0; q <= s; q++) {
-      if (sid[q] != e) continue;
-      if (seen == want) { start = q; break; }
-      seen++;
+      const int m = sid[q] == e ? 1 : 0;
+      if (m && seen == want) start = q;
+      seen += m;
     }
     open[s] = (pos % max_users) == 0;
   }
   __syncthreads();
   if (s < n) {
     int unit = 0;
+#pragma unroll 4
     for (int q = 0; q < start; q++) unit += open[q];
     const int i = pos % max_users;
     if (i == 0) {

@@ -15,6 +15,7 @@
 #include "moe_device.h"
 #include "moe_host.h"
 #include "moe_plan.h"
+#include "route.h"
 
 namespace moe {
 
@@ -91,95 +92,7 @@ __global__ __launch_bounds__(256) void router_logits_mfma(const uint16_t* __rest
   }
 }
 
-// ---------------------------------------------------------------- selection
-__device__ __forceinline__ float router_sigmoid(float v) {
-  const float y = 1.0f / (1.0f + expf(fabsf(v)));
-  return v < 0.0f ? y : 1.0f - y;
-}
-
-// Order-preserving map of a float onto an unsigned key (larger float -> larger key).
-__device__ __forceinline__ uint32_t float_key(float f) {
-  const uint32_t u = __float_as_uint(f);
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
-// One wave per row.  Lane l owns experts l, l+64, l+128, l+192.  COHERENT reads logits that
-// other blocks of the same launch wrote (L2-bypassing loads).
-//
-// Selection is a radix select on 40-bit keys (choice key << 8 | 255 - id): keys are unique, so
-// "top 8 by descending choice, ties to the lower id" is exactly "the 8 largest keys".  Each of
-// the 40 bisection steps counts candidates with wave ballots (no LDS round trip); the 8 winners
-// are then ranked against each other and the scores summed in rank order.
-template <bool COHERENT = false>
-__device__ __forceinline__ void route_row(const float* __restrict__ logits, const float* __restrict__ bias, int row,
-                                          uint32_t* __restrict__ ids, float* __restrict__ scores,
-                                          int32_t* sid = nullptr) {
-  const int lane = lane_id();
-  float orig[4];
-  uint64_t key[4];
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int e = lane + 64 * i;
-    const float* lp = logits + (int64_t)row * 256 + e;
-    const float lv = COHERENT ? __hip_atomic_load(const_cast<float*>(lp), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM)
-                              : *lp;
-    orig[i] = router_sigmoid(lv);
-    const float choice = orig[i] + bias[e];
-    key[i] = ((uint64_t)float_key(choice) << 8) | (uint64_t)(255 - e);
-  }
-  uint64_t thr = 0;
-  for (int b = 39; b >= 0; b--) {
-    const uint64_t cand = thr | (1ull << b);
-    int cnt = 0;
-#pragma unroll
-    for (int i = 0; i < 4; i++) cnt += __popcll(__ballot(key[i] >= cand));
-    if (cnt >= 8) thr = cand;
-  }
-  // exactly 8 keys are >= thr; rank each winner among the winners (descending)
-  int rank[4] = {-1, -1, -1, -1};
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    uint64_t m = __ballot(key[i] >= thr);
-    while (m) {
-      const int src = __builtin_ctzll(m);
-      m &= m - 1;
-      const uint64_t other = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(key[i] >> 32), src) << 32) |
-                             (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)key[i], src);
-#pragma unroll
-      for (int j = 0; j < 4; j++)
-        if (key[j] >= thr) rank[j] += (other >= key[j]) ? 1 : 0;
-    }
-  }
-  // rank[j] = (number of winners >= key[j]) - 1: 0 for the largest
-  __shared__ float sel_lds[kMaxRows][8];
-  __shared__ int id_lds[kMaxRows][8];
-  const int wv = wave_id_in_block();
-  (void)wv;
-  float* sel = sel_lds[row & (kMaxRows - 1)];
-  int* idl = id_lds[row & (kMaxRows - 1)];
-#pragma unroll
-  for (int j = 0; j < 4; j++) {
-    if (key[j] >= thr) {
-      sel[rank[j]] = orig[j];
-      idl[rank[j]] = lane + 64 * j;
-    }
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  if (lane == 0) {
-    float total = 1e-20f;
-#pragma unroll
-    for (int i = 0; i < 8; i++) total += sel[i];
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      scores[(int64_t)row * 8 + i] = sel[i] / total * 2.5f;
-      ids[(int64_t)row * 9 + i] = (uint32_t)idl[i];
-    }
-    ids[(int64_t)row * 9 + 8] = 256u;
-  }
-  if (sid != nullptr && lane < 9) sid[row * 9 + lane] = lane < 8 ? idl[lane] : 256;
-}
+// ---------------------------------------------------------------- selection (route.h)
 
 __global__ __launch_bounds__(64) void route_kernel(const float* __restrict__ logits, const float* __restrict__ bias,
                                                    int rows, uint32_t* __restrict__ ids, float* __restrict__ scores) {
@@ -188,7 +101,8 @@ __global__ __launch_bounds__(64) void route_kernel(const float* __restrict__ log
 }
 
 // Decode batches in one launch: block e computes logit e of every row; the last block to finish
-// routes all rows (one wave per row) and builds the token -> expert dispatch plan.
+// routes all rows (one wave per row) and builds the token -> expert dispatch plan.  With a null
+// counter only the logits (and the normalised rows) are produced.
 // KI = hidden / 1024 when known at compile time (all loads of a block are then issued before the
 // first multiply, one memory round trip), 0 for any multiple of 1024.
 //
@@ -306,6 +220,9 @@ __global__ __launch_bounds__(256) void router_decode_kernel(const uint16_t* __re
     const float lg = (red[r][0] + red[r][1]) + (red[r][2] + red[r][3]);
     __hip_atomic_store(logits + (int64_t)r * 256 + e, lg, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   }
+  // without a counter the routing is left to the expert kernels (they read the logits after
+  // this launch ends)
+  if (counter == nullptr) return;
   release_stores();
   __syncthreads();
   if (threadIdx.x == 0)
