@@ -149,7 +149,7 @@ enum FinMode { FIN_GATE = 0, FIN_VALUES = 1, FIN_COMBINE = 2 };
 // waves per block of the MFMA kernel for single-token units and for up to kMaxRows tokens (the
 // latter needs more registers for its A fragments)
 #ifndef MOE_K4_WAVES_1
-#define MOE_K4_WAVES_1 8
+#define MOE_K4_WAVES_1 16
 #endif
 #ifndef MOE_K4_WAVES_8
 #define MOE_K4_WAVES_8 8
@@ -415,6 +415,12 @@ __device__ __forceinline__ f16x8 frag(f16x2 a, f16x2 b, f16x2 c, f16x2 d) {
 __device__ __forceinline__ int a_rh(int r) { return (r >> 2) & 1; }
 __device__ __forceinline__ int a_j(int r) { return 4 * ((r >> 1) & 1) + 2 * ((r >> 3) & 1) + (r & 1); }
 
+// The kernel body takes its LDS regions as distinct restrict pointers (table, the wave's A
+// fragments), so the compiler knows they never alias.
+template <int IM, int FM, int NT, int ALU_EVEN, int ALU_ODD, int WV>
+__device__ __forceinline__ void k4_mfma_body(const GemvArgs& a, const uint8_t* __restrict__ tab,
+                                             _Float16* __restrict__ xw);
+
 template <int IM, int FM, int NT, int ALU_EVEN, int ALU_ODD, int WV>
 __global__ __launch_bounds__(WV * 64) void k4_mfma_kernel(GemvArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t tab[65536];
@@ -423,7 +429,13 @@ __global__ __launch_bounds__(WV * 64) void k4_mfma_kernel(GemvArgs a) {
 
   load_codebook_lds(tab);
   __syncthreads();
+  const int wv = wave_id_uniform();
+  k4_mfma_body<IM, FM, NT, ALU_EVEN, ALU_ODD, WV>(a, tab, xa + wv * (2 * 2 * (2 * NT) * 4 * 8));
+}
 
+template <int IM, int FM, int NT, int ALU_EVEN, int ALU_ODD, int WV>
+__device__ __forceinline__ void k4_mfma_body(const GemvArgs& a, const uint8_t* __restrict__ tab,
+                                             _Float16* __restrict__ xw) {
   const Plan* __restrict__ P = a.plan;
   const int U = P->units;
   const int it = a.in_f / 16;
@@ -439,7 +451,7 @@ __global__ __launch_bounds__(WV * 64) void k4_mfma_kernel(GemvArgs a) {
   // quad counts fit 32 bits (<= 72 units x 64 column blocks x 2 projections x 1024 quads)
   const Split sp = make_split((int)nq, nw);
   const int q_begin = sp.start(wave), q_end = sp.start(wave + 1);
-  _Float16* xw = xa + wave_id_uniform() * (2 * 2 * (2 * NT) * 4 * 8);
+
   // this lane's 16 B inside a chunk: tile 2s + n/8 at +256 s, word group n%8
   const int lane_off = (nn >> 3) * 128 + (nn & 7) * 16;
   const int src_lane = (lane & 7) == 0 ? lane + 7 : lane - 1;
@@ -545,9 +557,9 @@ __global__ __launch_bounds__(WV * 64) void k4_mfma_kernel(GemvArgs a) {
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     };
 
-    // One quad in flight per wave (with enough waves per CU this keeps HBM busy): each piece's
-    // registers are refilled with the next quad's piece once the piece has been decoded.  The
-    // last quad re-reads itself (a cache hit), so the prefetch needs no branch.
+    // One quad in flight per wave: each piece's registers are refilled with the next quad's
+    // piece once the piece has been decoded.  The last quad re-reads itself (a cache hit), so the
+    // prefetch needs no branch.
     const int tl = tq1 - 1;
     u32x4 pc[4];
     load_quad(pc, tq0);
