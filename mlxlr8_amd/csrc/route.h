@@ -89,16 +89,13 @@ __device__ __forceinline__ void route_row(const float* __restrict__ logits, cons
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  if (lane == 0 && store_global) {
+  if (store_global && lane < 9) {
+    // every lane forms the same rank-ordered sum; lane i < 8 writes winner i, lane 8 the shared id
     float total = 1e-20f;
 #pragma unroll
     for (int i = 0; i < 8; i++) total += sel[i];
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      scores[(int64_t)row * 8 + i] = sel[i] / total * 2.5f;
-      ids[(int64_t)row * 9 + i] = (uint32_t)idl[i];
-    }
-    ids[(int64_t)row * 9 + 8] = 256u;
+    if (lane < 8) scores[(int64_t)row * 8 + lane] = sel[lane] / total * 2.5f;
+    ids[(int64_t)row * 9 + lane] = lane < 8 ? (uint32_t)idl[lane] : 256u;
   }
   if (sid != nullptr && lane < 9) sid[row * 9 + lane] = lane < 8 ? idl[lane] : 256;
 }
