@@ -26,7 +26,7 @@
 //     nibble j (low nibble first) is k = 32(l/16)+j; lane l's scale byte scales k-block l/16.  The
 //     fp16 MFMAs of a 128-wide k step reuse the lane's 32 widened weights: MFMA q (q = 0..3) maps
 //     its k-group kg = l/16 to k = 32 kg + 8q + i, and the staged hi activations are read to match.
-//   * A work item is (block of <= 128 sorted rows of one expert, output block): the weights of the
+//   * A work item is (block of <= 64 sorted rows of one expert, output block): the weights of the
 //     output block are streamed once per item with 16 B loads per lane; the item's activation
 //     terms for one 128-wide k step are staged in LDS (double buffered) and shared by the 8 waves.
 //   * The gate finish (both 128-column halves of an intermediate block are in one item) and the
@@ -50,7 +50,7 @@ __device__ __forceinline__ f16x8 pack_f16x8(f16x2 a, f16x2 b, f16x2 c, f16x2 d) 
   return __builtin_shufflevector(ab, cd, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
-constexpr int kPfItemRows = 128; // sorted rows per GEMM work item (8 M-tiles of 16)
+constexpr int kPfItemRows = 64;  // sorted rows per GEMM work item (4 M-tiles of 16)
 constexpr int kPfWaves = 8;      // waves per GEMM block
 constexpr int kPfThreads = kPfWaves * 64;
 constexpr int kPfRowBytes = 528; // LDS row stride of a staged k step: 256 B hi + 2 x 128 B lo + pad
@@ -58,22 +58,36 @@ constexpr int kPfLo = 2;         // fp8 remainder terms
 constexpr int kPfMaxExperts = 1024;
 
 // ---------------------------------------------------------------- sorted work order
-// One block of 1024 threads.  Counting sort of the flat ids (stable: slots of one expert keep
-// their order), per-expert counts and starts, and the block table of `block_rows` rows.
+// One block of 1024 threads (16 waves).  Counting sort of the flat ids (stable: slots of one
+// expert keep their order), per-expert counts and starts, and the block table of `block_rows`
+// rows.  Wave w owns the contiguous slice [w n / 16, (w + 1) n / 16) of the ids: it counts its
+// slice into its own histogram row, the rows are turned into per-wave write offsets, and each wave
+// then places its slice in order (the rank among equal ids inside a 64-id chunk comes from
+// matching the ids bit by bit with ballots), all waves at once.
 __global__ __launch_bounds__(1024) void segment_table_kernel(const uint32_t* __restrict__ ids, int n, int experts,
                                                              int block_rows, int32_t* __restrict__ order,
                                                              int32_t* __restrict__ counts,
                                                              int32_t* __restrict__ starts, int32_t* __restrict__ blk,
                                                              int cap, int32_t* __restrict__ nblk) {
-  __shared__ int32_t cnt[kPfMaxExperts], st[kPfMaxExperts], fill[kPfMaxExperts], bst[kPfMaxExperts];
+  __shared__ int32_t hist[16][kPfMaxExperts];  // per wave: counts, then write offsets
+  __shared__ int32_t cnt[kPfMaxExperts], st[kPfMaxExperts], bst[kPfMaxExperts];
   __shared__ int32_t wsum[16];
-  const int tid = threadIdx.x, lane = lane_id(), wv = wave_id_in_block();
-  for (int e = tid; e < experts; e += 1024) { cnt[e] = 0; fill[e] = 0; }
+  const int tid = threadIdx.x, lane = lane_id(), wv = wave_id_uniform();
+  for (int i = tid; i < 16 * kPfMaxExperts; i += 1024) (&hist[0][0])[i] = 0;
   __syncthreads();
+  const int s0 = (int)((int64_t)n * wv / 16), s1 = (int)((int64_t)n * (wv + 1) / 16);
   // ids outside [0, experts) are skipped (they get no position; callers pass valid ids)
-  for (int i = tid; i < n; i += 1024) {
+  for (int i = s0 + lane; i < s1; i += 64) {
     const uint32_t e = ids[i];
-    if (e < (uint32_t)experts) atomicAdd(&cnt[e], 1);
+    if (e < (uint32_t)experts) atomicAdd(&hist[wv][e], 1);
+  }
+  __syncthreads();
+  // per expert: total, then the running offsets of the waves' slices (in wave order)
+  for (int e = tid; e < experts; e += 1024) {
+    int c = 0;
+#pragma unroll
+    for (int w = 0; w < 16; w++) c += hist[w][e];
+    cnt[e] = c;
   }
   __syncthreads();
   // exclusive scans of the counts and of the per-expert block counts (experts <= 1024: one per thread)
@@ -96,40 +110,42 @@ __global__ __launch_bounds__(1024) void segment_table_kernel(const uint32_t* __r
     int offb = 0;
     for (int w = 0; w < wv; w++) offb += wsum[w];
     if (tid < experts) {
-      st[tid] = offc + ic - c;
+      const int start = offc + ic - c;
+      st[tid] = start;
       bst[tid] = offb + ib - b;
       counts[tid] = c;
-      starts[tid] = offc + ic - c;
+      starts[tid] = start;
+      int run = start;
+#pragma unroll
+      for (int w = 0; w < 16; w++) {
+        const int h = hist[w][tid];
+        hist[w][tid] = run;
+        run += h;
+      }
     }
     if (tid == 1023) *nblk = offb + ib;
   }
   __syncthreads();
-  // stable placement: chunks of 1024 slots in order, waves of a chunk in order; inside a wave the
-  // rank of a slot among equal ids comes from matching the id bit by bit with ballots
-  for (int c0 = 0; c0 < n; c0 += 1024) {
-    for (int w = 0; w < 16; w++) {
-      if (wv == w) {
-        const int i = c0 + tid;
-        const uint32_t e = i < n ? ids[i] : 0xFFFFFFFFu;
-        const bool valid = e < (uint32_t)experts;
-        uint64_t same = __ballot(1);
+  // stable placement of each wave's slice, 64 ids at a time; ids are matched on 11 bits (valid ids
+  // are < 1024, invalid ones are given the key 2047 and not placed)
+  for (int c0 = s0; c0 < s1; c0 += 64) {
+    const int i = c0 + lane;
+    const uint32_t e = i < s1 ? ids[i] : 0xFFFFFFFFu;
+    const bool valid = e < (uint32_t)experts;
+    const uint32_t key = valid ? e : 2047u;
+    uint64_t same = __ballot(1);
 #pragma unroll
-        for (int bit = 0; bit < 32; bit++) {
-          const bool on = (e >> bit) & 1u;
-          const uint64_t bal = __ballot(on);
-          same &= on ? bal : ~bal;
-        }
-        const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-        const int rank = __popcll(same & below);
-        if (valid) {
-          const int pos = st[e] + fill[e] + rank;
-          order[pos] = i;
-        }
-        __builtin_amdgcn_wave_barrier();
-        if (valid && rank == 0) fill[e] += __popcll(same);
-      }
-      __syncthreads();
+    for (int bit = 0; bit < 11; bit++) {
+      const bool on = (key >> bit) & 1u;
+      const uint64_t bal = __ballot(on);
+      same &= on ? bal : ~bal;
     }
+    const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    const int rank = __popcll(same & below);
+    if (valid) order[hist[wv][e] + rank] = i;
+    __builtin_amdgcn_wave_barrier();
+    if (valid && rank == 0) hist[wv][e] += __popcll(same);
+    __builtin_amdgcn_wave_barrier();
   }
   // block table rows (expert, first, length)
   for (int e = tid; e < experts; e += 1024) {
@@ -384,7 +400,7 @@ __device__ __forceinline__ void gemm_item(const PfGemm& a, int e, const int (&co
 // Item = (plan block b, intermediate block c): columns gate [128c, +128) and up [m + 128c, +128);
 // wave w owns gate tile 16w and up tile 16w.
 template <int MT, int MTMAX>
-__device__ void gateup_item(const PfGemm& a, int e, int first, int len, int c, uint8_t* abuf, uint8_t* sbuf,
+__device__ __forceinline__ void gateup_item(const PfGemm& a, int e, int first, int len, int c, uint8_t* abuf, uint8_t* sbuf,
                             int64_t* rowidx, float* ex) {
   const int w = wave_id_uniform(), lane = lane_id(), nn = lane & 15, g = lane >> 4;
   item_rows<MT>(a, first, len, rowidx);
@@ -436,7 +452,7 @@ __device__ void gateup_item(const PfGemm& a, int e, int first, int len, int c, u
 // ---------------------------------------------------------------- down GEMM + value finish
 // Item = (plan block b, output block ob): columns [128 ob, +128); wave w owns tile 16w.
 template <int MT, int MTMAX>
-__device__ void down_item(const PfGemm& a, int e, int first, int len, int ob, uint8_t* abuf, uint8_t* sbuf,
+__device__ __forceinline__ void down_item(const PfGemm& a, int e, int first, int len, int ob, uint8_t* abuf, uint8_t* sbuf,
                           int64_t* rowidx, float* ex) {
   const int w = wave_id_uniform(), lane = lane_id(), nn = lane & 15, g = lane >> 4;
   item_rows<MT>(a, first, len, rowidx);
@@ -503,10 +519,6 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm_kernel(PfGemm a) {
     PF_CASE(2)
     PF_CASE(3)
     PF_CASE(4)
-    PF_CASE(5)
-    PF_CASE(6)
-    PF_CASE(7)
-    PF_CASE(8)
     default: break;
   }
 #undef PF_CASE
@@ -515,13 +527,13 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm_kernel(PfGemm a) {
 template <bool GATE>
 int launch_pf_gemm(const PfGemm& a, int outblocks, hipStream_t s) {
   const dim3 grid((unsigned)(a.cap * outblocks)), block(kPfThreads);
-  constexpr size_t small_lds = pf_lds_bytes<1, 2>(), large_lds = pf_lds_bytes<3, 8>();
+  constexpr size_t small_lds = pf_lds_bytes<1, 2>(), large_lds = pf_lds_bytes<3, 4>();
   // dynamic LDS beyond 64 KB must be allowed explicitly (idempotent; cheap)
-  MOE_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&pf_gemm_kernel<GATE, 3, 8>),
+  MOE_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&pf_gemm_kernel<GATE, 3, 4>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)large_lds));
   hipLaunchKernelGGL((pf_gemm_kernel<GATE, 1, 2>), grid, block, small_lds, s, a);
   MOE_HIP(hipGetLastError());
-  hipLaunchKernelGGL((pf_gemm_kernel<GATE, 3, 8>), grid, block, large_lds, s, a);
+  hipLaunchKernelGGL((pf_gemm_kernel<GATE, 3, 4>), grid, block, large_lds, s, a);
   MOE_HIP(hipGetLastError());
   return MOE_OK;
 }
