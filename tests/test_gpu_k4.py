@@ -218,3 +218,31 @@ def test_mlp_values_glm(cuda, orc, glm_layer):
     say(f"  rel_l2={err:.3e}")
     assert err <= 1e-3
     assert values.shape == (2, 9, 6144)
+
+
+def test_fp32_accumulation_known_answer(cuda):
+    """Known answer of the reference (tests/golden, from its tests/test_fast_prefill.py:208-228): an
+    all-zero K4 bitstream decodes to codebook[0] = 1.875 everywhere, so with unit scales and one
+    spike per 128-block the inner sum (6144 * 1.875 * spike / sqrt(128)) exceeds the fp16 range;
+    after the output H128 all of it sits in column 0 and the other columns are exactly zero."""
+    import json
+    from pathlib import Path
+    from mlxlr8_amd.trellis import expert_linear
+    say("case: fp32 accumulation known answer")
+    g = json.loads((Path(__file__).parent / "golden" / "reference_known_answers.json").read_text())["fp32_accumulation"]
+    w, n = g["width"], g["output"]
+    packed = torch.zeros(w * n // 2, dtype=torch.uint8, device=cuda)
+    x = torch.zeros((1, w), dtype=torch.float32, device=cuda)
+    x[0, ::128] = g["spike"]
+    x = x.to(torch.bfloat16)  # activations are bf16 here: the spike rounds to bf16
+    spike = float(x[0, 0])
+    ones_in = torch.ones((1, w), dtype=torch.float16, device=cuda)
+    ones_out = torch.ones((1, n), dtype=torch.float16, device=cuda)
+    ids = torch.zeros((1, 1), dtype=torch.int32, device=cuda)
+    y = expert_linear(x, ids, packed, ones_in, ones_out, 4, w, n, 1).float().cpu().numpy().reshape(-1)
+    inner = w * 1.875 * spike / np.sqrt(128)
+    assert inner > g["fp16_max"]
+    want0 = w * 1.875 * spike
+    say(f"  col0={y[0]} want={want0} max|other|={np.abs(y[1:]).max()}")
+    assert abs(y[0] - want0) <= want0 * 2.0 ** -8
+    assert np.all(y[1:] == 0.0)
