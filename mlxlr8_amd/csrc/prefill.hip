@@ -266,27 +266,41 @@ struct PfStage {
   static constexpr int kScaleBytes = MT * 16 * 4 * kPfLo;
 };
 
+// A k step's activation chunks in flight in registers: thread t holds chunks t + kPfThreads i
+// (16 B each; MT * 16 rows x 32 chunks = MT chunks per thread) and at most one scale dword.
 template <int MT>
-__device__ __forceinline__ void stage_k(const PfGemm& a, int ks, const int64_t* rowidx, uint8_t* buf, uint8_t* sbuf) {
-  // 16 B chunks per row: 16 of hi, 8 per remainder term
+struct PfFetch {
+  i32x4 v[MT];
+  uint32_t sc;
+};
+template <int MT>
+__device__ __forceinline__ void fetch_k(const PfGemm& a, int ks, const int64_t* rowidx, PfFetch<MT>& f) {
   constexpr int kPer = 16 + 8 * kPfLo;
-  constexpr int kChunks = MT * 16 * kPer;
-  for (int c = threadIdx.x; c < kChunks; c += kPfThreads) {
+  static_assert(MT * 16 * kPer == MT * kPfThreads, "one chunk per thread and M-tile");
+#pragma unroll
+  for (int i = 0; i < MT; i++) {
+    const int c = threadIdx.x + i * kPfThreads;
     const int r = c / kPer, ch = c % kPer;
-    i32x4 v;
     if (ch < 16) {
-      v = *reinterpret_cast<const i32x4*>(a.ahi + rowidx[r] * a.K + ks * 128 + ch * 8);
+      f.v[i] = *reinterpret_cast<const i32x4*>(a.ahi + rowidx[r] * a.K + ks * 128 + ch * 8);
     } else {
       const int t = (ch - 16) / 8, cc = (ch - 16) % 8;
-      v = *reinterpret_cast<const i32x4*>(a.aq + (t * a.arows + rowidx[r]) * a.K + ks * 128 + cc * 16);
+      f.v[i] = *reinterpret_cast<const i32x4*>(a.aq + (t * a.arows + rowidx[r]) * a.K + ks * 128 + cc * 16);
     }
-    *reinterpret_cast<i32x4*>(buf + r * kPfRowBytes + ch * 16) = v;
   }
-  for (int c = threadIdx.x; c < MT * 16 * kPfLo; c += kPfThreads) {
-    const int r = c / kPfLo, t = c % kPfLo;
-    *reinterpret_cast<uint32_t*>(sbuf + (r * kPfLo + t) * 4) =
-        *reinterpret_cast<const uint32_t*>(a.as + (t * a.arows + rowidx[r]) * (a.K / 32) + ks * 4);
+  const int c = min((int)threadIdx.x, MT * 16 * kPfLo - 1);
+  const int r = c / kPfLo, t = c % kPfLo;
+  f.sc = *reinterpret_cast<const uint32_t*>(a.as + (t * a.arows + rowidx[r]) * (a.K / 32) + ks * 4);
+}
+template <int MT>
+__device__ __forceinline__ void put_k(const PfFetch<MT>& f, uint8_t* buf, uint8_t* sbuf) {
+  constexpr int kPer = 16 + 8 * kPfLo;
+#pragma unroll
+  for (int i = 0; i < MT; i++) {
+    const int c = threadIdx.x + i * kPfThreads;
+    *reinterpret_cast<i32x4*>(buf + (c / kPer) * kPfRowBytes + (c % kPer) * 16) = f.v[i];
   }
+  if ((int)threadIdx.x < MT * 16 * kPfLo) *reinterpret_cast<uint32_t*>(sbuf + threadIdx.x * 4) = f.sc;
 }
 
 // The item's rows: sorted positions [first, first + len), clamped into the item for the padding
@@ -304,33 +318,33 @@ template <int MT, int NT>
 __device__ __forceinline__ void gemm_step(const uint8_t* ab, const uint8_t* sb, const i32x4 (&bw)[NT],
                                           const uint32_t (&bs)[NT], f32x4 (&acc)[MT][NT]) {
   const int lane = lane_id(), nn = lane & 15, g = lane >> 4;
-  // the weights widened to fp16 with their block scale: bf[j][b] = codes of byte b
-  f16x2 bf[NT][16];
+  float wsc[NT];
 #pragma unroll
-  for (int j = 0; j < NT; j++) {
-    const float wsc = __builtin_amdgcn_ldexpf(1.0f, (int)bs[j] - 127);
-    const uint32_t words[4] = {(uint32_t)bw[j].x, (uint32_t)bw[j].y, (uint32_t)bw[j].z, (uint32_t)bw[j].w};
+  for (int j = 0; j < NT; j++) wsc[j] = __builtin_amdgcn_ldexpf(1.0f, (int)bs[j] - 127);
+  // hi: 4 fp16 MFMAs per M-tile; the q-th reads k = 32 g + 8 q + i, i.e. the 8 codes of word q,
+  // widened to fp16 with their block scale just before use
 #pragma unroll
-    for (int wd = 0; wd < 4; wd++) {
-      bf[j][4 * wd + 0] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(words[wd], wsc, 0);
-      bf[j][4 * wd + 1] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(words[wd], wsc, 1);
-      bf[j][4 * wd + 2] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(words[wd], wsc, 2);
-      bf[j][4 * wd + 3] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(words[wd], wsc, 3);
+  for (int q = 0; q < 4; q++) {
+    f16x8 bh[NT];
+#pragma unroll
+    for (int j = 0; j < NT; j++) {
+      const uint32_t word = (uint32_t)bw[j][q];
+      bh[j] = pack_f16x8(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(word, wsc[j], 0),
+                         __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(word, wsc[j], 1),
+                         __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(word, wsc[j], 2),
+                         __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(word, wsc[j], 3));
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) {
+      const f16x8 ah =
+          *reinterpret_cast<const f16x8*>(ab + (mt * 16 + nn) * kPfRowBytes + (32 * g + 8 * q) * 2);
+#pragma unroll
+      for (int j = 0; j < NT; j++) acc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh[j], acc[mt][j], 0, 0, 0);
     }
   }
 #pragma unroll
   for (int mt = 0; mt < MT; mt++) {
     const uint8_t* rp = ab + (mt * 16 + nn) * kPfRowBytes;
-    // hi: 4 fp16 MFMAs, q-th reads k = 32 g + 8 q + i
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-      const f16x8 ah = *reinterpret_cast<const f16x8*>(rp + (32 * g + 8 * q) * 2);
-#pragma unroll
-      for (int j = 0; j < NT; j++) {
-        const f16x8 bh = pack_f16x8(bf[j][4 * q], bf[j][4 * q + 1], bf[j][4 * q + 2], bf[j][4 * q + 3]);
-        acc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, acc[mt][j], 0, 0, 0);
-      }
-    }
     // remainder terms: one scaled MX MFMA each on the resident codes
 #pragma unroll
     for (int t = 0; t < kPfLo; t++) {
@@ -349,8 +363,7 @@ __device__ __forceinline__ void gemm_step(const uint8_t* ab, const uint8_t* sb, 
 }
 
 // One wave's NT column tiles (cols[j] .. +16) over all K for the item's MT M-tiles.  The weights
-// are prefetched two k steps ahead in two register sets (even and odd steps; K/128 is even), the
-// activations one step ahead in the other LDS buffer.
+// are prefetched two k steps ahead in two register sets (even and odd steps; K/128 is even).
 template <int MT, int NT, int MTMAX>
 __device__ __forceinline__ void gemm_item(const PfGemm& a, int e, const int (&cols)[NT], const int64_t* rowidx,
                                           uint8_t* abuf, uint8_t* sbuf, f32x4 (&acc)[MT][NT]) {
@@ -376,22 +389,28 @@ __device__ __forceinline__ void gemm_item(const PfGemm& a, int e, const int (&co
       bs[j] = srow[j][ks * 4];
     }
   };
-  stage_k<MT>(a, 0, rowidx, abuf, sbuf);
+  // the activations of step ks + 1 are loaded while step ks computes and stored to LDS after it
+  PfFetch<MT> f;
+  fetch_k<MT>(a, 0, rowidx, f);
+  put_k<MT>(f, abuf, sbuf);
   i32x4 b0[NT], b1[NT];
   uint32_t s0[NT], s1[NT];
   load_w(b0, s0, 0);
   load_w(b1, s1, min(1, ksteps - 1));
+  fetch_k<MT>(a, min(1, ksteps - 1), rowidx, f);
   __syncthreads();
   for (int ks = 0; ks < ksteps; ks += 2) {
-    // even step ks (buffer 0): stage ks+1, compute, refill set 0 with ks+2
-    stage_k<MT>(a, ks + 1, rowidx, abuf + kStage, sbuf + kSStage);
+    // even step ks (buffer 0); f holds step ks + 1
     gemm_step<MT, NT>(abuf, sbuf, b0, s0, acc);
     load_w(b0, s0, min(ks + 2, ksteps - 1));
+    put_k<MT>(f, abuf + kStage, sbuf + kSStage);
+    fetch_k<MT>(a, min(ks + 2, ksteps - 1), rowidx, f);
     __syncthreads();
-    // odd step ks+1 (buffer 1): stage ks+2, compute, refill set 1 with ks+3
-    if (ks + 2 < ksteps) stage_k<MT>(a, ks + 2, rowidx, abuf, sbuf);
+    // odd step ks + 1 (buffer 1); f holds step ks + 2
     gemm_step<MT, NT>(abuf + kStage, sbuf + kSStage, b1, s1, acc);
     load_w(b1, s1, min(ks + 3, ksteps - 1));
+    if (ks + 2 < ksteps) put_k<MT>(f, abuf, sbuf);
+    fetch_k<MT>(a, min(ks + 3, ksteps - 1), rowidx, f);
     __syncthreads();
   }
 }
