@@ -56,6 +56,7 @@ constexpr int kPfThreads = kPfWaves * 64;
 constexpr int kPfRowBytes = 528; // LDS row stride of a staged k step: 256 B hi + 2 x 128 B lo + pad
 constexpr int kPfLo = 2;         // fp8 remainder terms
 constexpr int kPfMaxExperts = 1024;
+constexpr size_t kPfMaxLds = 160 * 1024;  // LDS per workgroup on gfx950
 
 // ---------------------------------------------------------------- sorted work order
 // One block of 1024 threads (16 waves).  Counting sort of the flat ids (stable: slots of one
@@ -273,24 +274,41 @@ struct PfFetch {
   i32x4 v[MT];
   uint32_t sc;
 };
+// Where a thread's chunks come from: chunk i is row r = t / 32 + 16 i of the item (t = thread) and
+// chunk t % 32 of the row (0-15: hi, 16-23: lo1, 24-31: lo2); the addresses are fixed per item up
+// to the k step offset, so they are formed once per item.
 template <int MT>
-__device__ __forceinline__ void fetch_k(const PfGemm& a, int ks, const int64_t* rowidx, PfFetch<MT>& f) {
+struct PfSrc {
+  const uint8_t* p[MT];  // chunk i at k step 0
+  const uint8_t* sp;     // the thread's scale dword at k step 0
+  int step;              // bytes per k step of the thread's chunks: 256 (hi) or 128 (lo)
+};
+template <int MT>
+__device__ __forceinline__ void item_src(const PfGemm& a, const int64_t* rowidx, PfSrc<MT>& s) {
   constexpr int kPer = 16 + 8 * kPfLo;
   static_assert(MT * 16 * kPer == MT * kPfThreads, "one chunk per thread and M-tile");
+  const int ch = (int)threadIdx.x % kPer;
+  s.step = ch < 16 ? 256 : 128;
 #pragma unroll
   for (int i = 0; i < MT; i++) {
-    const int c = threadIdx.x + i * kPfThreads;
-    const int r = c / kPer, ch = c % kPer;
+    const int r = (int)threadIdx.x / kPer + i * (kPfThreads / kPer);
     if (ch < 16) {
-      f.v[i] = *reinterpret_cast<const i32x4*>(a.ahi + rowidx[r] * a.K + ks * 128 + ch * 8);
+      s.p[i] = reinterpret_cast<const uint8_t*>(a.ahi + rowidx[r] * a.K) + ch * 16;
     } else {
       const int t = (ch - 16) / 8, cc = (ch - 16) % 8;
-      f.v[i] = *reinterpret_cast<const i32x4*>(a.aq + (t * a.arows + rowidx[r]) * a.K + ks * 128 + cc * 16);
+      s.p[i] = a.aq + (t * a.arows + rowidx[r]) * a.K + cc * 16;
     }
   }
   const int c = min((int)threadIdx.x, MT * 16 * kPfLo - 1);
   const int r = c / kPfLo, t = c % kPfLo;
-  f.sc = *reinterpret_cast<const uint32_t*>(a.as + (t * a.arows + rowidx[r]) * (a.K / 32) + ks * 4);
+  s.sp = a.as + (t * a.arows + rowidx[r]) * (a.K / 32);
+}
+template <int MT>
+__device__ __forceinline__ void fetch_k(const PfSrc<MT>& s, int ks, PfFetch<MT>& f) {
+  const int off = ks * s.step;
+#pragma unroll
+  for (int i = 0; i < MT; i++) f.v[i] = *reinterpret_cast<const i32x4*>(s.p[i] + off);
+  f.sc = *reinterpret_cast<const uint32_t*>(s.sp + ks * 4);
 }
 template <int MT>
 __device__ __forceinline__ void put_k(const PfFetch<MT>& f, uint8_t* buf, uint8_t* sbuf) {
@@ -363,151 +381,194 @@ __device__ __forceinline__ void gemm_step(const uint8_t* ab, const uint8_t* sb, 
 }
 
 // One wave's NT column tiles (cols[j] .. +16) over all K for the item's MT M-tiles.  The weights
-// are prefetched two k steps ahead in two register sets (even and odd steps; K/128 is even).
-template <int MT, int NT, int MTMAX>
+// and the activations are loaded D k steps ahead into rings of D register sets (set s % D holds
+// step s); a step's activations go to LDS (double buffered) in the step before their use, after
+// that step's MFMAs (D even).  The tiles' block scales for all k steps (16 rows x K/32 bytes per
+// tile, one contiguous span in memory) are copied once per item into the wave's LDS region `wsl`
+// with 16 B loads: a byte load per lane and k step from HBM costs about as much as the weights.
+template <int MT, int NT, int MTMAX, int D>
 __device__ __forceinline__ void gemm_item(const PfGemm& a, int e, const int (&cols)[NT], const int64_t* rowidx,
-                                          uint8_t* abuf, uint8_t* sbuf, f32x4 (&acc)[MT][NT]) {
+                                          uint8_t* abuf, uint8_t* sbuf, uint8_t* wsl, f32x4 (&acc)[MT][NT]) {
+  static_assert(D % 2 == 0, "the LDS stage alternates with the step parity");
   const int lane = lane_id(), nn = lane & 15, g = lane >> 4;
-  const int ksteps = a.K / 128;
+  const int ksteps = a.K / 128, last = ksteps - 1;
 #pragma unroll
   for (int mt = 0; mt < MT; mt++)
 #pragma unroll
     for (int j = 0; j < NT; j++) acc[mt][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  const int sb = a.K / 32;  // scale bytes per weight row
+#pragma unroll
+  for (int j = 0; j < NT; j++) {
+    const uint8_t* src = a.wscales + ((int64_t)e * a.N + cols[j]) * sb;
+    uint8_t* dst = wsl + j * 16 * sb;
+    for (int c = lane; c < sb; c += 64)  // 16 sb bytes = sb chunks of 16 B
+      *reinterpret_cast<i32x4*>(dst + 16 * c) = *reinterpret_cast<const i32x4*>(src + 16 * c);
+  }
   const uint8_t* wrow[NT];
   const uint8_t* srow[NT];
 #pragma unroll
   for (int j = 0; j < NT; j++) {
-    const int64_t row = (int64_t)e * a.N + cols[j] + nn;
-    wrow[j] = a.codes + row * (a.K / 2) + g * 16;
-    srow[j] = a.wscales + row * (a.K / 32) + g;
+    wrow[j] = a.codes + ((int64_t)e * a.N + cols[j] + nn) * (a.K / 2) + g * 16;
+    srow[j] = wsl + (j * 16 + nn) * sb + g;
   }
   constexpr int kStage = PfStage<MTMAX>::kBytes, kSStage = PfStage<MTMAX>::kScaleBytes;
   auto load_w = [&](i32x4 (&bw)[NT], uint32_t (&bs)[NT], int ks) {
 #pragma unroll
     for (int j = 0; j < NT; j++) {
       bw[j] = *reinterpret_cast<const i32x4*>(wrow[j] + ks * 64);
-      bs[j] = srow[j][ks * 4];
+      bs[j] = srow[j][ks * 4];  // LDS; written above by this wave
     }
   };
-  // the activations of step ks + 1 are loaded while step ks computes and stored to LDS after it
-  PfFetch<MT> f;
-  fetch_k<MT>(a, 0, rowidx, f);
-  put_k<MT>(f, abuf, sbuf);
-  i32x4 b0[NT], b1[NT];
-  uint32_t s0[NT], s1[NT];
-  load_w(b0, s0, 0);
-  load_w(b1, s1, min(1, ksteps - 1));
-  fetch_k<MT>(a, min(1, ksteps - 1), rowidx, f);
+  PfSrc<MT> src;
+  item_src<MT>(a, rowidx, src);
+  PfFetch<MT> f[D];
+  i32x4 bw[D][NT];
+  uint32_t bs[D][NT];
+  fetch_k<MT>(src, 0, f[0]);
+  put_k<MT>(f[0], abuf, sbuf);
+#pragma unroll
+  for (int d = 0; d < D; d++) load_w(bw[d], bs[d], min(d, last));
+#pragma unroll
+  for (int d = 1; d <= D; d++) fetch_k<MT>(src, min(d, last), f[d % D]);
   __syncthreads();
-  for (int ks = 0; ks < ksteps; ks += 2) {
-    // even step ks (buffer 0); f holds step ks + 1
-    gemm_step<MT, NT>(abuf, sbuf, b0, s0, acc);
-    load_w(b0, s0, min(ks + 2, ksteps - 1));
-    put_k<MT>(f, abuf + kStage, sbuf + kSStage);
-    fetch_k<MT>(a, min(ks + 2, ksteps - 1), rowidx, f);
-    __syncthreads();
-    // odd step ks + 1 (buffer 1); f holds step ks + 2
-    gemm_step<MT, NT>(abuf + kStage, sbuf + kSStage, b1, s1, acc);
-    load_w(b1, s1, min(ks + 3, ksteps - 1));
-    if (ks + 2 < ksteps) put_k<MT>(f, abuf, sbuf);
-    fetch_k<MT>(a, min(ks + 3, ksteps - 1), rowidx, f);
-    __syncthreads();
+  for (int ks = 0; ks < ksteps; ks += D) {
+#pragma unroll
+    for (int u = 0; u < D; u++) {
+      const int t = ks + u;  // block-uniform
+      if (t < ksteps) {
+        gemm_step<MT, NT>(abuf + (u & 1) * kStage, sbuf + (u & 1) * kSStage, bw[u], bs[u], acc);
+        load_w(bw[u], bs[u], min(t + D, last));
+        if (t + 1 < ksteps) put_k<MT>(f[(u + 1) % D], abuf + ((u + 1) & 1) * kStage, sbuf + ((u + 1) & 1) * kSStage);
+        fetch_k<MT>(src, min(t + 1 + D, last), f[(u + 1) % D]);
+        __syncthreads();
+      }
+    }
   }
 }
 
 // ---------------------------------------------------------------- gate/up GEMM + gate finish
-// Item = (plan block b, intermediate block c): columns gate [128c, +128) and up [m + 128c, +128);
-// wave w owns gate tile 16w and up tile 16w.
-template <int MT, int MTMAX>
+// Item = (plan block b, intermediate blocks c NB .. c NB + NB - 1 of 128): for each block cb the
+// gate columns [128 cb, +128) and the up columns [m + 128 cb, +128); wave w owns gate and up tile
+// 16w of each block (tiles 2 bb, 2 bb + 1).  More blocks per item share each staged activation step
+// among more weights.
+template <int MT, int MTMAX, int NB>
 __device__ __forceinline__ void gateup_item(const PfGemm& a, int e, int first, int len, int c, uint8_t* abuf, uint8_t* sbuf,
-                            int64_t* rowidx, float* ex) {
+                                            uint8_t* wsl, int64_t* rowidx, float* ex) {
   const int w = wave_id_uniform(), lane = lane_id(), nn = lane & 15, g = lane >> 4;
   item_rows<MT>(a, first, len, rowidx);
   __syncthreads();
-  const int cols[2] = {128 * c + 16 * w, a.m + 128 * c + 16 * w};
-  f32x4 acc[MT][2];
-  gemm_item<MT, 2, MTMAX>(a, e, cols, rowidx, abuf, sbuf, acc);
-  // epilogue per M-tile: gate/up tiles -> LDS [16][2][128] -> per row: H128, scale, SwiGLU, in_down, H128
-  const int64_t si = (int64_t)e * a.m + 128 * c + 2 * lane;
-  const float og0 = f16_to_f32(a.out_gate[si]), og1 = f16_to_f32(a.out_gate[si + 1]);
-  const float ou0 = f16_to_f32(a.out_up[si]), ou1 = f16_to_f32(a.out_up[si + 1]);
-  const float id0 = f16_to_f32(a.in_down[si]), id1 = f16_to_f32(a.in_down[si + 1]);
+  int cols[2 * NB];
 #pragma unroll
-  for (int mt = 0; mt < MT; mt++) {
+  for (int bb = 0; bb < NB; bb++) {
+    cols[2 * bb] = 128 * (c * NB + bb) + 16 * w;
+    cols[2 * bb + 1] = a.m + 128 * (c * NB + bb) + 16 * w;
+  }
+  f32x4 acc[MT][2 * NB];
+  gemm_item<MT, 2 * NB, MTMAX, 2>(a, e, cols, rowidx, abuf, sbuf, wsl, acc);
+  // epilogue per block and M-tile: gate/up tiles -> LDS [16][2][128] -> per row: H128, scale,
+  // SwiGLU, in_down, H128
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int r = 4 * g + i;
-      ex[(r * 2 + 0) * 128 + 16 * w + nn] = acc[mt][0][i];
-      ex[(r * 2 + 1) * 128 + 16 * w + nn] = acc[mt][1][i];
-    }
-    __syncthreads();
+  for (int bb = 0; bb < NB; bb++) {
+    const int cb = c * NB + bb;
+    const int64_t si = (int64_t)e * a.m + 128 * cb + 2 * lane;
+    const float og0 = f16_to_f32(a.out_gate[si]), og1 = f16_to_f32(a.out_gate[si + 1]);
+    const float ou0 = f16_to_f32(a.out_up[si]), ou1 = f16_to_f32(a.out_up[si + 1]);
+    const float id0 = f16_to_f32(a.in_down[si]), id1 = f16_to_f32(a.in_down[si + 1]);
 #pragma unroll
-    for (int rr = 0; rr < 2; rr++) {
-      const int r = 2 * w + rr;  // 8 waves x 2 rows
-      const int pr = mt * 16 + r;
-      if (pr < len) {
-        float g0 = ex[(r * 2) * 128 + 2 * lane], g1 = ex[(r * 2) * 128 + 2 * lane + 1];
-        float u0 = ex[(r * 2 + 1) * 128 + 2 * lane], u1 = ex[(r * 2 + 1) * 128 + 2 * lane + 1];
-        hadamard128_wave(g0, g1);
-        hadamard128_wave(u0, u1);
-        float h0 = swiglu_bf16(g0 * og0, u0 * ou0) * id0;
-        float h1 = swiglu_bf16(g1 * og1, u1 * ou1) * id1;
-        hadamard128_wave(h0, h1);
-        uint32_t lo[kPfLo], sc[kPfLo];
-        const uint32_t hi = hi_lo_terms(h0, h1, lo, sc);
-        const int64_t p = first + pr;
-        *reinterpret_cast<uint32_t*>(a.hhi + p * a.m + 128 * c + 2 * lane) = hi;
+    for (int mt = 0; mt < MT; mt++) {
 #pragma unroll
-        for (int t = 0; t < kPfLo; t++) {
-          *reinterpret_cast<uint16_t*>(a.hq + (t * a.nslots + p) * a.m + 128 * c + 2 * lane) = (uint16_t)lo[t];
-          if (nn == 0) a.hs[(t * a.nslots + p) * (a.m / 32) + 4 * c + g] = (uint8_t)sc[t];
+      for (int i = 0; i < 4; i++) {
+        const int r = 4 * g + i;
+        ex[(r * 2 + 0) * 128 + 16 * w + nn] = acc[mt][2 * bb][i];
+        ex[(r * 2 + 1) * 128 + 16 * w + nn] = acc[mt][2 * bb + 1][i];
+      }
+      __syncthreads();
+#pragma unroll
+      for (int rr = 0; rr < 2; rr++) {
+        const int r = 2 * w + rr;  // 8 waves x 2 rows
+        const int pr = mt * 16 + r;
+        if (pr < len) {
+          float g0 = ex[(r * 2) * 128 + 2 * lane], g1 = ex[(r * 2) * 128 + 2 * lane + 1];
+          float u0 = ex[(r * 2 + 1) * 128 + 2 * lane], u1 = ex[(r * 2 + 1) * 128 + 2 * lane + 1];
+          hadamard128_wave(g0, g1);
+          hadamard128_wave(u0, u1);
+          float h0 = swiglu_bf16(g0 * og0, u0 * ou0) * id0;
+          float h1 = swiglu_bf16(g1 * og1, u1 * ou1) * id1;
+          hadamard128_wave(h0, h1);
+          uint32_t lo[kPfLo], sc[kPfLo];
+          const uint32_t hi = hi_lo_terms(h0, h1, lo, sc);
+          const int64_t p = first + pr;
+          *reinterpret_cast<uint32_t*>(a.hhi + p * a.m + 128 * cb + 2 * lane) = hi;
+#pragma unroll
+          for (int t = 0; t < kPfLo; t++) {
+            *reinterpret_cast<uint16_t*>(a.hq + (t * a.nslots + p) * a.m + 128 * cb + 2 * lane) = (uint16_t)lo[t];
+            if (nn == 0) a.hs[(t * a.nslots + p) * (a.m / 32) + 4 * cb + g] = (uint8_t)sc[t];
+          }
         }
       }
+      __syncthreads();
     }
-    __syncthreads();
   }
 }
 
 // ---------------------------------------------------------------- down GEMM + value finish
-// Item = (plan block b, output block ob): columns [128 ob, +128); wave w owns tile 16w.
-template <int MT, int MTMAX>
+// Item = (plan block b, output blocks ob NB .. ob NB + NB - 1 of 128); wave w owns tile 16w of each.
+template <int MT, int MTMAX, int NB>
 __device__ __forceinline__ void down_item(const PfGemm& a, int e, int first, int len, int ob, uint8_t* abuf, uint8_t* sbuf,
-                          int64_t* rowidx, float* ex) {
+                                          uint8_t* wsl, int64_t* rowidx, float* ex) {
   const int w = wave_id_uniform(), lane = lane_id(), nn = lane & 15, g = lane >> 4;
   item_rows<MT>(a, first, len, rowidx);
   __syncthreads();
-  const int cols[1] = {128 * ob + 16 * w};
-  f32x4 acc[MT][1];
-  gemm_item<MT, 1, MTMAX>(a, e, cols, rowidx, abuf, sbuf, acc);
-  const int64_t si = (int64_t)e * a.N + 128 * ob + 2 * lane;
-  const float od0 = f16_to_f32(a.out_down[si]), od1 = f16_to_f32(a.out_down[si + 1]);
+  int cols[NB];
 #pragma unroll
-  for (int mt = 0; mt < MT; mt++) {
+  for (int bb = 0; bb < NB; bb++) cols[bb] = 128 * (ob * NB + bb) + 16 * w;
+  f32x4 acc[MT][NB];
+  gemm_item<MT, NB, MTMAX, 2>(a, e, cols, rowidx, abuf, sbuf, wsl, acc);
 #pragma unroll
-    for (int i = 0; i < 4; i++) ex[(4 * g + i) * 128 + 16 * w + nn] = acc[mt][0][i];
-    __syncthreads();
+  for (int bb = 0; bb < NB; bb++) {
+    const int cb = ob * NB + bb;
+    const int64_t si = (int64_t)e * a.N + 128 * cb + 2 * lane;
+    const float od0 = f16_to_f32(a.out_down[si]), od1 = f16_to_f32(a.out_down[si + 1]);
 #pragma unroll
-    for (int rr = 0; rr < 2; rr++) {
-      const int r = 2 * w + rr;
-      const int pr = mt * 16 + r;
-      if (pr < len) {
-        float v0 = ex[r * 128 + 2 * lane], v1 = ex[r * 128 + 2 * lane + 1];
-        hadamard128_wave(v0, v1);
-        const int slot = a.order[first + pr];
-        const uint32_t pk = (uint32_t)f32_to_bf16(v0 * od0) | ((uint32_t)f32_to_bf16(v1 * od1) << 16);
-        *reinterpret_cast<uint32_t*>(a.values + (int64_t)slot * a.N + 128 * ob + 2 * lane) = pk;
+    for (int mt = 0; mt < MT; mt++) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) ex[(4 * g + i) * 128 + 16 * w + nn] = acc[mt][bb][i];
+      __syncthreads();
+#pragma unroll
+      for (int rr = 0; rr < 2; rr++) {
+        const int r = 2 * w + rr;
+        const int pr = mt * 16 + r;
+        if (pr < len) {
+          float v0 = ex[r * 128 + 2 * lane], v1 = ex[r * 128 + 2 * lane + 1];
+          hadamard128_wave(v0, v1);
+          const int slot = a.order[first + pr];
+          const uint32_t pk = (uint32_t)f32_to_bf16(v0 * od0) | ((uint32_t)f32_to_bf16(v1 * od1) << 16);
+          *reinterpret_cast<uint32_t*>(a.values + (int64_t)slot * a.N + 128 * cb + 2 * lane) = pk;
+        }
       }
+      __syncthreads();
     }
-    __syncthreads();
   }
 }
 
 // Grid: (plan blocks) x (output blocks per item).  Items of MTMIN..MTMAX M-tiles only (the others
-// exit at once): the small class needs little LDS, so several blocks share a CU.  Dynamic LDS:
-// double-buffered activation stage, scale stage, row map (the epilogue exchange reuses the stage).
+// exit at once).  Dynamic LDS: double-buffered activation stage, its scale stage and the row map
+// (the epilogue exchange reuses the stage), then per wave its tiles' weight scales.
 template <int MTMIN, int MTMAX>
 constexpr size_t pf_lds_bytes() {
   return 2 * PfStage<MTMAX>::kBytes + 2 * PfStage<MTMAX>::kScaleBytes + MTMAX * 16 * sizeof(int64_t);
+}
+// per wave: NT tiles x 16 rows x K/32 scale bytes
+inline size_t pf_wscale_lds_bytes(int nt, int K) { return (size_t)kPfWaves * nt * 16 * (K / 32); }
+// 128-column output blocks per item: two for the small items (activations re-staged half as often
+// per weight byte), one for the large ones (register budget)
+__host__ __device__ constexpr int pf_blocks_per_item(int mtmax) { return mtmax <= 2 ? 2 : 1; }
+// LDS of the small and large GEMM kernels (GATE: gate/up, K = hidden; else down, K = intermediate)
+inline size_t pf_small_lds(bool gate, int K) {
+  return pf_lds_bytes<1, 2>() + pf_wscale_lds_bytes((gate ? 2 : 1) * pf_blocks_per_item(2), K);
+}
+inline size_t pf_large_lds(bool gate, int K) {
+  return pf_lds_bytes<3, 4>() + pf_wscale_lds_bytes((gate ? 2 : 1) * pf_blocks_per_item(4), K);
 }
 
 template <bool GATE, int MTMIN, int MTMAX>
@@ -518,8 +579,22 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm_kernel(PfGemm a) {
   int64_t* rowidx = reinterpret_cast<int64_t*>(sbuf + 2 * PfStage<MTMAX>::kScaleBytes);
   static_assert(2 * PfStage<1>::kBytes >= 16 * 2 * 128 * 4, "the epilogue exchange must fit in the stage");
   float* ex = reinterpret_cast<float*>(abuf);
-  const int outblocks = GATE ? a.m / 128 : a.N / 128;
-  const int b = blockIdx.x / outblocks, ob = blockIdx.x % outblocks;
+  constexpr int kNB = pf_blocks_per_item(MTMAX), kNT = GATE ? 2 * kNB : kNB;
+  uint8_t* wsl = pf_lds + pf_lds_bytes<MTMIN, MTMAX>() + wave_id_uniform() * kNT * 16 * (a.K / 32);
+  const int outblocks = (GATE ? a.m : a.N) / (128 * kNB);
+  // Workgroups are dealt to the 8 XCDs in turn.  Small items: the outblocks items of one plan block
+  // go to one XCD, so its activation rows are read into one L2 (workgroup i -> plan block
+  // 8 (i / 8 outblocks) + i % 8, output block (i % 8 outblocks) / 8).  Large items (the blocks of
+  // the popular experts): consecutive plan blocks of an output block share an XCD and its weights.
+  int b, ob;
+  if (MTMAX <= 2) {
+    const int grp = blockIdx.x / (8 * outblocks), r = blockIdx.x % (8 * outblocks);
+    b = 8 * grp + r % 8;
+    ob = r / 8;
+  } else {
+    b = blockIdx.x / outblocks;
+    ob = blockIdx.x % outblocks;
+  }
   if (b >= *a.nblk) return;
   const int e = a.blk[b], first = a.blk[a.cap + b], len = a.blk[2 * a.cap + b];
   const int mt = (len + 15) / 16;
@@ -528,9 +603,9 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm_kernel(PfGemm a) {
   case M:                                                                                   \
     if (M >= MTMIN && M <= MTMAX) {                                                         \
       if (GATE)                                                                             \
-        gateup_item<(M <= MTMAX ? M : 1), MTMAX>(a, e, first, len, ob, abuf, sbuf, rowidx, ex); \
+        gateup_item<(M <= MTMAX ? M : 1), MTMAX, kNB>(a, e, first, len, ob, abuf, sbuf, wsl, rowidx, ex); \
       else                                                                                  \
-        down_item<(M <= MTMAX ? M : 1), MTMAX>(a, e, first, len, ob, abuf, sbuf, rowidx, ex);   \
+        down_item<(M <= MTMAX ? M : 1), MTMAX, kNB>(a, e, first, len, ob, abuf, sbuf, wsl, rowidx, ex);     \
     }                                                                                       \
     break;
   switch (mt) {
@@ -544,15 +619,23 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm_kernel(PfGemm a) {
 }
 
 template <bool GATE>
-int launch_pf_gemm(const PfGemm& a, int outblocks, hipStream_t s) {
-  const dim3 grid((unsigned)(a.cap * outblocks)), block(kPfThreads);
-  constexpr size_t small_lds = pf_lds_bytes<1, 2>(), large_lds = pf_lds_bytes<3, 4>();
+int launch_pf_gemm(const PfGemm& a, hipStream_t s) {
+  const int n128 = (GATE ? a.m : a.N) / 128;  // 128-column output blocks
+  // whole groups of 8 plan blocks (b < *nblk <= cap is checked in the kernel)
+  const unsigned groups = (unsigned)((a.cap + 7) / 8 * 8);
+  const size_t small_lds = pf_small_lds(GATE, a.K), large_lds = pf_large_lds(GATE, a.K);
+  if (small_lds > kPfMaxLds || large_lds > kPfMaxLds)
+    return fail(MOE_EINVAL, "prefill GEMM needs %zu / %zu B of LDS (K = %d)", small_lds, large_lds, a.K);
   // dynamic LDS beyond 64 KB must be allowed explicitly (idempotent; cheap)
+  MOE_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&pf_gemm_kernel<GATE, 1, 2>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)small_lds));
   MOE_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&pf_gemm_kernel<GATE, 3, 4>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)large_lds));
-  hipLaunchKernelGGL((pf_gemm_kernel<GATE, 1, 2>), grid, block, small_lds, s, a);
+  hipLaunchKernelGGL((pf_gemm_kernel<GATE, 1, 2>), dim3(groups * (n128 / pf_blocks_per_item(2))), dim3(kPfThreads),
+                     small_lds, s, a);
   MOE_HIP(hipGetLastError());
-  hipLaunchKernelGGL((pf_gemm_kernel<GATE, 3, 4>), grid, block, large_lds, s, a);
+  hipLaunchKernelGGL((pf_gemm_kernel<GATE, 3, 4>), dim3(groups * (n128 / pf_blocks_per_item(4))), dim3(kPfThreads),
+                     large_lds, s, a);
   MOE_HIP(hipGetLastError());
   return MOE_OK;
 }
@@ -693,6 +776,10 @@ int moe_mxfp4_prefill(const uint16_t* x, const uint16_t* residual, int rows, con
   MOE_ARG(hidden % 1024 == 0 && hidden > 0, "hidden must be a positive multiple of 1024 (got %d)", hidden);
   MOE_ARG(intermediate % 256 == 0 && intermediate > 0, "intermediate must be a positive multiple of 256 (got %d)",
           intermediate);
+  MOE_ARG(pf_small_lds(true, hidden) <= kPfMaxLds && pf_large_lds(true, hidden) <= kPfMaxLds &&
+              pf_small_lds(false, intermediate) <= kPfMaxLds && pf_large_lds(false, intermediate) <= kPfMaxLds,
+          "hidden %d / intermediate %d too large for the prefill GEMM's LDS", hidden, intermediate);
+  MOE_ARG(((uintptr_t)gate_up_scales | (uintptr_t)down_scales) % 16 == 0, "weight scale arrays must be 16-byte aligned");
   MOE_ARG(workspace != nullptr, "workspace must not be NULL");
   const PfWorkspace w = pf_carve(workspace, rows, hidden, intermediate, experts);
   if (workspace_bytes < w.bytes)
@@ -739,7 +826,7 @@ int moe_mxfp4_prefill(const uint16_t* x, const uint16_t* residual, int rows, con
   g.hq = w.hq;
   g.hs = w.hs;
   g.nslots = n;
-  if ((rc = launch_pf_gemm<true>(g, intermediate / 128, s))) return rc;
+  if ((rc = launch_pf_gemm<true>(g, s))) return rc;
   // down GEMM + value finish -> per-slot values
   PfGemm d{};
   d.codes = down_codes;
@@ -759,7 +846,7 @@ int moe_mxfp4_prefill(const uint16_t* x, const uint16_t* residual, int rows, con
   d.m = intermediate;
   d.out_down = out_down;
   d.values = w.values;
-  if ((rc = launch_pf_gemm<false>(d, hidden / 128, s))) return rc;
+  if ((rc = launch_pf_gemm<false>(d, s))) return rc;
   hipLaunchKernelGGL(pf_combine_kernel, dim3(rows), dim3(256), 0, s, w.values, sc, residual, hidden, out);
   MOE_HIP(hipGetLastError());
   return MOE_OK;
