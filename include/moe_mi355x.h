@@ -203,6 +203,22 @@ int moe_mxfp4_prefill(const uint16_t* x, const uint16_t* residual, int rows, con
                       float* scores, void* workspace, size_t workspace_bytes, moe_stream_t stream);
 size_t moe_mxfp4_prefill_workspace_bytes(int rows, int hidden, int intermediate, int64_t experts);
 
+/* ---------------------------------------------------------------- load-time conversion */
+
+/* K4 trellis experts of one projection -> MXFP4 rows of the joined resident format: for every
+ * expert e of `packed` (packed_bytes / (in*out/2) experts), inner_e = decoded [in, out] matrix;
+ * gate/up (in_scale [E, in] and unit [in] fp16 given): inner_e[k, :] *= in_scale[e, k] * unit[k];
+ * down: both NULL.  Row n of inner_e^T is quantised (groups of 32 along in, shared exponent
+ * floor(log2 amax) - 2 as e8m0, E2M1 codes round-to-nearest-even, saturating; low nibble = even k)
+ * into codes [E, out_rows, in/2] and scales [E, out_rows, in/32] at row row_offset + n (gate/up:
+ * out_rows = 2 out, offsets 0 and out; down: out_rows = out, offset 0).  Workspace:
+ * moe_k4_to_mxfp4_workspace_bytes(in, out) (one decoded expert).
+ * Replaces: exlr8/joined_mxfp4.py:12-47 encode (one projection; mx.quantize(mode="mxfp4")). */
+int moe_k4_to_mxfp4(const void* packed, int64_t packed_bytes, int in_features, int out_features, int side,
+                    const uint16_t* in_scale, const uint16_t* unit, uint8_t* codes, uint8_t* scales, int out_rows,
+                    int row_offset, void* workspace, size_t workspace_bytes, moe_stream_t stream);
+size_t moe_k4_to_mxfp4_workspace_bytes(int in_features, int out_features);
+
 /* ---------------------------------------------------------------- workspace */
 
 /* Bytes of workspace needed by the decode entry points above for the given shape on the

@@ -15,20 +15,52 @@ BF16 = torch.bfloat16
 
 
 def encode(expert):
-    """Load-time K4 -> MXFP4 conversion (exlr8/joined_mxfp4.py:12-47).
+    """Load-time K4 -> joined MXFP4 (exlr8/joined_mxfp4.py:12-47), on the GPU.
 
-    Not part of this build: the reference quantises with MLX's ``mx.quantize(mode="mxfp4")``,
-    whose scale/rounding choice cannot be pinned here.  Construct ``JoinedMXFP4`` from MXFP4
-    tensors directly.
+    ``expert`` is a K4 ``ExpertLayer`` (packed gate/up/down, (in, out) scale pairs).  Returns
+    ``(unit, weights)``: ``unit`` = sign of expert 0's gate input scales, fp16 [1, h];
+    ``weights = {"gate_up": (codes [E, 2m, h/2], scales [E, 2m, h/32], None),
+    "down": (codes [E, h, m/2], scales [E, h, m/32], None)}`` (uint8; low nibble = even k).  Gate
+    and up are decoded, multiplied per input channel by ``in_scale * unit`` and quantised along
+    their input dimension; down is quantised as decoded.  The MXFP4 rounding is the OCP MX
+    conversion (shared exponent floor(log2 amax) - 2, E2M1 round-to-nearest-even, saturating):
+    the reference's ``mx.quantize`` cannot be run here to confirm its choice.
     """
-    raise NotImplementedError("K4 -> MXFP4 encoding is not built (MLX quantizer parity is unpinned)")
+    h, m, experts = expert.hidden, expert.intermediate, expert.experts
+    dev = expert.packed["gate"].device
+    unit = torch.sign(expert.scales["gate"][0][:1]).to(torch.float16).contiguous()
+    u8 = dict(dtype=torch.uint8, device=dev)
+    gate_up = (torch.empty((experts, 2 * m, h // 2), **u8), torch.empty((experts, 2 * m, h // 32), **u8))
+    down = (torch.empty((experts, h, m // 2), **u8), torch.empty((experts, h, m // 32), **u8))
+    need = max(lib().moe_k4_to_mxfp4_workspace_bytes(h, m), lib().moe_k4_to_mxfp4_workspace_bytes(m, h))
+    ws = torch.empty(need, **u8)
+    st = stream(dev)
+    for projection, (inc, out, side, dest, rows, offset) in (("gate", (h, m, 1, gate_up, 2 * m, 0)),
+                                                            ("up", (h, m, 1, gate_up, 2 * m, m)),
+                                                            ("down", (m, h, 2, down, h, 0))):
+        packed = expert.packed[projection].contiguous()
+        in_scale = expert.scales[projection][0].to(torch.float16).contiguous() if side == 1 else None
+        check(lib().moe_k4_to_mxfp4(ptr(packed), packed.numel() * packed.element_size(), inc, out, side,
+                                    ptr(in_scale) if in_scale is not None else None,
+                                    ptr(unit) if in_scale is not None else None, ptr(dest[0]), ptr(dest[1]), rows,
+                                    offset, ptr(ws), ws.numel(), st))
+    return unit, {"gate_up": gate_up + (None,), "down": down + (None,)}
 
 
 class JoinedMXFP4:
     """``weights = {"gate_up": (codes, scales), "down": (codes, scales)}``, ``unit`` fp16 [h],
     ``scales = {"gate": (None, out_gate), "up": (None, out_up), "down": (in_down, out_down)}``."""
 
-    def __init__(self, weights, unit, scales, hidden, intermediate):
+    def __init__(self, weights, unit=None, scales=None, hidden=None, intermediate=None):
+        if unit is None:
+            # JoinedMXFP4(expert) as in the reference (exlr8/joined_mxfp4.py:137-142): encode the
+            # K4 expert layer on the GPU
+            expert = weights
+            unit, weights = encode(expert)
+            scales = {"gate": (None, expert.scales["gate"][1]), "up": (None, expert.scales["up"][1]),
+                      "down": tuple(expert.scales["down"])}
+            hidden, intermediate = expert.hidden, expert.intermediate
+        weights = {p: tuple(v[:2]) for p, v in weights.items()}
         self.weights, self.unit, self.scales = weights, unit, scales
         self.hidden, self.intermediate = hidden, intermediate
         codes, sc = weights["gate_up"]

@@ -40,6 +40,8 @@ class _Oracle:
             "orc_swiglu_bf16": (f32, [f32, f32]),
             "orc_k4_linear": (None, [vp, vp, i32, vp, i32, i32, i32, i32, vp, vp, vp]),
             "orc_mxfp4_linear": (None, [vp, vp, i32, vp, vp, i32, i32, vp]),
+            "orc_mx_quantize_row": (None, [vp, i32, vp, vp]),
+            "orc_k4_to_mxfp4": (None, [vp, i32, i32, i32, i64, vp, vp, vp, vp, i32, i32]),
             "orc_k4_moe": (None, [vp, vp, vp, vp, i32, i32, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]),
             "orc_mxfp4_moe": (None, [vp, vp, vp, vp, i32, i32, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]),
             "orc_residual_rmsnorm": (None, [vp, vp, vp, i32, i32, f32, vp, vp]),
@@ -110,6 +112,26 @@ class _Oracle:
         y = np.empty((x.shape[0], N), np.float32)
         self.h.orc_mxfp4_linear(_p(x), _p(ids), x.shape[0], _p(np.ascontiguousarray(codes)), _p(np.ascontiguousarray(scales)), K, N, _p(y))
         return y
+
+    def mx_quantize(self, v):
+        """rows of float32 values [..., n] (n % 32 == 0) -> (codes uint8 [..., n/2], scales uint8 [..., n/32])"""
+        v = np.ascontiguousarray(v, np.float32)
+        n = v.shape[-1]
+        flat = v.reshape(-1, n)
+        codes = np.empty((flat.shape[0], n // 2), np.uint8)
+        scales = np.empty((flat.shape[0], n // 32), np.uint8)
+        for r in range(flat.shape[0]):
+            self.h.orc_mx_quantize_row(_p(flat[r]), n, _p(codes[r]), _p(scales[r]))
+        return codes.reshape(*v.shape[:-1], n // 2), scales.reshape(*v.shape[:-1], n // 32)
+
+    def k4_to_mxfp4(self, packed, in_f, out_f, side, experts, in_scale, unit, codes, scales, row_offset):
+        """fills codes [E, out_rows, in/2] / scales [E, out_rows, in/32] (uint8, C-contiguous) in place"""
+        assert codes.flags.c_contiguous and scales.flags.c_contiguous
+        ins = None if in_scale is None else np.ascontiguousarray(in_scale, np.uint16)
+        un = None if unit is None else np.ascontiguousarray(unit, np.uint16)
+        self.h.orc_k4_to_mxfp4(_p(np.ascontiguousarray(packed)), in_f, out_f, side, experts,
+                               None if ins is None else _p(ins), None if un is None else _p(un),
+                               _p(codes), _p(scales), codes.shape[1], row_offset)
 
     def k4_moe(self, x, idx9, scores8, residual, h, m, pg, pu, pd, in_g, out_g, in_u, out_u, in_d, out_d, want_values=False):
         x = np.ascontiguousarray(x, np.uint16).reshape(-1, h)

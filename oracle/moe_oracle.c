@@ -32,6 +32,18 @@
  *   orc_k4_moe / orc_mxfp4_moe  model.py:406-418, fast_decode_finish_fused.metal:24-63
  *   orc_residual_rmsnorm  residual_rms.metal:18-90 (rms_looped), model.py:376-384
  *   orc_segment_table     fast_prefill.py:19-46  brute-force counting on small inputs
+ *   orc_mx_quantize_row / orc_k4_to_mxfp4  joined_mxfp4.py:12-47 (encode)
+ *                                               orientation, fold and layout: the reference's
+ *                                               tests/test_joined_mxfp4.py:44-58 structure
+ *                                               (decode, x factor per input channel, quantise
+ *                                               the transpose, gate||up rows); quantiser: every
+ *                                               element within half an E2M1 step of its value,
+ *                                               exact groups reproduced, zero and saturating
+ *                                               groups.  The scale and rounding choice of MLX's
+ *                                               mx.quantize(mode="mxfp4") is PARITY UNPINNED
+ *                                               (MLX absent): this restates the OCP MX v1.0
+ *                                               conversion (shared exponent floor(log2 amax) - 2,
+ *                                               elements round-to-nearest-even, saturating at 6)
  */
 #include <math.h>
 #include <stdint.h>
@@ -316,6 +328,71 @@ static void mxfp4_linear_one(const float* x, const uint8_t* codes, const uint8_t
     }
     y[n] = (float)acc;
   }
+}
+
+/* ---------------- MXFP4 encode (joined_mxfp4.py:12-47) ---------------- */
+/* E2M1 code of |a| (a = v / 2^s): nearest of 0, .5, 1, 1.5, 2, 3, 4, 6, ties to the even code, saturating */
+static uint32_t e2m1_code(float a) {
+  if (a <= 0.25f) return 0;
+  if (a < 0.75f) return 1;
+  if (a <= 1.25f) return 2;
+  if (a < 1.75f) return 3;
+  if (a <= 2.5f) return 4;
+  if (a < 3.5f) return 5;
+  if (a <= 5.0f) return 6;
+  return 7;
+}
+
+/* One row of n values (n % 32 == 0) -> n/2 code bytes (low nibble = even k) and n/32 e8m0 scales.
+ * Shared exponent s = floor(log2 amax) - 2 clamped to [-127, 127] (e8m0 byte s + 127; an all-zero
+ * group gets byte 0); element code = sign | E2M1(|v| / 2^s). */
+void orc_mx_quantize_row(const float* v, int n, uint8_t* codes, uint8_t* scales) {
+  for (int g = 0; g < n / 32; g++) {
+    const float* x = v + 32 * g;
+    float amax = 0.0f;
+    for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(x[i]));
+    int s = -127;
+    if (amax > 0.0f) {
+      int ex;
+      frexpf(amax, &ex);  /* amax = m 2^ex, m in [0.5, 1): floor(log2 amax) = ex - 1 */
+      s = ex - 1 - 2;
+      if (s < -127) s = -127;
+      if (s > 127) s = 127;
+    }
+    scales[g] = (uint8_t)(s + 127);
+    for (int i = 0; i < 32; i += 2) {
+      uint32_t c[2];
+      for (int j = 0; j < 2; j++) {
+        const float xv = x[i + j];
+        c[j] = e2m1_code(ldexpf(fabsf(xv), -s)) | (signbit(xv) ? 8u : 0u);
+      }
+      codes[16 * g + i / 2] = (uint8_t)(c[0] | (c[1] << 4));
+    }
+  }
+}
+
+/* Encode one projection of every expert: inner_e = decode(packed, e) [in, out]; gate/up (in_scale
+ * non-null): inner_e[k, :] *= float(in_scale[e, k] * unit[k]); each output row n of inner_e^T is
+ * quantised into codes[e][row_offset + n][in/2], scales[e][row_offset + n][in/32] of arrays with
+ * out_rows rows per expert (gate at 0 and up at m of the joined gate_up; down at 0). */
+void orc_k4_to_mxfp4(const uint8_t* packed, int in_f, int out_f, int side, int64_t experts, const uint16_t* in_scale,
+                     const uint16_t* unit, uint8_t* codes, uint8_t* scales, int out_rows, int row_offset) {
+  float* inner = (float*)malloc(sizeof(float) * (size_t)in_f * out_f);
+  float* row = (float*)malloc(sizeof(float) * (size_t)in_f);
+  for (int64_t e = 0; e < experts; e++) {
+    orc_decode_trellis(packed, 4, in_f, out_f, side, e, inner);
+    for (int n = 0; n < out_f; n++) {
+      for (int k = 0; k < in_f; k++) {
+        float v = inner[(int64_t)k * out_f + n];
+        if (in_scale) v *= f16_to_f32(in_scale[e * in_f + k]) * f16_to_f32(unit[k]);
+        row[k] = v;
+      }
+      const int64_t r = e * out_rows + row_offset + n;
+      orc_mx_quantize_row(row, in_f, codes + r * (in_f / 2), scales + r * (in_f / 32));
+    }
+  }
+  free(row);
+  free(inner);
 }
 
 void orc_mxfp4_linear(const float* x, const uint32_t* ids, int slots, const uint8_t* codes, const uint8_t* scales,
