@@ -58,32 +58,68 @@ __global__ __launch_bounds__(256) void router_logits_small(const uint16_t* __res
 }
 
 // ---------------------------------------------------------------- logits, prefill batches
-// 16 rows x 16 experts per block on the fp32 matrix cores (v_mfma_f32_16x16x4_f32); the 4 waves
-// split K and their tiles are summed in LDS in wave order.  Lane l = 16 kk + r loads 4 consecutive
-// k of row r of x and of expert r of w; MFMA j takes element j, so its k-group kk covers k0+4kk+j.
-__global__ __launch_bounds__(256) void router_logits_mfma(const uint16_t* __restrict__ x,
-                                                          const float* __restrict__ w, int rows, int hidden,
-                                                          int experts, float* __restrict__ logits) {
-  __shared__ f32x4 red[4][64];
-  const int r0 = blockIdx.y * 16, e0 = blockIdx.x * 16;
-  const int wv = wave_id_uniform(), lane = lane_id(), r = lane & 15, kk = lane >> 4;
-  const int kq = hidden / 4;
-  const uint16_t* __restrict__ xr = x + (int64_t)min(r0 + r, rows - 1) * hidden + wv * kq + 4 * kk;
-  const float* __restrict__ wr = w + (int64_t)min(e0 + r, experts - 1) * hidden + wv * kq + 4 * kk;
-  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 4
-  for (int k = 0; k < kq; k += 16) {
-    const u32x2 xv = *reinterpret_cast<const u32x2*>(xr + k);
-    const f32x4 wvv = *reinterpret_cast<const f32x4*>(wr + k);
-    const float xa[4] = {bf16_to_f32((uint16_t)(xv.x & 0xFFFFu)), bf16_to_f32((uint16_t)(xv.x >> 16)),
-                         bf16_to_f32((uint16_t)(xv.y & 0xFFFFu)), bf16_to_f32((uint16_t)(xv.y >> 16))};
-#pragma unroll
-    for (int j = 0; j < 4; j++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[j], wvv[j], acc, 0, 0, 0);
+// 16 rows x 16 experts per block on the fp32 matrix cores (v_mfma_f32_16x16x4_f32); the 16 waves
+// split K into 16 chunks and the chunk tiles are summed in LDS in chunk order.  Which wave takes
+// which chunk rotates with the block, so the blocks do not all read the same k offsets at once.
+// Per 64-wide k step, lane l = 16 kk + r loads 16 consecutive k (32 B of x row r, 64 B of w row r)
+// at 16 kk: a row's four lanes read whole 128 B lines.  MFMA i (0..15) takes element i, so its
+// k-group kk covers k0 + 16 kk + i.
+constexpr int kLogitWaves = 16;
+__global__ __launch_bounds__(kLogitWaves * 64) void router_logits_mfma(const uint16_t* __restrict__ x,
+                                                                      const float* __restrict__ w, int rows,
+                                                                      int hidden, int experts,
+                                                                      float* __restrict__ logits) {
+  __shared__ f32x4 red[kLogitWaves][64];
+  // 1-D grid of (expert blocks) x (row blocks).  Workgroups are dealt to the 8 XCDs in turn; when
+  // the expert blocks split evenly over them, XCD x takes expert blocks [x n/8, (x+1) n/8) for
+  // every row block (its slice of w stays in its L2, and the row block's x is read once per XCD)
+  const int neb = (experts + 15) / 16;
+  int bx, by;
+  if (neb % 8 == 0) {
+    const int per = neb / 8, j = blockIdx.x / 8;
+    bx = (blockIdx.x % 8) * per + j % per;
+    by = j / per;
+  } else {
+    bx = blockIdx.x % neb;
+    by = blockIdx.x / neb;
   }
-  red[wv][lane] = acc;
+  const int r0 = by * 16, e0 = bx * 16;
+  const int wv = wave_id_uniform(), lane = lane_id(), r = lane & 15, kk = lane >> 4;
+  const int chunk = (wv + 5 * bx + 3 * by) % kLogitWaves;
+  const int kq = hidden / kLogitWaves;  // a multiple of 64 (hidden % 1024 == 0)
+  const uint16_t* __restrict__ xr = x + (int64_t)min(r0 + r, rows - 1) * hidden + chunk * kq + 16 * kk;
+  const float* __restrict__ wr = w + (int64_t)min(e0 + r, experts - 1) * hidden + chunk * kq + 16 * kk;
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  // two 64-wide steps per batch: all of a batch's loads are issued before its MFMAs
+  for (int k0 = 0; k0 < kq; k0 += 128) {
+    u32x4 xv[2][2];
+    f32x4 wvv[2][4];
+#pragma unroll
+    for (int b = 0; b < 2; b++) {
+      const int k = min(k0 + 64 * b, kq - 64);  // past the end: re-read the last step (not used)
+#pragma unroll
+      for (int i = 0; i < 2; i++) xv[b][i] = *reinterpret_cast<const u32x4*>(xr + k + 8 * i);
+#pragma unroll
+      for (int i = 0; i < 4; i++) wvv[b][i] = *reinterpret_cast<const f32x4*>(wr + k + 4 * i);
+    }
+#pragma unroll
+    for (int b = 0; b < 2; b++) {
+      if (k0 + 64 * b < kq) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+          const uint32_t xw = xv[b][i >> 3][(i >> 1) & 3];
+          const float xa = bf16_to_f32((uint16_t)((i & 1) ? (xw >> 16) : (xw & 0xFFFFu)));
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xa, wvv[b][i >> 2][i & 3], acc, 0, 0, 0);
+        }
+      }
+    }
+  }
+  red[chunk][lane] = acc;
   __syncthreads();
   if (wv == 0) {
-    const f32x4 t = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
+    f32x4 t = red[0][lane];
+#pragma unroll
+    for (int i = 1; i < kLogitWaves; i++) t = t + red[i][lane];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const int row = r0 + 4 * kk + i, e = e0 + r;  // D[4 kk + i][r]
@@ -245,8 +281,9 @@ int launch_router_logits(const uint16_t* x, const float* w, int rows, int hidden
     hipLaunchKernelGGL(router_logits_small<kMaxRows>, dim3(experts), dim3(256), 0, s, x, w, rows, hidden, experts,
                        logits);
   } else {
-    dim3 grid((experts + 15) / 16, (rows + 15) / 16);
-    hipLaunchKernelGGL(router_logits_mfma, grid, dim3(256), 0, s, x, w, rows, hidden, experts, logits);
+    const unsigned grid = (unsigned)((experts + 15) / 16) * (unsigned)((rows + 15) / 16);
+    hipLaunchKernelGGL(router_logits_mfma, dim3(grid), dim3(kLogitWaves * 64), 0, s, x, w, rows, hidden, experts,
+                       logits);
   }
   MOE_HIP(hipGetLastError());
   return MOE_OK;
