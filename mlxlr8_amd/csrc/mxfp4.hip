@@ -140,16 +140,25 @@ __global__ __launch_bounds__(kMxThreads) void mx_gemv_kernel(MxArgs a) {
     const int s = s0 + q;
     float* dst = xs[q];
     if (MODE == MX_GATEUP) {
-      // H128(x_row * unit) for the slot's token row, one 128-block per wave iteration
+      // H128(x_row * unit) for the slot's token row: the wave's K/128/waves blocks, all loads
+      // issued before the first transform (one memory round trip)
       const int row = s / a.slots_per_row;
-      for (int blk = wv; blk < K / 128; blk += kMxWaves) {
-        const int c = blk * 128 + 2 * lane;
-        const uint16_t* xr = a.x_bf16 + (int64_t)row * K + c;
-        float v0 = bf16_to_f32(xr[0]) * f16_to_f32(a.unit[c]);
-        float v1 = bf16_to_f32(xr[1]) * f16_to_f32(a.unit[c + 1]);
+      constexpr int kPer = K / 128 / kMxWaves;
+      static_assert(kPer * 128 * kMxWaves == K, "whole 128-blocks per wave");
+      uint32_t xv[kPer], uv[kPer];
+#pragma unroll
+      for (int i = 0; i < kPer; i++) {
+        const int c = (wv + i * kMxWaves) * 128 + 2 * lane;
+        xv[i] = *reinterpret_cast<const uint32_t*>(a.x_bf16 + (int64_t)row * K + c);
+        uv[i] = *reinterpret_cast<const uint32_t*>(a.unit + c);
+      }
+#pragma unroll
+      for (int i = 0; i < kPer; i++) {
+        const int c = (wv + i * kMxWaves) * 128 + 2 * lane;
+        float v0 = bf16_to_f32((uint16_t)(xv[i] & 0xFFFFu)) * f16_to_f32((uint16_t)(uv[i] & 0xFFFFu));
+        float v1 = bf16_to_f32((uint16_t)(xv[i] >> 16)) * f16_to_f32((uint16_t)(uv[i] >> 16));
         hadamard128_wave(v0, v1);
-        dst[c] = v0;
-        dst[c + 1] = v1;
+        *reinterpret_cast<f32x2*>(dst + c) = f32x2{v0, v1};
       }
     } else {
       for (int c = threadIdx.x * 4; c < K; c += kMxThreads * 4)
