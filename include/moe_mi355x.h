@@ -203,6 +203,21 @@ int moe_mxfp4_prefill(const uint16_t* x, const uint16_t* residual, int rows, con
                       float* scores, void* workspace, size_t workspace_bytes, moe_stream_t stream);
 size_t moe_mxfp4_prefill_workspace_bytes(int rows, int hidden, int intermediate, int64_t experts);
 
+/* Grouped K4 expert MLP over many rows (prefill): values[slot] = T(out_down[e] * H(H(h) @ down_e))
+ * with h = H(swiglu_T(gate, up) * in_down[e]), gate/up = out_scale * H(H(x * in_scale[e]) @ inner_e),
+ * for ids [rows, slots] (flat ids < experts; x [rows, hidden] bf16 shared by a row's slots).
+ * Slots are sorted by expert into blocks of <= 64 rows; every expert's weights are streamed once
+ * per block and 256-column group.  values [rows*slots, hidden] bf16 in slot order; side vectors
+ * and packed layouts as moe_k4_mlp; hidden and intermediate multiples of 256.
+ * Workspace: moe_k4_grouped_mlp_workspace_bytes(rows, slots, hidden, intermediate, experts).
+ * Replaces: exlr8/fast_prefill.py:188-211 grouped_expert_mlp (sorted block-table trellis GEMMs). */
+int moe_k4_grouped_mlp(const uint16_t* x, const uint32_t* ids, int rows, int slots, const void* packed_gate,
+                       const void* packed_up, const void* packed_down, int64_t packed_bytes, const uint16_t* in_gate,
+                       const uint16_t* out_gate, const uint16_t* in_up, const uint16_t* out_up,
+                       const uint16_t* in_down, const uint16_t* out_down, int hidden, int intermediate,
+                       uint16_t* values, void* workspace, size_t workspace_bytes, moe_stream_t stream);
+size_t moe_k4_grouped_mlp_workspace_bytes(int rows, int slots, int hidden, int intermediate, int64_t experts);
+
 /* ---------------------------------------------------------------- load-time conversion */
 
 /* K4 trellis experts of one projection -> MXFP4 rows of the joined resident format: for every

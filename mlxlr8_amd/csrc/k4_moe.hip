@@ -183,13 +183,6 @@ struct GemvArgs {
   uint16_t* out;               // COMBINE [rows, out_f]
 };
 
-__device__ __forceinline__ uint64_t chunk_offset(int side, uint64_t e, uint32_t ob, uint32_t tk, uint32_t it,
-                                                 uint32_t obs) {
-  // 1 KB chunk (8 tiles of 128 B) of expert e, output block ob, input tile tk
-  if (side == 2) return ((((e * (it / 8u) + tk / 8u) * obs + ob) * 8u + tk % 8u) << 10);
-  return (((e * obs + ob) * it + tk) << 10);
-}
-
 // Static split of n work units over nw waves: every wave takes `base` units and the first `rem`
 // waves one more, so a wave's range start is a multiply-add (no division in the finish path).
 struct Split {
@@ -403,17 +396,6 @@ __device__ __forceinline__ void complete_visit(const GemvArgs& a, const Plan* __
 //     and 2t+1 for token row t of the unit; staged once per 128-row block in the wave's LDS slice
 //     in A order.
 //   * D[2t] + 2^-11 * D[2t+1] gives token t's fp32 dot products.
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-
-__device__ __forceinline__ f16x8 frag(f16x2 a, f16x2 b, f16x2 c, f16x2 d) {
-  typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-  const f16x4 ab = __builtin_shufflevector(a, b, 0, 1, 2, 3), cd = __builtin_shufflevector(c, d, 0, 1, 2, 3);
-  return __builtin_shufflevector(ab, cd, 0, 1, 2, 3, 4, 5, 6, 7);
-}
-
-// block element r (row within a 16-row tile) -> (row half, position inside the 8-wide k group)
-__device__ __forceinline__ int a_rh(int r) { return (r >> 2) & 1; }
-__device__ __forceinline__ int a_j(int r) { return 4 * ((r >> 1) & 1) + 2 * ((r >> 3) & 1) + (r & 1); }
 
 // The kernel body takes its LDS regions as distinct restrict pointers (table, the wave's A
 // fragments), so the compiler knows they never alias.
@@ -630,6 +612,7 @@ namespace {
 struct DeviceState {
   bool ready = false;
   int cus = 0;
+  const uint8_t* codebook = nullptr;
 };
 std::mutex g_mutex;
 DeviceState g_devices[64];
@@ -662,11 +645,20 @@ int ensure_device_ready() {
   DeviceState& st = g_devices[dev];
   if (st.ready) return MOE_OK;
   MOE_HIP(hipDeviceGetAttribute(&st.cus, hipDeviceAttributeMultiprocessorCount, dev));
+  void* table = nullptr;
+  MOE_HIP(hipGetSymbolAddress(&table, HIP_SYMBOL(g_codebook_e4m3)));
+  st.codebook = static_cast<const uint8_t*>(table);
   hipLaunchKernelGGL(build_codebook_kernel, dim3(128), dim3(256), 0, 0);
   MOE_HIP(hipGetLastError());
   MOE_HIP(hipDeviceSynchronize());
   st.ready = true;
   return MOE_OK;
+}
+
+const uint8_t* codebook_device_table() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  return g_devices[dev].codebook;
 }
 
 int device_cus() {

@@ -1,0 +1,412 @@
+// K4 trellis experts over sorted prefill rows on gfx950: grouped GEMMs with the trellis decoded
+// next to the fp16 matrix cores, one weight stream per (expert block, column block).
+//
+// Reference semantics (paths relative to the reference root), exlr8/fast_prefill.py:188-211
+// grouped_expert_mlp (values per slot; the caller combines):
+//   sorted work order: argsort of the flat ids, per-expert blocks        fast_prefill.py:19-46
+//   xh = H128(x * in_scale[e]) for gate and for up                        fast_prefill.py:87-97 (_prep)
+//   inner = xh @ decode(packed[e]), fp32 dot                              fast_prefill.py:151-164 (_inner_sorted)
+//   h = H128(swiglu_T(H128(g) * out_gate, H128(u) * out_up) * in_down)    fast_prefill.py:203-207 (gate_finish)
+//   value = T(H128(h @ decode(down[e])) * out_down)                       fast_prefill.py:118-127 (_finish)
+//
+// MI355X design:
+//   * Activations are split as x = hi + lo * 2^-11 with hi = f16(x) and lo = f16((x - hi) * 2^11)
+//     (about 22 bits, the decode GEMV's split); both rows go through v_mfma_f32_16x16x32_f16
+//     against the decoded fp16 weights (the codebook values are exact in fp16), so an M-tile of
+//     16 A rows carries 8 tokens.  The prep and gate-finish kernels write the A operand directly
+//     in the MFMA's k order (a_rh / a_j of the K4 tile rows), 256 B per row and 64-row quad.
+//   * A work item is (block of <= 64 sorted rows of one expert, 256 output columns).  Each of the
+//     8 waves owns one set of 2 tiles (32 columns): per 64-row quad it loads its 16 B piece of the
+//     packed tiles, decodes it with the decode GEMV's piece decoder (LDS code table + arithmetic
+//     route) and runs 4 MFMAs per M-tile; the quad's A rows of the item are staged in LDS once
+//     for the 8 waves.  No split of K: every output is produced by one wave, no atomics.
+//   * Items are classed by M-tiles (1, 2, 4, 8) so small experts pay no padded MFMAs; each class
+//     is one persistent launch (the code table is loaded into LDS once per block).
+#include <hip/hip_runtime.h>
+
+#include "moe_device.h"
+#include "moe_host.h"
+
+namespace moe {
+namespace {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kKpRows = 64;        // sorted rows per item
+constexpr int kKpWaves = 8;
+constexpr int kKpThreads = kKpWaves * 64;
+constexpr int kKpRowQuad = 256;    // A bytes per (row, 64-row quad): [rh 2][hl 2][g 4][j 8] fp16
+constexpr int kKpCols = 256;       // output columns per item
+
+// A operand element (row p, input k, hl = 0 hi / 1 lo) -> fp16 index in the quad-ordered buffer
+__device__ __forceinline__ int64_t kp_a_index(int64_t p, int nq, int k, int hl) {
+  const int q = k >> 6, g = (k >> 4) & 3, r = k & 15;
+  return ((((p * nq + q) * 2 + a_rh(r)) * 2 + hl) * 4 + g) * 8 + a_j(r);
+}
+__device__ __forceinline__ void kp_store_a(uint16_t* a, int64_t p, int nq, int k, float x) {
+  asm volatile("" : "+v"(x));  // x in fp32 before both conversions
+  const _Float16 hi = (_Float16)x;
+  const _Float16 lo = (_Float16)((x - (float)hi) * 2048.0f);
+  a[kp_a_index(p, nq, k, 0)] = __builtin_bit_cast(uint16_t, hi);
+  a[kp_a_index(p, nq, k, 1)] = __builtin_bit_cast(uint16_t, lo);
+}
+
+// ---------------------------------------------------------------- prep: xh for gate and up
+// One wave per (sorted row p, 128-block kb, projection): H128(x_token * in_scale[e]) -> A buffer.
+// Sorted rows placed by the segment table: ids outside [0, experts) get no position.
+__device__ __forceinline__ int64_t kp_placed(const int32_t* counts, const int32_t* starts, int experts) {
+  return (int64_t)starts[experts - 1] + counts[experts - 1];
+}
+
+__global__ __launch_bounds__(256) void kp_prep_kernel(const uint16_t* __restrict__ x, const uint32_t* __restrict__ ids,
+                                                      const int32_t* __restrict__ order, const int32_t* __restrict__ counts,
+                                                      const int32_t* __restrict__ starts, int experts, int n, int slots, int K,
+                                                      const uint16_t* __restrict__ in_gate,
+                                                      const uint16_t* __restrict__ in_up, uint16_t* __restrict__ a_gate,
+                                                      uint16_t* __restrict__ a_up) {
+  const int64_t wid = (int64_t)blockIdx.x * 4 + wave_id_uniform();
+  const int kbs = K / 128;
+  if (wid >= (int64_t)n * kbs * 2) return;
+  const int proj = (int)(wid & 1);
+  const int kb = (int)((wid >> 1) % kbs);
+  const int64_t p = (wid >> 1) / kbs;
+  if (p >= kp_placed(counts, starts, experts)) return;
+  const int slot = order[p];
+  const int64_t e = ids[slot];
+  const int lane = lane_id();
+  const int k = kb * 128 + 2 * lane;
+  const uint32_t xv = *reinterpret_cast<const uint32_t*>(x + (int64_t)(slot / slots) * K + k);
+  const uint32_t sv = *reinterpret_cast<const uint32_t*>((proj ? in_up : in_gate) + e * K + k);
+  float v0 = bf16_to_f32((uint16_t)(xv & 0xFFFFu)) * f16_to_f32((uint16_t)(sv & 0xFFFFu));
+  float v1 = bf16_to_f32((uint16_t)(xv >> 16)) * f16_to_f32((uint16_t)(sv >> 16));
+  hadamard128_wave(v0, v1);
+  uint16_t* a = proj ? a_up : a_gate;
+  kp_store_a(a, p, K / 64, k, v0);
+  kp_store_a(a, p, K / 64, k + 1, v1);
+}
+
+// ---------------------------------------------------------------- grouped GEMM
+struct KpGemm {
+  const uint8_t* codebook;    // device E4M3 code table (64 KB)
+  const uint8_t* packed[2];   // per projection: [E] experts of K4 tiles
+  const uint16_t* a[2];       // per projection: A operand [n][K/64][256 B]
+  int col_off[2];             // per projection: first column in `inner`
+  int nproj, side, K, N;      // input / output features of one projection
+  const int32_t* blk;         // plan [3][cap]: expert, first sorted row, length
+  int cap;
+  const int32_t* nblk;
+  float* inner;               // [n][inner_stride] fp32
+  int inner_stride;
+};
+
+// MT M-tiles (8 rows each) per item: items of 8 (MT - 1) < len <= 8 MT rows (MT = 1, 2, 4, 8)
+template <int MT>
+__global__ __launch_bounds__(kKpThreads) void kp_gemm_kernel(KpGemm a) {
+  __shared__ __attribute__((aligned(16))) uint8_t tab[65536];
+  __shared__ __attribute__((aligned(16))) uint8_t abuf[2][MT * 8 * kKpRowQuad];
+  load_codebook_lds(tab, a.codebook);
+  __syncthreads();
+  const int w = wave_id_uniform(), lane = lane_id(), nn = lane & 15, g = lane >> 4;
+  const int ncb = a.N / kKpCols, nq = a.K / 64, it = a.K / 16, obs = a.N / 128;
+  const int lane_off = (nn >> 3) * 128 + (nn & 7) * 16;
+  const int src_lane = (lane & 7) == 0 ? lane + 7 : lane - 1;
+  const int s4 = w & 3;
+  const int nblk = *a.nblk;
+  const int items = nblk * a.nproj * ncb;
+  for (int item = blockIdx.x; item < items; item += gridDim.x) {
+    const int cb = item % ncb, proj = (item / ncb) % a.nproj, b = item / (ncb * a.nproj);
+    const int len = a.blk[2 * a.cap + b];
+    if (len <= (MT / 2) * 8 || len > MT * 8) continue;  // another class
+    const int e = a.blk[b], first = a.blk[a.cap + b];
+    const int ob = 2 * cb + (w >> 2);
+    const uint8_t* wbase = a.packed[proj] + lane_off + 256 * s4;
+    auto piece = [&](int q) -> u32x4 {
+      return *reinterpret_cast<const u32x4*>(wbase + chunk_offset(a.side, e, ob, 4 * q + g, it, obs));
+    };
+    // A staging: chunk c of the quad = row c / 16, 16 B part c % 16 ([rh][hl][g] of the row)
+    constexpr int kChunks = MT * 8 * 16, kPer = (kChunks + kKpThreads - 1) / kKpThreads;
+    const uint8_t* abase = reinterpret_cast<const uint8_t*>(a.a[proj]);
+    auto fetch_a = [&](int q, i32x4 (&f)[kPer]) {
+#pragma unroll
+      for (int i = 0; i < kPer; i++) {
+        const int c = min((int)threadIdx.x + i * kKpThreads, kChunks - 1);
+        const int64_t p = first + min(c >> 4, len - 1);
+        f[i] = *reinterpret_cast<const i32x4*>(abase + (p * nq + q) * kKpRowQuad + (c & 15) * 16);
+      }
+    };
+    auto put_a = [&](const i32x4 (&f)[kPer], uint8_t* dst) {
+#pragma unroll
+      for (int i = 0; i < kPer; i++) {
+        const int c = (int)threadIdx.x + i * kKpThreads;
+        if (c < kChunks) {
+          const int row = c >> 4, part = c & 15;  // part = (rh * 2 + hl) * 4 + g
+          const int rh = part >> 3, hl = (part >> 2) & 1, gg = part & 3;
+          const int m = 2 * (row & 7) + hl;
+          *reinterpret_cast<i32x4*>(dst + (((row >> 3) * 2 + rh) * 16 + m) * 64 + gg * 16) = f[i];
+        }
+      }
+    };
+    f32x4 acc[MT][2];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) acc[mt][0] = acc[mt][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    i32x4 fa[kPer];
+    fetch_a(0, fa);
+    put_a(fa, abuf[0]);
+    u32x4 pc0 = piece(0), pc1 = piece(min(1, nq - 1));
+    fetch_a(min(1, nq - 1), fa);
+    __syncthreads();
+    auto quad = [&](const uint8_t* ab, const u32x4& pc) {
+      const uint32_t prior = (uint32_t)__shfl((int)pc.w, src_lane, 64);
+#pragma unroll
+      for (int rh = 0; rh < 2; rh++) {
+        f16x2 qv[2][4];
+        if (rh == 0)
+          decode_pair_words_f16<2, 2>(pc.x, pc.y, prior, tab, qv);
+        else
+          decode_pair_words_f16<2, 2>(pc.z, pc.w, pc.y, tab, qv);
+        const f16x8 b0 = frag(qv[0][0], qv[0][1], qv[1][0], qv[1][1]);
+        const f16x8 b1 = frag(qv[0][2], qv[0][3], qv[1][2], qv[1][3]);
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+          const f16x8 av = *reinterpret_cast<const f16x8*>(ab + ((mt * 2 + rh) * 16 + nn) * 64 + g * 16);
+          acc[mt][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b0, acc[mt][0], 0, 0, 0);
+          acc[mt][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b1, acc[mt][1], 0, 0, 0);
+        }
+      }
+    };
+    for (int q = 0; q < nq; q += 2) {  // nq is even (K % 128 == 0)
+      quad(abuf[0], pc0);
+      pc0 = piece(min(q + 2, nq - 1));
+      put_a(fa, abuf[1]);
+      fetch_a(min(q + 2, nq - 1), fa);
+      __syncthreads();
+      quad(abuf[1], pc1);
+      pc1 = piece(min(q + 3, nq - 1));
+      if (q + 2 < nq) put_a(fa, abuf[0]);
+      fetch_a(min(q + 3, nq - 1), fa);
+      __syncthreads();
+    }
+    // D rows 4g + i of M-tile mt: rows 2t (hi) and 2t+1 (lo) of item row 8 mt + t, t = 2g + i/2
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+      for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int tt = 0; tt < 2; tt++) {
+          const int row = mt * 8 + 2 * g + tt;
+          if (row < len) {
+            const int col = a.col_off[proj] + ob * 128 + 16 * (2 * s4 + (nn >> 3)) + (nn & 7) + 8 * h;
+            a.inner[(int64_t)(first + row) * a.inner_stride + col] =
+                fmaf(acc[mt][h][2 * tt + 1], 1.0f / 2048.0f, acc[mt][h][2 * tt]);
+          }
+        }
+  }
+}
+
+// ---------------------------------------------------------------- gate finish -> down A operand
+// One wave per (sorted row p, 128-column block cb of the intermediate); the decode GEMV's gate
+// finish arithmetic.
+__global__ __launch_bounds__(256) void kp_gate_finish_kernel(const float* __restrict__ inner, const uint32_t* __restrict__ ids,
+                                                             const int32_t* __restrict__ order,
+                                                             const int32_t* __restrict__ counts,
+                                                             const int32_t* __restrict__ starts, int experts, int n, int m,
+                                                             const uint16_t* __restrict__ out_gate,
+                                                             const uint16_t* __restrict__ out_up,
+                                                             const uint16_t* __restrict__ in_down,
+                                                             uint16_t* __restrict__ a_down) {
+  const int64_t wid = (int64_t)blockIdx.x * 4 + wave_id_uniform();
+  const int cbs = m / 128;
+  if (wid >= (int64_t)n * cbs) return;
+  const int64_t p = wid / cbs;
+  if (p >= kp_placed(counts, starts, experts)) return;
+  const int cb = (int)(wid % cbs);
+  const int64_t e = ids[order[p]];
+  const int col = cb * 128 + 2 * lane_id();
+  const f32x2 gv = *reinterpret_cast<const f32x2*>(inner + p * 2 * m + col);
+  const f32x2 uv = *reinterpret_cast<const f32x2*>(inner + p * 2 * m + m + col);
+  const uint32_t og = *reinterpret_cast<const uint32_t*>(out_gate + e * m + col);
+  const uint32_t ou = *reinterpret_cast<const uint32_t*>(out_up + e * m + col);
+  const uint32_t idn = *reinterpret_cast<const uint32_t*>(in_down + e * m + col);
+  auto lo = [](uint32_t v) { return f16_to_f32((uint16_t)(v & 0xFFFFu)); };
+  auto hi = [](uint32_t v) { return f16_to_f32((uint16_t)(v >> 16)); };
+  float g0 = gv.x, g1 = gv.y, u0 = uv.x, u1 = uv.y;
+  hadamard128_wave(g0, g1);
+  hadamard128_wave(u0, u1);
+  float h0 = swiglu_bf16(g0 * lo(og), u0 * lo(ou));
+  float h1 = swiglu_bf16(g1 * hi(og), u1 * hi(ou));
+  h0 *= lo(idn);
+  h1 *= hi(idn);
+  hadamard128_wave(h0, h1);
+  kp_store_a(a_down, p, m / 64, col, h0);
+  kp_store_a(a_down, p, m / 64, col + 1, h1);
+}
+
+// ---------------------------------------------------------------- value finish
+// One wave per (sorted row p, 128-column block): T(H128(inner) * out_down[e]) -> values[slot].
+__global__ __launch_bounds__(256) void kp_value_finish_kernel(const float* __restrict__ inner, const uint32_t* __restrict__ ids,
+                                                              const int32_t* __restrict__ order,
+                                                              const int32_t* __restrict__ counts,
+                                                              const int32_t* __restrict__ starts, int experts, int n, int h,
+                                                              const uint16_t* __restrict__ out_down,
+                                                              uint16_t* __restrict__ values) {
+  const int64_t wid = (int64_t)blockIdx.x * 4 + wave_id_uniform();
+  const int hbs = h / 128;
+  if (wid >= (int64_t)n * hbs) return;
+  const int64_t p = wid / hbs;
+  if (p >= kp_placed(counts, starts, experts)) return;
+  const int hb = (int)(wid % hbs);
+  const int slot = order[p];
+  const int64_t e = ids[slot];
+  const int col = hb * 128 + 2 * lane_id();
+  const f32x2 v = *reinterpret_cast<const f32x2*>(inner + p * h + col);
+  float v0 = v.x, v1 = v.y;
+  hadamard128_wave(v0, v1);
+  const uint32_t od = *reinterpret_cast<const uint32_t*>(out_down + e * h + col);
+  const uint32_t pk = (uint32_t)f32_to_bf16(v0 * f16_to_f32((uint16_t)(od & 0xFFFFu))) |
+                      ((uint32_t)f32_to_bf16(v1 * f16_to_f32((uint16_t)(od >> 16))) << 16);
+  *reinterpret_cast<uint32_t*>(values + (int64_t)slot * h + col) = pk;
+}
+
+// ---------------------------------------------------------------- workspace
+struct KpWorkspace {
+  int32_t* order;   // [n]
+  int32_t* counts;  // [E]
+  int32_t* starts;  // [E]
+  int32_t* blk;     // [3][cap]
+  int32_t* nblk;
+  uint16_t* a_gate; // [n][h/64][256 B]
+  uint16_t* a_up;
+  uint16_t* a_down; // [n][m/64][256 B]
+  float* inner_gu;  // [n][2m]
+  float* inner_d;   // [n][h]
+  int cap;
+  size_t bytes;
+};
+
+KpWorkspace kp_carve(void* base, int64_t n, int h, int m, int64_t experts) {
+  KpWorkspace w{};
+  w.cap = (int)(n / kKpRows + experts + 1);
+  size_t off = 0;
+  char* p = static_cast<char*>(base);
+  auto take = [&](size_t bytes) { char* r = p ? p + off : nullptr; off += (bytes + 255) & ~(size_t)255; return r; };
+  w.order = reinterpret_cast<int32_t*>(take((size_t)n * 4));
+  w.counts = reinterpret_cast<int32_t*>(take((size_t)experts * 4));
+  w.starts = reinterpret_cast<int32_t*>(take((size_t)experts * 4));
+  w.blk = reinterpret_cast<int32_t*>(take((size_t)3 * w.cap * 4));
+  w.nblk = reinterpret_cast<int32_t*>(take(4));
+  w.a_gate = reinterpret_cast<uint16_t*>(take((size_t)n * h * 4));
+  w.a_up = reinterpret_cast<uint16_t*>(take((size_t)n * h * 4));
+  w.a_down = reinterpret_cast<uint16_t*>(take((size_t)n * m * 4));
+  w.inner_gu = reinterpret_cast<float*>(take((size_t)n * 2 * m * 4));
+  w.inner_d = reinterpret_cast<float*>(take((size_t)n * h * 4));
+  w.bytes = off;
+  return w;
+}
+
+int launch_kp_gemm(const KpGemm& g, hipStream_t s) {
+  // persistent blocks, items strided over them.  The classes of up to 4 M-tiles fit two blocks per
+  // CU (68-80 KB of LDS) and get 4 blocks per CU queued, so the CUs stay busy to the end of the
+  // launch; the 8-tile class (96 KB) runs one block per CU.
+  const int blocks = device_cus() > 0 ? device_cus() : 256;
+  hipLaunchKernelGGL(kp_gemm_kernel<1>, dim3(4 * blocks), dim3(kKpThreads), 0, s, g);
+  MOE_HIP(hipGetLastError());
+  hipLaunchKernelGGL(kp_gemm_kernel<2>, dim3(4 * blocks), dim3(kKpThreads), 0, s, g);
+  MOE_HIP(hipGetLastError());
+  hipLaunchKernelGGL(kp_gemm_kernel<4>, dim3(4 * blocks), dim3(kKpThreads), 0, s, g);
+  MOE_HIP(hipGetLastError());
+  hipLaunchKernelGGL(kp_gemm_kernel<8>, dim3(blocks), dim3(kKpThreads), 0, s, g);
+  MOE_HIP(hipGetLastError());
+  return MOE_OK;
+}
+
+}  // namespace
+}  // namespace moe
+
+using namespace moe;
+
+extern "C" {
+
+size_t moe_k4_grouped_mlp_workspace_bytes(int rows, int slots, int hidden, int intermediate, int64_t experts) {
+  if (rows <= 0 || slots <= 0 || hidden <= 0 || intermediate <= 0 || experts <= 0) return 0;
+  return kp_carve(nullptr, (int64_t)rows * slots, hidden, intermediate, experts).bytes;
+}
+
+int moe_k4_grouped_mlp(const uint16_t* x, const uint32_t* ids, int rows, int slots, const void* packed_gate,
+                       const void* packed_up, const void* packed_down, int64_t packed_bytes, const uint16_t* in_gate,
+                       const uint16_t* out_gate, const uint16_t* in_up, const uint16_t* out_up,
+                       const uint16_t* in_down, const uint16_t* out_down, int hidden, int intermediate,
+                       uint16_t* values, void* workspace, size_t workspace_bytes, moe_stream_t stream) {
+  MOE_ARG(x && ids && packed_gate && packed_up && packed_down && in_gate && out_gate && in_up && out_up && in_down &&
+              out_down && values && workspace,
+          "null pointer argument");
+  MOE_ARG(rows >= 1 && slots >= 1, "rows and slots must be positive");
+  MOE_ARG(hidden > 0 && intermediate > 0 && hidden % kKpCols == 0 && intermediate % kKpCols == 0,
+          "hidden and intermediate must be positive multiples of %d (got %d, %d)", kKpCols, hidden, intermediate);
+  const int64_t per = (int64_t)hidden * intermediate / 2;
+  MOE_ARG(packed_bytes > 0 && packed_bytes % per == 0, "packed size %lld is not a whole number of K4 experts",
+          (long long)packed_bytes);
+  const int64_t experts = packed_bytes / per;
+  MOE_ARG(experts <= 1024, "at most 1024 experts (got %lld)", (long long)experts);
+  const int64_t n = (int64_t)rows * slots;
+  MOE_ARG(n <= (int64_t)1 << 24, "too many slots (%lld)", (long long)n);
+  const KpWorkspace w = kp_carve(workspace, n, hidden, intermediate, experts);
+  if (workspace_bytes < w.bytes)
+    return fail(MOE_EWORKSPACE, "workspace too small: %zu < %zu bytes", workspace_bytes, w.bytes);
+  int rc = ensure_device_ready();
+  if (rc) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  // sorted work order in blocks of <= 64 rows (ids outside [0, experts) get no position)
+  if ((rc = moe_segment_table(ids, (int)n, (int)experts, kKpRows, w.order, w.counts, w.starts, w.blk, w.cap, w.nblk,
+                              stream)))
+    return rc;
+  const int64_t pw = n * (hidden / 128) * 2;
+  hipLaunchKernelGGL(kp_prep_kernel, dim3((unsigned)((pw + 3) / 4)), dim3(256), 0, s, x, ids, w.order, w.counts, w.starts,
+                     (int)experts, (int)n, slots, hidden, in_gate, in_up, w.a_gate, w.a_up);
+  MOE_HIP(hipGetLastError());
+  const uint8_t* table = codebook_device_table();
+  if (!table) return fail(MOE_ENOTSUP, "code table not initialised on this device");
+  KpGemm g{};
+  g.codebook = table;
+  g.packed[0] = static_cast<const uint8_t*>(packed_gate);
+  g.packed[1] = static_cast<const uint8_t*>(packed_up);
+  g.a[0] = w.a_gate;
+  g.a[1] = w.a_up;
+  g.col_off[0] = 0;
+  g.col_off[1] = intermediate;
+  g.nproj = 2;
+  g.side = 1;
+  g.K = hidden;
+  g.N = intermediate;
+  g.blk = w.blk;
+  g.cap = w.cap;
+  g.nblk = w.nblk;
+  g.inner = w.inner_gu;
+  g.inner_stride = 2 * intermediate;
+  if ((rc = launch_kp_gemm(g, s))) return rc;
+  const int64_t fw = n * (intermediate / 128);
+  hipLaunchKernelGGL(kp_gate_finish_kernel, dim3((unsigned)((fw + 3) / 4)), dim3(256), 0, s, w.inner_gu, ids, w.order,
+                     w.counts, w.starts, (int)experts, (int)n, intermediate, out_gate, out_up, in_down, w.a_down);
+  MOE_HIP(hipGetLastError());
+  KpGemm d{};
+  d.codebook = table;
+  d.packed[0] = static_cast<const uint8_t*>(packed_down);
+  d.a[0] = w.a_down;
+  d.col_off[0] = 0;
+  d.nproj = 1;
+  d.side = 2;
+  d.K = intermediate;
+  d.N = hidden;
+  d.blk = w.blk;
+  d.cap = w.cap;
+  d.nblk = w.nblk;
+  d.inner = w.inner_d;
+  d.inner_stride = hidden;
+  if ((rc = launch_kp_gemm(d, s))) return rc;
+  const int64_t vw = n * (hidden / 128);
+  hipLaunchKernelGGL(kp_value_finish_kernel, dim3((unsigned)((vw + 3) / 4)), dim3(256), 0, s, w.inner_d, ids, w.order,
+                     w.counts, w.starts, (int)experts, (int)n, hidden, out_down, values);
+  MOE_HIP(hipGetLastError());
+  return MOE_OK;
+}
+
+}  // extern "C"

@@ -65,12 +65,14 @@ __device__ __forceinline__ float fp8_to_f32(uint32_t byte) { return __builtin_am
 // moe_build_codebook_kernel; copied into LDS by the decode GEMVs.
 extern __device__ uint8_t g_codebook_e4m3[65536];
 
-// Cooperative copy of the 64 KB table into LDS (blockDim threads, 16 B each).
-__device__ __forceinline__ void load_codebook_lds(uint8_t* lds) {
-  const u32x4* src = reinterpret_cast<const u32x4*>(g_codebook_e4m3);
+// Cooperative copy of the 64 KB table into LDS (blockDim threads, 16 B each), from the table of
+// this translation unit or, in other ones, from its device address (codebook_device_table()).
+__device__ __forceinline__ void load_codebook_lds(uint8_t* lds, const uint8_t* table) {
+  const u32x4* src = reinterpret_cast<const u32x4*>(table);
   u32x4* dst = reinterpret_cast<u32x4*>(lds);
   for (int i = threadIdx.x; i < 65536 / 16; i += blockDim.x) dst[i] = src[i];
 }
+__device__ __forceinline__ void load_codebook_lds(uint8_t* lds) { load_codebook_lds(lds, g_codebook_e4m3); }
 
 // ---------------------------------------------------------------- K4 word layout
 // Word w of a tile with its circular predecessor p holds 8 codewords (A.1 direct form):
@@ -346,6 +348,30 @@ __device__ __forceinline__ void decode_pair_words_f16(uint32_t w0, uint32_t w1, 
     if (pend_i >= 0) q[pend_i][kOut[pend_k]] = widen_one(lb[pend_i][pend_k]);
   }
 }
+
+// ---------------------------------------------------------------- K4 storage and MFMA fragments
+// 1 KB chunk (8 tiles of 128 B) of expert e, output block ob (128 columns), input tile tk of a
+// packed projection with `it` input tiles and `obs` output blocks (side 1: gate/up order, side 2:
+// down order)
+__device__ __forceinline__ uint64_t chunk_offset(int side, uint64_t e, uint32_t ob, uint32_t tk, uint32_t it,
+                                                 uint32_t obs) {
+  if (side == 2) return ((((e * (it / 8u) + tk / 8u) * obs + ob) * 8u + tk % 8u) << 10);
+  return (((e * obs + ob) * it + tk) << 10);
+}
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+// four fp16 pairs -> one 8-wide MFMA operand
+__device__ __forceinline__ f16x8 frag(f16x2 a, f16x2 b, f16x2 c, f16x2 d) {
+  typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+  const f16x4 ab = __builtin_shufflevector(a, b, 0, 1, 2, 3), cd = __builtin_shufflevector(c, d, 0, 1, 2, 3);
+  return __builtin_shufflevector(ab, cd, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// A operand of the K4 fp16 MFMAs: row r of a 16-row input tile -> (row half rh, position j inside
+// the 8-wide k group), matching the B fragments decode_pair_words_f16 builds from a tile's words
+__device__ __forceinline__ int a_rh(int r) { return (r >> 2) & 1; }
+__device__ __forceinline__ int a_j(int r) { return 4 * ((r >> 1) & 1) + 2 * ((r >> 3) & 1) + (r & 1); }
 
 // ---------------------------------------------------------------- wave-level H128
 // 128 values held as 2 per lane (element i = 2*lane + j).  Normalised Sylvester order;

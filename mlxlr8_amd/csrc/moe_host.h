@@ -17,6 +17,10 @@ int ensure_device_ready();
 // Number of compute units of the current device (cached per device).
 int device_cus();
 
+// Device address of the current device's 64 KB E4M3 code table (after ensure_device_ready), for
+// kernels of other translation units.
+const uint8_t* codebook_device_table();
+
 // Router GEMV + route + dispatch plan for decode batches (router.hip).
 int moe_router_fused_plan(const uint16_t* x, const float* w, const float* bias, int rows, int hidden, int experts,
                           float* logits, uint32_t* ids, float* scores, Plan* plan, int32_t* counter, hipStream_t s,

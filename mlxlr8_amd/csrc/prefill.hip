@@ -42,7 +42,6 @@ namespace {
 
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 __device__ __forceinline__ f16x8 pack_f16x8(f16x2 a, f16x2 b, f16x2 c, f16x2 d) {
   typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));

@@ -10,6 +10,7 @@ import torch
 
 from ._lib import check, lib, ptr, require_cuda, stream, workspace
 from .fast_decode import _weights, fast_expert_mlp
+from .fast_prefill import grouped_expert_mlp
 from .trellis import BF16, _check_format
 
 
@@ -42,10 +43,12 @@ class ExpertLayer:
         return _check_format(self.packed["gate"], self.k, self.hidden, self.intermediate, 1)
 
     def __call__(self, x, ids):
-        """values[*ids.shape, hidden] for the selected experts (exlr8/experts.py:150-188)."""
+        """values[*ids.shape, hidden] for the selected experts (exlr8/experts.py:150-188): up to 16
+        rows through the decode MLP, more through the grouped (sorted-by-expert) prefill MLP."""
         if self.affine is not None:
             return self.affine.slots(x, ids)
-        return fast_expert_mlp(x, ids, self.packed, self.scales, self.k, self.hidden, self.intermediate)
+        mlp = fast_expert_mlp if ids.numel() // ids.shape[-1] <= 16 else grouped_expert_mlp
+        return mlp(x, ids, self.packed, self.scales, self.k, self.hidden, self.intermediate)
 
     def decode_block(self, x, residual, router_weight, bias):
         """Router GEMV + route + expert MLP + combine in one C call (decode batches, <= 8 rows).
