@@ -55,6 +55,8 @@ def parse():
     p.add_argument("--config", type=int, default=0, choices=range(5),
                    help="workload: 0 K4 b=1 (default), 1 MXFP4 b=1, 2 K4 8-token verify, 3 MXFP4 512-token "
                         "prefill, 4 20-layer K4 stack")
+    p.add_argument("--k4-prefill", action="store_true",
+                   help="instead: the K4 grouped prefill MLP (values of 512 Zipf-routed rows x 9 slots)")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="also run a plain 1 GiB device copy (reference point for rocprofv3 FETCH/WRITE_SIZE)")
     return p.parse_args()
@@ -108,6 +110,9 @@ def main():
         print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported (this path has no "
               "multi-GPU collectives; see DESIGN.md for how it would shard)", file=sys.stderr)
         sys.exit(2)
+    if args.k4_prefill:
+        print(json.dumps(bench_k4_prefill(args)), flush=True)
+        return
     if args.config != 0:
         print(json.dumps(OTHER[args.config](args)), flush=True)
         return
@@ -327,6 +332,33 @@ def bench_prefill(args):
     out["steps"] = steps
     flops = 512 * 9 * 3 * 2 * H * M
     out["mfma_util_fp4_peak"] = round(flops / (ms * 1e-3) / 10.1e15, 4)
+    return out
+
+
+def bench_k4_prefill(args):
+    """K4 grouped prefill MLP (exlr8/fast_prefill.py:188-211): values of 512 rows x 9 slots, ids from
+    the Zipf-skewed router of the 512-token prefill workload, two K4 layers rotated."""
+    import torch
+    from mlxlr8_amd import synth
+    from mlxlr8_amd.fast_prefill import grouped_expert_mlp
+    from mlxlr8_amd.fast_router import route, router_logits
+    dev = torch.device("cuda:0")
+    layers = [synth.k4_layer(dev, args.seed + 41 * i) for i in range(2)]
+    w, bias = synth.router(dev, args.seed + 1, zipf=True)
+    x, _ = synth.activations(dev, args.seed + 3000, 512)
+    ids, _ = route(router_logits(x, w), bias)
+    torch.cuda.synchronize()
+    touched = len(set(ids.cpu().numpy().ravel().tolist()))
+    run = lambda i: grouped_expert_mlp(x, ids, layers[i % 2]["packed"], layers[i % 2]["scales"], 4, H, M)
+    steps = max(1, min(args.steps, 20))
+    ms = _time_steps(run, steps, min(args.warmup, 3))
+    algo = touched * 3 * TRELLIS + touched * 6 * H * 2 + 512 * H * 2 + 512 * 9 * H * 2
+    out = _line(args, 512e3 / ms, "tokens/s", ms, "f32",
+                "K4-trellis grouped prefill MLP, 512 Zipf(1.1)-routed rows x 9 slots (values; sort-by-expert "
+                "blocks, trellis decoded next to the fp16 matrix cores)",
+                {"global_batch": 512, "seq_len": 512, "touched_experts": touched}, algo,
+                "whole step: segment table + prep + grouped gate/up and down GEMMs + finishes")
+    out["steps"] = steps
     return out
 
 
