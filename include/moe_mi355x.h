@@ -208,7 +208,7 @@ size_t moe_mxfp4_prefill_workspace_bytes(int rows, int hidden, int intermediate,
  * for ids [rows, slots] (flat ids < experts; x [rows, hidden] bf16 shared by a row's slots).
  * Slots are sorted by expert into blocks of <= 64 rows; every expert's weights are streamed once
  * per block and 256-column group.  values [rows*slots, hidden] bf16 in slot order; side vectors
- * and packed layouts as moe_k4_mlp; hidden and intermediate multiples of 256.
+ * and packed layouts as moe_k4_mlp; hidden and intermediate multiples of 128.
  * Workspace: moe_k4_grouped_mlp_workspace_bytes(rows, slots, hidden, intermediate, experts).
  * Replaces: exlr8/fast_prefill.py:188-211 grouped_expert_mlp (sorted block-table trellis GEMMs). */
 int moe_k4_grouped_mlp(const uint16_t* x, const uint32_t* ids, int rows, int slots, const void* packed_gate,

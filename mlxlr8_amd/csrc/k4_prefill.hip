@@ -15,7 +15,8 @@
 //     against the decoded fp16 weights (the codebook values are exact in fp16), so an M-tile of
 //     16 A rows carries 8 tokens.  The prep and gate-finish kernels write the A operand directly
 //     in the MFMA's k order (a_rh / a_j of the K4 tile rows), 256 B per row and 64-row quad.
-//   * A work item is (block of <= 64 sorted rows of one expert, 256 output columns).  Each of the
+//   * A work item is (block of <= 64 sorted rows of one expert, 256 output columns; 128 for the
+//     last one when N % 256 == 128).  Each of the
 //     8 waves owns one set of 2 tiles (32 columns): per 64-row quad it loads its 16 B piece of the
 //     packed tiles, decodes it with the decode GEMV's piece decoder (LDS code table + arithmetic
 //     route) and runs 4 MFMAs per M-tile; the quad's A rows of the item are staged in LDS once
@@ -107,7 +108,7 @@ __global__ __launch_bounds__(kKpThreads) void kp_gemm_kernel(KpGemm a) {
   load_codebook_lds(tab, a.codebook);
   __syncthreads();
   const int w = wave_id_uniform(), lane = lane_id(), nn = lane & 15, g = lane >> 4;
-  const int ncb = a.N / kKpCols, nq = a.K / 64, it = a.K / 16, obs = a.N / 128;
+  const int ncb = (a.N + kKpCols - 1) / kKpCols, nq = a.K / 64, it = a.K / 16, obs = a.N / 128;
   const int lane_off = (nn >> 3) * 128 + (nn & 7) * 16;
   const int src_lane = (lane & 7) == 0 ? lane + 7 : lane - 1;
   const int s4 = w & 3;
@@ -118,7 +119,9 @@ __global__ __launch_bounds__(kKpThreads) void kp_gemm_kernel(KpGemm a) {
     const int len = a.blk[2 * a.cap + b];
     if (len <= (MT / 2) * 8 || len > MT * 8) continue;  // another class
     const int e = a.blk[b], first = a.blk[a.cap + b];
-    const int ob = 2 * cb + (w >> 2);
+    // the last item of N % 256 == 128 has one column block: waves 4-7 then only stage A
+    const bool active = 2 * cb + (w >> 2) < obs;
+    const int ob = min(2 * cb + (w >> 2), obs - 1);
     const uint8_t* wbase = a.packed[proj] + lane_off + 256 * s4;
     auto piece = [&](int q) -> u32x4 {
       return *reinterpret_cast<const u32x4*>(wbase + chunk_offset(a.side, e, ob, 4 * q + g, it, obs));
@@ -156,6 +159,7 @@ __global__ __launch_bounds__(kKpThreads) void kp_gemm_kernel(KpGemm a) {
     fetch_a(min(1, nq - 1), fa);
     __syncthreads();
     auto quad = [&](const uint8_t* ab, const u32x4& pc) {
+      if (!active) return;
       const uint32_t prior = (uint32_t)__shfl((int)pc.w, src_lane, 64);
 #pragma unroll
       for (int rh = 0; rh < 2; rh++) {
@@ -194,7 +198,7 @@ __global__ __launch_bounds__(kKpThreads) void kp_gemm_kernel(KpGemm a) {
 #pragma unroll
         for (int tt = 0; tt < 2; tt++) {
           const int row = mt * 8 + 2 * g + tt;
-          if (row < len) {
+          if (active && row < len) {
             const int col = a.col_off[proj] + ob * 128 + 16 * (2 * s4 + (nn >> 3)) + (nn & 7) + 8 * h;
             a.inner[(int64_t)(first + row) * a.inner_stride + col] =
                 fmaf(acc[mt][h][2 * tt + 1], 1.0f / 2048.0f, acc[mt][h][2 * tt]);
@@ -340,8 +344,8 @@ int moe_k4_grouped_mlp(const uint16_t* x, const uint32_t* ids, int rows, int slo
               out_down && values && workspace,
           "null pointer argument");
   MOE_ARG(rows >= 1 && slots >= 1, "rows and slots must be positive");
-  MOE_ARG(hidden > 0 && intermediate > 0 && hidden % kKpCols == 0 && intermediate % kKpCols == 0,
-          "hidden and intermediate must be positive multiples of %d (got %d, %d)", kKpCols, hidden, intermediate);
+  MOE_ARG(hidden > 0 && intermediate > 0 && hidden % 128 == 0 && intermediate % 128 == 0,
+          "hidden and intermediate must be positive multiples of 128 (got %d, %d)", hidden, intermediate);
   const int64_t per = (int64_t)hidden * intermediate / 2;
   MOE_ARG(packed_bytes > 0 && packed_bytes % per == 0, "packed size %lld is not a whole number of K4 experts",
           (long long)packed_bytes);

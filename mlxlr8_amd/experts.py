@@ -150,3 +150,111 @@ class ExpertLayer:
                                       h, self.intermediate, ptr(out), ptr(ids), ptr(scores), ptr(ws), ws.numel(),
                                       stream(x.device)))
         return out.reshape(residual.shape), ids, scores
+
+
+# ---------------------------------------------------------------- checkpoint loading
+def layer_arrays(path, number):
+    """Host arrays of one up1 layer (exlr8/experts.py:80-131): ``(k, hidden, intermediate, packed,
+    scales)`` with ``packed[p]`` = routed experts then the shared expert (uint8) and ``scales[p]`` =
+    (in, out) fp16 [257, features]: gate/up in = su_block per 128-block x signs.in, out = svh;
+    down in = suh, out = sv_block per 128-block x signs.out."""
+    import json
+    from pathlib import Path
+
+    import numpy as np
+
+    from .weights import SafeTensorFile
+    path = Path(path)
+    manifest = json.loads((path / "manifests/exlr8-manifest-up1.json").read_text())
+    if manifest["name"] != "up1":
+        raise ValueError("This loader requires the up1 manifest")
+    plan = manifest["layers"][str(number)]
+    widths = {v for rows in (plan["gate"], plan["up"]) for row in rows for v in row}
+    widths.update(plan["down"])
+    widths.update(plan["shared"]["gate"])
+    widths.update(plan["shared"]["up"])
+    widths.add(plan["shared"]["down"])
+    k = 3 if number == 78 else 4
+    if widths != {k}:
+        raise ValueError(f"Layer {number} is not uniform K{k}")
+    if k != 4:
+        raise ValueError(f"Layer {number} is K3; this build decodes K4 trellis only")
+    directory = path / "experts"
+    weights = SafeTensorFile(directory / f"exlr8-layer-{number:03d}.k{k}.safetensors")
+    index = SafeTensorFile(directory / f"exlr8-layer-{number:03d}.index.safetensors")
+    hidden = index.header["signs.in"]["shape"][0]
+    intermediate = index.header[f"k{k}.gate.svh"]["shape"][-1]
+    signs_in = index.raw("signs.in").astype(np.float16)
+    signs_out = index.raw("signs.out").astype(np.float16)
+    scales, packed = {}, {}
+    for projection in ("gate", "up", "down"):
+        down = projection == "down"
+        block_name, channel_name = ("sv_block", "suh") if down else ("su_block", "svh")
+        block = np.concatenate([index.raw(f"k{k}.{projection}.{block_name}"),
+                                index.raw(f"shared.k{k}.{projection}.{block_name}")])
+        channel = np.concatenate([index.raw(f"k{k}.{projection}.{channel_name}"),
+                                  index.raw(f"shared.k{k}.{projection}.{channel_name}")])
+        hidden_scale = np.repeat(block, 128, axis=-1) * (signs_out if down else signs_in)
+        scales[projection] = (channel, hidden_scale) if down else (hidden_scale, channel)
+        packed[projection] = np.concatenate([weights.raw("trellis." + projection),
+                                             weights.raw("shared.trellis." + projection)])
+    return k, hidden, intermediate, packed, scales
+
+
+class ExpertStore:
+    """Resident up1 expert store (exlr8/experts.py:12-76).  On an MI355X every layer's experts fit in
+    HBM, so layers are always loaded resident; ``cache_gib`` is accepted for signature parity and
+    ``resident=False`` loads resident as well (the reference's SSD cache is not built)."""
+
+    def __init__(self, path, cache_gib=32, resident=False, optimize=True, device=None):
+        import json
+        from pathlib import Path
+        self.path = Path(path)
+        self.resident, self.optimize = True, optimize
+        self.manifest = json.loads((self.path / "manifests/exlr8-manifest-up1.json").read_text())
+        if self.manifest["name"] != "up1":
+            raise ValueError("This loader requires the up1 manifest")
+        if cache_gib < 0:
+            raise ValueError("cache_gib must be nonnegative")
+        self.limit = int(cache_gib * 1024 ** 3)
+        self.device = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+        self.cache, self.cache_bytes, self.hits, self.misses = {}, 0, 0, 0
+        self.resident_bytes = 0
+        self._layers = {}
+
+    def layer(self, number):
+        if number not in self._layers:
+            self._layers[number] = ExpertLayer.from_store(self, number)
+        return self._layers[number]
+
+    def stats(self):
+        return {"cache_bytes": self.cache_bytes, "cache_limit_bytes": self.limit,
+                "resident_bytes": self.resident_bytes, "hits": self.hits, "misses": self.misses}
+
+
+def _from_store(cls, store, number):
+    """ExpertLayer of layer `number` of an ExpertStore, resident on the store's device; with
+    ``optimize`` and the GLM-5.3 shape (6144, 2048) its experts are converted to joined MXFP4 and
+    served by them (exlr8/experts.py:132-148)."""
+    k, hidden, intermediate, packed, scales = layer_arrays(store.path, number)
+    dev = store.device
+    layer = cls({p: torch.from_numpy(a).to(dev) for p, a in packed.items()},
+                {p: tuple(torch.from_numpy(v).to(dev) for v in pair) for p, pair in scales.items()},
+                hidden, intermediate, k=k, number=number)
+    layer.store = store
+    store.resident_bytes += sum(a.nbytes for a in packed.values())
+    store.resident_bytes += sum(v.nbytes for pair in scales.values() for v in pair)
+    if store.optimize and (hidden, intermediate) == (6144, 2048):
+        from .joined_mxfp4 import JoinedMXFP4
+        layer.affine = JoinedMXFP4(layer)
+        store.resident_bytes += (sum(a.numel() * a.element_size() for v in layer.affine.weights.values() for a in v)
+                                 - sum(a.nbytes for a in packed.values()) + layer.affine.unit.numel() * 2)
+        for projection in ("gate", "up"):
+            incoming, outgoing = layer.scales[projection]
+            store.resident_bytes -= incoming.numel() * incoming.element_size()
+            layer.scales[projection] = (None, outgoing)
+        del layer.packed
+    return layer
+
+
+ExpertLayer.from_store = classmethod(_from_store)
