@@ -266,10 +266,31 @@ __global__ __launch_bounds__(256) void router_decode_kernel(const uint16_t* __re
   __syncthreads();
   if (!last) return;
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-  for (int row = wv; row < rows; row += 4) route_row<true>(logits, bias, row, ids, scores, sid);
-  __syncthreads();
   (void)experts;  // routed ids are 0..255 plus the shared expert 256
-  build_plan_parallel(sid, rows, kSlots, max_users, plan, open);
+  if (rows == 1) {
+    // one row: slot s is unit s (the 8 routed ids are distinct and the shared id is 256), so the
+    // routing lanes write the plan build_plan_parallel would build, without its passes
+    if (wv == 0) {
+      route_row<true>(logits, bias, 0, ids, scores, sid);
+      const int lane = lane_id();
+      if (lane < kSlots) {
+        plan->expert[lane] = sid[lane];  // written by this lane in route_row
+        plan->ntok[lane] = 1;
+        plan->tok[lane][0] = 0;
+        plan->slot[lane][0] = lane;
+        plan->slot_unit[lane] = lane;
+        plan->slot_pos[lane] = 0;
+        if (lane == 0) {
+          plan->units = kSlots;
+          plan->rows = 1;
+        }
+      }
+    }
+  } else {
+    for (int row = wv; row < rows; row += 4) route_row<true>(logits, bias, row, ids, scores, sid);
+    __syncthreads();
+    build_plan_parallel(sid, rows, kSlots, max_users, plan, open);
+  }
   if (threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
