@@ -69,3 +69,28 @@ def test_product_never_imports_oracle():
     for path in (ROOT / "mlxlr8_amd").rglob("*.py"):
         text = path.read_text()
         assert "import oracle" not in text and "from oracle" not in text, path
+
+
+def test_encode_and_grouped_argument_errors_without_device():
+    from mlxlr8_amd._lib import lib
+    L = lib()
+    p = ctypes.c_void_p(256)
+    # moe_k4_to_mxfp4: in_scale and unit come together; rows must fit; codes aligned; whole experts
+    assert L.moe_k4_to_mxfp4(p, 128 * 128 // 2, 128, 128, 1, p, None, p, p, 256, 0, p, 1 << 20, None) == -1
+    assert b"together" in L.moe_last_error()
+    assert L.moe_k4_to_mxfp4(p, 128 * 128 // 2, 128, 128, 1, None, None, p, p, 128, 64, p, 1 << 20, None) == -1
+    assert b"destination" in L.moe_last_error()
+    assert L.moe_k4_to_mxfp4(p, 100, 128, 128, 2, None, None, p, p, 128, 0, p, 1 << 20, None) == -1
+    assert b"whole number" in L.moe_last_error()
+    assert L.moe_k4_to_mxfp4(p, 128 * 128 // 2, 128, 128, 2, None, None, p, p, 128, 0, p, 16, None) == -3
+    assert b"workspace" in L.moe_last_error()
+    assert L.moe_k4_to_mxfp4_workspace_bytes(6144, 2048) == 6144 * 2048 * 2
+    # moe_k4_grouped_mlp: widths, whole experts, workspace
+    args = [p, p, 4, 9, p, p, p, 128 * 128 // 2] + [p] * 6
+    assert L.moe_k4_grouped_mlp(*args[:7], 128 * 128 // 2, *args[8:], 100, 128, p, p, 1 << 30, None) == -1
+    assert b"multiples of 128" in L.moe_last_error()
+    assert L.moe_k4_grouped_mlp(*args[:7], 1000, *args[8:], 128, 128, p, p, 1 << 30, None) == -1
+    assert b"whole number" in L.moe_last_error()
+    assert L.moe_k4_grouped_mlp(*args, 128, 128, p, p, 16, None) == -3
+    assert b"workspace" in L.moe_last_error()
+    assert L.moe_k4_grouped_mlp_workspace_bytes(512, 9, 6144, 2048, 257) > 0
