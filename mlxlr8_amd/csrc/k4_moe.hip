@@ -126,6 +126,33 @@ __global__ __launch_bounds__(1024) void trellis_decode_kernel(const uint32_t* __
   }
 }
 
+// K2 / K3 tiles (8k words, exlr8/trellis.py:78-102): one thread per codeword.  Codeword i is the 16
+// bits that end after its k-bit symbol in the tile's circular MSB-first bitstream; its weight is
+// the E4M3 table entry widened to fp16 (exact), placed by the tensor-core position map.
+__global__ __launch_bounds__(256) void trellis_decode_generic_kernel(const uint32_t* __restrict__ packed, int k,
+                                                                      int in_f, int out_f, int side, int64_t expert,
+                                                                      uint16_t* __restrict__ inner) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)in_f * out_f) return;
+  const uint32_t it = (uint32_t)in_f / 16u, ot = (uint32_t)out_f / 16u;
+  const int64_t t = idx >> 8;
+  const uint32_t i = (uint32_t)(idx & 255);
+  const uint32_t tk = (uint32_t)(t / ot), tn = (uint32_t)(t % ot);
+  const uint64_t e = (uint64_t)expert;
+  const uint64_t tile = side == 2 ? ((((e * (it / 8u) + tk / 8u) * (ot / 8u) + tn / 8u) * 8u + tk % 8u) * 8u + tn % 8u)
+                                  : (((e * (ot / 8u) + tn / 8u) * it + tk) * 8u + tn % 8u);
+  const uint32_t nw = 8u * (uint32_t)k;
+  const uint32_t* tw = packed + tile * nw;
+  const uint32_t end = (i + 1u) * (uint32_t)k + 256u * (uint32_t)k;
+  const uint32_t last = (end - 1u) / 32u;
+  const uint64_t merged = ((uint64_t)tw[(last - 1u) % nw] << 32) | (uint64_t)tw[last % nw];
+  const uint32_t cw = (uint32_t)(merged >> ((last + 1u) * 32u - end)) & 0xFFFFu;
+  const uint32_t lane = i / 8u, slot = i % 8u;
+  const uint32_t r = (lane % 4u) * 2u + (slot & 1u) + (slot & 2u) * 4u, c = lane / 4u + (slot & 4u) * 2u;
+  const _Float16 v = (_Float16)fp8_to_f32(g_codebook_e4m3[cw]);
+  inner[(uint64_t)(16u * tk + r) * (uint64_t)out_f + 16u * tn + c] = __builtin_bit_cast(uint16_t, v);
+}
+
 // ============================================================== GEMV machinery
 
 enum InMode { IN_PREP = 0, IN_DIRECT = 1 };
@@ -787,16 +814,24 @@ size_t moe_workspace_bytes(int hidden, int intermediate) {
 
 int moe_trellis_decode_f16(const void* packed, int64_t packed_bytes, int k, int in_f, int out_f, int side,
                            int64_t expert, uint16_t* inner, moe_stream_t stream) {
-  MOE_ARG(k == 4, "this build decodes K4 trellis only (got k=%d)", k);
+  MOE_ARG(k >= 2 && k <= 4, "EXLR8 trellis width must be 2, 3, or 4 (got k=%d)", k);
   MOE_ARG(side >= 0 && side <= 2, "sharded_side must be 0, 1, or 2");
   MOE_ARG(packed && inner, "packed and inner must not be NULL");
   int64_t experts = 0;
-  int rc = check_trellis(packed_bytes, in_f, out_f, &experts);
+  int rc = check_trellis(packed_bytes * 4 / k, in_f, out_f, &experts);  // same tile count as K4 bytes
   if (rc) return rc;
+  MOE_ARG(packed_bytes % ((int64_t)in_f * out_f * k / 8) == 0, "packed byte count does not match the trellis dimensions");
   MOE_ARG(expert >= 0 && expert < experts, "expert %lld out of range (%lld experts)", (long long)expert,
           (long long)experts);
   rc = ensure_device_ready();
   if (rc) return rc;
+  if (k != 4) {
+    const int64_t n = (int64_t)in_f * out_f;
+    hipLaunchKernelGGL(trellis_decode_generic_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                       (hipStream_t)stream, (const uint32_t*)packed, k, in_f, out_f, side, expert, inner);
+    MOE_HIP(hipGetLastError());
+    return MOE_OK;
+  }
   const int64_t pieces = (int64_t)in_f * out_f / 32;
   hipLaunchKernelGGL(trellis_decode_kernel, dim3((unsigned)((pieces + 1023) / 1024)), dim3(1024), 0,
                      (hipStream_t)stream, (const uint32_t*)packed, in_f, out_f, side, expert, inner);

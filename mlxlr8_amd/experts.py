@@ -178,7 +178,8 @@ def layer_arrays(path, number):
     if widths != {k}:
         raise ValueError(f"Layer {number} is not uniform K{k}")
     if k != 4:
-        raise ValueError(f"Layer {number} is K3; this build decodes K4 trellis only")
+        raise ValueError(f"Layer {number} is K3: its experts decode (trellis.decode_inner) but this build "
+                         "has no K3 expert GEMV")
     directory = path / "experts"
     weights = SafeTensorFile(directory / f"exlr8-layer-{number:03d}.k{k}.safetensors")
     index = SafeTensorFile(directory / f"exlr8-layer-{number:03d}.index.safetensors")

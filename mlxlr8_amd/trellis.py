@@ -1,4 +1,4 @@
-"""K4 EXL3/QTIP-style trellis operators on MI355X.
+"""EXL3/QTIP-style trellis operators on MI355X (K4 GEMVs; K2/K3/K4 decode).
 
 Mirrors the operator surface of the reference module ``exlr8/trellis.py`` (format check,
 decode, ``trellis_linear``, ``expert_linear``, ``dequantize_trellis``) on PyTorch-ROCm
@@ -38,13 +38,13 @@ def _check_format(packed, k, in_features, out_features, sharded_side):
 
 def _require_k4(k):
     if k != 4:
-        raise NotImplementedError("this build runs the K4 trellis path (K2/K3 are not built yet)")
+        raise NotImplementedError("the trellis GEMVs of this build are K4; K2/K3 weights decode "
+                                  "(decode_inner, dequantize_trellis) but have no fused linear")
 
 
 def decode_inner(packed, k, in_features, out_features, sharded_side=1, expert=0):
-    """Decoded inner weights [in, out] (fp16, bit-exact codebook values) of one expert."""
+    """Decoded inner weights [in, out] (fp16, bit-exact codebook values) of one expert (K2, K3, K4)."""
     experts = _check_format(packed, k, in_features, out_features, sharded_side)
-    _require_k4(k)
     if not 0 <= expert < experts:
         raise ValueError("expert index out of range")
     require_cuda(packed)

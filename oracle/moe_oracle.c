@@ -15,7 +15,7 @@
  *                                               all 65536 entries against an independent
  *                                               integer-rounding restatement
  *                                               (tests/test_fast_decode.py:43-53)
- *   orc_decode_trellis    trellis.py:78-102     brute force: random nibbles packed MSB-first
+ *   orc_decode_trellis    trellis.py:78-102     brute force: random k-bit symbols (k = 2, 3, 4) packed MSB-first
  *                                               (ponyexl3/ref/trellis.py:13-49), placed by the
  *                                               tensor-core map (ponyexl3/ref/perm.py:8-26)
  *                                               in both storage orders (trellis.metal:44-48)

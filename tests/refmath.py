@@ -75,24 +75,28 @@ def fp8_e4m3_decode(byte):
     return np.where(b & 128, -mag, mag)
 
 
-def build_trellis_matrix(nibbles, side):
-    """Per-tile symbols nibbles [IT, OT, 256] (kernel order) -> stored bytes for one K4 matrix."""
+def build_trellis_matrix(nibbles, side, k=4):
+    """Per-tile k-bit symbols [IT, OT, 256] (kernel order) -> stored bytes for one matrix."""
     it, ot = nibbles.shape[:2]
-    words = pack_trellis(nibbles, 4)  # [IT, OT, 32]
+    words = pack_trellis(nibbles, k)  # [IT, OT, 8k]
     if side == 2:
-        stored = words.reshape(it // 8, 8, ot // 8, 8, 32).transpose(0, 2, 1, 3, 4)
+        stored = words.reshape(it // 8, 8, ot // 8, 8, 8 * k).transpose(0, 2, 1, 3, 4)
     else:
-        stored = words.reshape(it, ot // 8, 8, 32).transpose(1, 0, 2, 3)
+        stored = words.reshape(it, ot // 8, 8, 8 * k).transpose(1, 0, 2, 3)
     return np.ascontiguousarray(stored).reshape(-1).view(np.uint8)
 
 
-def expected_inner(nibbles):
-    """Inner [IT*16, OT*16] values from per-tile symbols using windows = last 4 symbols (circular)."""
+def expected_inner(nibbles, k=4):
+    """Inner [IT*16, OT*16] values from per-tile k-bit symbols: codeword i = the last 16 bits of the
+    symbols up to and including symbol i (circular within the tile)."""
     from oracle import lib
     cb = lib().codebook().astype(np.float32)
     it, ot = nibbles.shape[:2]
     n = nibbles.astype(np.uint32)
-    cw = (np.roll(n, 3, -1) << 12) | (np.roll(n, 2, -1) << 8) | (np.roll(n, 1, -1) << 4) | n
+    cw = np.zeros_like(n)
+    for j in range(-(-16 // k)):
+        cw |= np.roll(n, j, -1) << (k * j)
+    cw &= 0xFFFF
     vals = cb[cw]  # kernel order
     perm = tensor_core_perm()
     tile = np.zeros((it, ot, 256), np.float32)

@@ -47,8 +47,10 @@ def test_argument_errors_without_device():
     L = lib()
     assert L.moe_route_f32(None, None, 1, None, None, None) == -1
     assert b"null" in L.moe_last_error()
+    assert L.moe_trellis_decode_f16(ctypes.c_void_p(16), 128 * 128 // 2, 5, 128, 128, 1, 0, ctypes.c_void_p(16), None) == -1
+    assert b"2, 3, or 4" in L.moe_last_error()
     assert L.moe_trellis_decode_f16(ctypes.c_void_p(16), 128 * 128 // 2, 3, 128, 128, 1, 0, ctypes.c_void_p(16), None) == -1
-    assert b"K4" in L.moe_last_error()
+    assert b"byte count" in L.moe_last_error()
     assert L.moe_trellis_decode_f16(ctypes.c_void_p(16), 5, 4, 128, 128, 1, 0, ctypes.c_void_p(16), None) == -1
     assert b"byte count" in L.moe_last_error()
 

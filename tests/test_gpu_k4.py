@@ -246,3 +246,26 @@ def test_fp32_accumulation_known_answer(cuda):
     say(f"  col0={y[0]} want={want0} max|other|={np.abs(y[1:]).max()}")
     assert abs(y[0] - want0) <= want0 * 2.0 ** -8
     assert np.all(y[1:] == 0.0)
+
+
+@pytest.mark.parametrize("k", [2, 3])
+@pytest.mark.parametrize("side", [1, 2])
+def test_decode_inner_k2_k3_bit_exact(cuda, orc, k, side):
+    """The K2 / K3 trellis decode (the MTP layer's K3 experts): brute-force symbols and the oracle."""
+    from mlxlr8_amd.trellis import decode_inner
+    say(f"case: decode k={k} side={side}")
+    rng = np.random.default_rng(60 + 10 * k + side)
+    syms = [rng.integers(0, 1 << k, (8, 16, 256), dtype=np.uint32) for _ in range(2)]
+    host = np.concatenate([refmath.build_trellis_matrix(s, side, k) for s in syms])
+    packed = torch.from_numpy(host).to(cuda)
+    for e in range(2):
+        got = decode_inner(packed, k, 128, 256, side, e).cpu().numpy().astype(np.float32)
+        np.testing.assert_array_equal(got, refmath.expected_inner(syms[e], k))
+        np.testing.assert_array_equal(got, orc.decode(host, k, 128, 256, side, e))
+    # GLM-size K3 matrix against the oracle
+    g = torch.Generator(device=cuda)
+    g.manual_seed(70 + k)
+    big = torch.randint(0, 256, (6144 * 2048 * k // 8,), generator=g, device=cuda, dtype=torch.uint8)
+    in_f, out_f = (6144, 2048) if side == 1 else (2048, 6144)
+    got = decode_inner(big, k, in_f, out_f, side, 0).cpu().numpy().astype(np.float32)
+    np.testing.assert_array_equal(got, orc.decode(big.cpu().numpy(), k, in_f, out_f, side, 0))

@@ -99,3 +99,14 @@ def test_hadamard_matches_sylvester_matrix(orc):
     e[0, 0], e[1, 129] = 1, 2
     np.testing.assert_allclose(orc.hadamard(orc.hadamard(e)), e, atol=3e-7)
     assert np.all(orc.hadamard(e)[0, 128:] == 0)
+
+
+@pytest.mark.parametrize("k", [2, 3])
+@pytest.mark.parametrize("side", [1, 2])
+def test_oracle_decode_k2_k3_brute_force(orc, k, side):
+    # random k-bit symbols packed MSB-first (ponyexl3/ref/trellis.py:13-49 semantics), two experts
+    rng = np.random.default_rng(40 + 10 * k + side)
+    syms = [rng.integers(0, 1 << k, (8, 16, 256), dtype=np.uint32) for _ in range(2)]
+    host = np.concatenate([refmath.build_trellis_matrix(s, side, k) for s in syms])
+    for e in range(2):
+        np.testing.assert_array_equal(orc.decode(host, k, 128, 256, side, e), refmath.expected_inner(syms[e], k))
