@@ -188,6 +188,13 @@ int moe_profile_events(void** events, int count);
 int moe_segment_table(const uint32_t* ids, int n, int experts, int block_rows, int32_t* order, int32_t* counts,
                       int32_t* starts, int32_t* table, int capacity, int32_t* num_blocks, moe_stream_t stream);
 
+/* Model combine of per-slot expert values [rows, 9, hidden] bf16 (slot 8 = shared expert):
+ * out[t] = T(T(sum_{i<8} values[t,i] * scores[t,i]) + values[t,8]) + residual[t] cast to bf16,
+ * the routed sum accumulated in slot order in fp32.  16-byte aligned buffers; hidden % 8 == 0.
+ * Replaces: exlr8/model.py:415-418 (the caller-side combine after ExpertLayer.__call__). */
+int moe_combine_values(const uint16_t* values, const float* scores, const uint16_t* residual, int rows, int hidden,
+                       uint16_t* out, moe_stream_t stream);
+
 /* Prefill chunk through the joined-MXFP4 experts: router GEMV + route for `rows` rows, sorted
  * work order, grouped gate_up GEMM + gate finish, grouped down GEMM + value finish, weighted
  * combine with the shared expert and the residual.  Weights/side vectors as moe_mxfp4_mlp
@@ -217,6 +224,32 @@ int moe_k4_grouped_mlp(const uint16_t* x, const uint32_t* ids, int rows, int slo
                        const uint16_t* in_down, const uint16_t* out_down, int hidden, int intermediate,
                        uint16_t* values, void* workspace, size_t workspace_bytes, moe_stream_t stream);
 size_t moe_k4_grouped_mlp_workspace_bytes(int rows, int slots, int hidden, int intermediate, int64_t experts);
+
+/* moe_k4_grouped_mlp for trellis width k = 2, 3 or 4 (packed_bytes / (hidden*intermediate*k/8)
+ * experts; same workspace).  K2/K3 tiles are read through the generic circular window; this is
+ * the expert MLP of K3 layers (the multi-token-prediction layer) at every row count.
+ * Replaces: exlr8/fast_prefill.py:188-211 and exlr8/fast_decode.py:208-221 for k != 4
+ * (exlr8/metal/trellis.metal:25-40 window extraction). */
+int moe_trellis_grouped_mlp(int k, const uint16_t* x, const uint32_t* ids, int rows, int slots,
+                            const void* packed_gate, const void* packed_up, const void* packed_down,
+                            int64_t packed_bytes, const uint16_t* in_gate, const uint16_t* out_gate,
+                            const uint16_t* in_up, const uint16_t* out_up, const uint16_t* in_down,
+                            const uint16_t* out_down, int hidden, int intermediate, uint16_t* values, void* workspace,
+                            size_t workspace_bytes, moe_stream_t stream);
+
+/* One trellis projection y[slot] = T(out_scale[e] * H(H(x * in_scale[e]) @ inner_e)) for
+ * ids [rows, slots] at width k = 2, 3 or 4, over the grouped sorted-expert kernel: x is
+ * [rows, in] (a token row shared by its slots, x_per_slot = 0) or [rows*slots, in]; y
+ * [rows*slots, out] bf16.  Side vectors [E, in] / [E, out] fp16; side 1 (gate/up) or 2 (down)
+ * storage order.  Slots whose id is outside [0, experts) are not written.
+ * Workspace: moe_trellis_grouped_linear_workspace_bytes(rows, slots, in, out, experts).
+ * Replaces: exlr8/trellis.py:172-196 expert_linear (and trellis.metal's generic window) for k != 4. */
+int moe_trellis_grouped_linear(int k, const uint16_t* x, int x_per_slot, const uint32_t* ids, int rows, int slots,
+                               const void* packed, int64_t packed_bytes, const uint16_t* in_scale,
+                               const uint16_t* out_scale, int in_features, int out_features, int side, uint16_t* y,
+                               void* workspace, size_t workspace_bytes, moe_stream_t stream);
+size_t moe_trellis_grouped_linear_workspace_bytes(int rows, int slots, int in_features, int out_features,
+                                                  int64_t experts);
 
 /* ---------------------------------------------------------------- load-time conversion */
 

@@ -54,6 +54,12 @@ _SIGNATURES = {
     "moe_k4_grouped_mlp": (_I32, [_VP, _VP, _I32, _I32, _VP, _VP, _VP, _I64] + [_VP] * 6 + [_I32, _I32, _VP, _VP, _SZ,
                                                                                       _VP]),
     "moe_k4_grouped_mlp_workspace_bytes": (_SZ, [_I32, _I32, _I32, _I32, _I64]),
+    "moe_trellis_grouped_linear": (_I32, [_I32, _VP, _I32, _VP, _I32, _I32, _VP, _I64, _VP, _VP, _I32, _I32, _I32,
+                                          _VP, _VP, _SZ, _VP]),
+    "moe_trellis_grouped_linear_workspace_bytes": (_SZ, [_I32, _I32, _I32, _I32, _I64]),
+    "moe_combine_values": (_I32, [_VP, _VP, _VP, _I32, _I32, _VP, _VP]),
+    "moe_trellis_grouped_mlp": (_I32, [_I32, _VP, _VP, _I32, _I32, _VP, _VP, _VP, _I64] + [_VP] * 6
+                                + [_I32, _I32, _VP, _VP, _SZ, _VP]),
 }
 
 

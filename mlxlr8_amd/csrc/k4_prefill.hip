@@ -23,7 +23,13 @@
 //     for the 8 waves.  No split of K: every output is produced by one wave, no atomics.
 //   * Items are classed by M-tiles (1, 2, 4, 8) so small experts pay no padded MFMAs; each class
 //     is one persistent launch (the code table is loaded into LDS once per block).
+//   * K2/K3 tiles (the K3 experts of the multi-token-prediction layer) take the same items and
+//     MFMAs; a lane reads the 4-5 words of the circular tile stream that hold its 32 codewords
+//     (the generic window of exlr8/metal/trellis.metal:25-40) and looks every codeword up in the
+//     LDS table.
 #include <hip/hip_runtime.h>
+
+#include <type_traits>
 
 #include "moe_device.h"
 #include "moe_host.h"
@@ -53,7 +59,8 @@ __device__ __forceinline__ void kp_store_a(uint16_t* a, int64_t p, int nq, int k
 }
 
 // ---------------------------------------------------------------- prep: xh for gate and up
-// One wave per (sorted row p, 128-block kb, projection): H128(x_token * in_scale[e]) -> A buffer.
+// One wave per (sorted row p, 128-block kb, projection of nproj = 1 or 2): H128(x_row *
+// in_scale[e]) -> A buffer, x_row = the slot's token row (x_per_slot = 0) or its own row.
 // Sorted rows placed by the segment table: ids outside [0, experts) get no position.
 __device__ __forceinline__ int64_t kp_placed(const int32_t* counts, const int32_t* starts, int experts) {
   return (int64_t)starts[experts - 1] + counts[experts - 1];
@@ -62,21 +69,23 @@ __device__ __forceinline__ int64_t kp_placed(const int32_t* counts, const int32_
 __global__ __launch_bounds__(256) void kp_prep_kernel(const uint16_t* __restrict__ x, const uint32_t* __restrict__ ids,
                                                       const int32_t* __restrict__ order, const int32_t* __restrict__ counts,
                                                       const int32_t* __restrict__ starts, int experts, int n, int slots, int K,
+                                                      int nproj, int x_per_slot,
                                                       const uint16_t* __restrict__ in_gate,
                                                       const uint16_t* __restrict__ in_up, uint16_t* __restrict__ a_gate,
                                                       uint16_t* __restrict__ a_up) {
   const int64_t wid = (int64_t)blockIdx.x * 4 + wave_id_uniform();
-  const int kbs = K / 128;
-  if (wid >= (int64_t)n * kbs * 2) return;
-  const int proj = (int)(wid & 1);
-  const int kb = (int)((wid >> 1) % kbs);
-  const int64_t p = (wid >> 1) / kbs;
+  const int kbs = K / 128, sh = nproj - 1;
+  if (wid >= (int64_t)n * kbs * nproj) return;
+  const int proj = (int)(wid & sh);
+  const int kb = (int)((wid >> sh) % kbs);
+  const int64_t p = (wid >> sh) / kbs;
   if (p >= kp_placed(counts, starts, experts)) return;
   const int slot = order[p];
   const int64_t e = ids[slot];
   const int lane = lane_id();
   const int k = kb * 128 + 2 * lane;
-  const uint32_t xv = *reinterpret_cast<const uint32_t*>(x + (int64_t)(slot / slots) * K + k);
+  const int64_t xrow = x_per_slot ? slot : slot / slots;
+  const uint32_t xv = *reinterpret_cast<const uint32_t*>(x + xrow * K + k);
   const uint32_t sv = *reinterpret_cast<const uint32_t*>((proj ? in_up : in_gate) + e * K + k);
   float v0 = bf16_to_f32((uint16_t)(xv & 0xFFFFu)) * f16_to_f32((uint16_t)(sv & 0xFFFFu));
   float v1 = bf16_to_f32((uint16_t)(xv >> 16)) * f16_to_f32((uint16_t)(sv >> 16));
@@ -89,7 +98,7 @@ __global__ __launch_bounds__(256) void kp_prep_kernel(const uint16_t* __restrict
 // ---------------------------------------------------------------- grouped GEMM
 struct KpGemm {
   const uint8_t* codebook;    // device E4M3 code table (64 KB)
-  const uint8_t* packed[2];   // per projection: [E] experts of K4 tiles
+  const uint8_t* packed[2];   // per projection: [E] experts of K-bit tiles
   const uint16_t* a[2];       // per projection: A operand [n][K/64][256 B]
   int col_off[2];             // per projection: first column in `inner`
   int nproj, side, K, N;      // input / output features of one projection
@@ -98,10 +107,56 @@ struct KpGemm {
   const int32_t* nblk;
   float* inner;               // [n][inner_stride] fp32
   int inner_stride;
+  int bits;                   // trellis width K (2, 3 or 4)
 };
 
-// MT M-tiles (8 rows each) per item: items of 8 (MT - 1) < len <= 8 MT rows (MT = 1, 2, 4, 8)
-template <int MT>
+// K2/K3: the 8 codewords of each of a lane's kernel-order tile lanes L0..L0+3 (L0 = 4 (nn & 7))
+// are the 16-bit windows starting at stream bits b0 + j K, j = 0..31, of the circular tile
+// stream (codeword i ends at bit (i + 1) K + 256 K, modulo 256 K), b0 = (8 L0 K + K - 16) mod
+// 256 K.  The lane loads the words that hold bits b0 .. b0 + 31 K + 15.
+template <int KB>
+struct KpWords {
+  static constexpr int kStream = (31 * KB + 16 + 31) / 32;  // 32-bit words of the lane's window
+  uint32_t v[kStream + 1];                                   // from word b0 / 32 on (circular)
+};
+
+// The lane's two B fragments per row half rh (h = 0: slots 0-3, h = 1: slots 4-7 of each tile
+// lane), in the order the K4 piece decoder gives them; o = b0 % 32.
+template <int KB>
+__device__ __forceinline__ void kp_generic_frags(const KpWords<KB>& p, int o, const uint8_t* __restrict__ tab,
+                                                 f16x8 (&b)[2][2]) {
+  constexpr int S = KpWords<KB>::kStream;
+  uint32_t u[S];  // the stream from bit b0 on
+#pragma unroll
+  for (int k = 0; k < S; k++) u[k] = (uint32_t)(((((uint64_t)p.v[k]) << 32 | p.v[k + 1]) << o) >> 32);
+  uint32_t q[4][2];  // [tile lane L0 + i][h]: the E4M3 bytes of 4 codewords
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      uint32_t pk = 0;
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        const int pos = (8 * i + 4 * h + t) * KB, wi = pos / 32, off = pos % 32;
+        const uint32_t cw = off <= 16 ? (u[wi] >> (16 - off)) & 0xFFFFu
+                                      : __builtin_amdgcn_alignbit(u[wi], u[min(wi + 1, S - 1)], 48 - off) & 0xFFFFu;
+        pk |= (uint32_t)tab[cw] << (8 * t);
+      }
+      q[i][h] = pk;
+    }
+#pragma unroll
+  for (int rh = 0; rh < 2; rh++)
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+      b[rh][h] = frag(__builtin_amdgcn_cvt_scalef32_pk_f16_fp8(q[2 * rh][h], 1.0f, false),
+                      __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(q[2 * rh][h], 1.0f, true),
+                      __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(q[2 * rh + 1][h], 1.0f, false),
+                      __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(q[2 * rh + 1][h], 1.0f, true));
+}
+
+// MT M-tiles (8 rows each) per item: items of 8 (MT - 1) < len <= 8 MT rows (MT = 1, 2, 4, 8);
+// KB = trellis width
+template <int MT, int KB>
 __global__ __launch_bounds__(kKpThreads) void kp_gemm_kernel(KpGemm a) {
   __shared__ __attribute__((aligned(16))) uint8_t tab[65536];
   __shared__ __attribute__((aligned(16))) uint8_t abuf[2][MT * 8 * kKpRowQuad];
@@ -112,6 +167,14 @@ __global__ __launch_bounds__(kKpThreads) void kp_gemm_kernel(KpGemm a) {
   const int lane_off = (nn >> 3) * 128 + (nn & 7) * 16;
   const int src_lane = (lane & 7) == 0 ? lane + 7 : lane - 1;
   const int s4 = w & 3;
+  // K2/K3: the lane's first window bit b0 within its tile, and the tile words it reads
+  constexpr int kNw = 8 * KB;
+  const int b0 = (8 * 4 * (nn & 7) * KB + KB - 16 + 256 * KB) % (256 * KB), bo = b0 & 31;
+  int gw[KB == 4 ? 1 : KpWords<KB>::kStream + 1];
+  if constexpr (KB != 4) {
+#pragma unroll
+    for (int k = 0; k <= KpWords<KB>::kStream; k++) gw[k] = (b0 / 32 + k) % kNw;
+  }
   const int nblk = *a.nblk;
   const int items = nblk * a.nproj * ncb;
   for (int item = blockIdx.x; item < items; item += gridDim.x) {
@@ -122,9 +185,19 @@ __global__ __launch_bounds__(kKpThreads) void kp_gemm_kernel(KpGemm a) {
     // the last item of N % 256 == 128 has one column block: waves 4-7 then only stage A
     const bool active = 2 * cb + (w >> 2) < obs;
     const int ob = min(2 * cb + (w >> 2), obs - 1);
-    const uint8_t* wbase = a.packed[proj] + lane_off + 256 * s4;
-    auto piece = [&](int q) -> u32x4 {
-      return *reinterpret_cast<const u32x4*>(wbase + chunk_offset(a.side, e, ob, 4 * q + g, it, obs));
+    using Piece = std::conditional_t<KB == 4, u32x4, KpWords<KB>>;
+    const uint8_t* wbase = a.packed[proj] + (KB == 4 ? lane_off + 256 * s4 : 32 * KB * (2 * s4 + (nn >> 3)));
+    auto piece = [&](int q) -> Piece {
+      if constexpr (KB == 4) {
+        return *reinterpret_cast<const u32x4*>(wbase + chunk_offset(a.side, e, ob, 4 * q + g, it, obs));
+      } else {
+        const uint32_t* t =
+            reinterpret_cast<const uint32_t*>(wbase + chunk_index(a.side, e, ob, 4 * q + g, it, obs) * (256 * KB));
+        Piece r;
+#pragma unroll
+        for (int k = 0; k <= KpWords<KB>::kStream; k++) r.v[k] = t[gw[k]];
+        return r;
+      }
     };
     // A staging: chunk c of the quad = row c / 16, 16 B part c % 16 ([rh][hl][g] of the row)
     constexpr int kChunks = MT * 8 * 16, kPer = (kChunks + kKpThreads - 1) / kKpThreads;
@@ -155,27 +228,35 @@ __global__ __launch_bounds__(kKpThreads) void kp_gemm_kernel(KpGemm a) {
     i32x4 fa[kPer];
     fetch_a(0, fa);
     put_a(fa, abuf[0]);
-    u32x4 pc0 = piece(0), pc1 = piece(min(1, nq - 1));
+    Piece pc0 = piece(0), pc1 = piece(min(1, nq - 1));
     fetch_a(min(1, nq - 1), fa);
     __syncthreads();
-    auto quad = [&](const uint8_t* ab, const u32x4& pc) {
+    auto mfmas = [&](const uint8_t* ab, int rh, const f16x8& b0, const f16x8& b1) {
+#pragma unroll
+      for (int mt = 0; mt < MT; mt++) {
+        const f16x8 av = *reinterpret_cast<const f16x8*>(ab + ((mt * 2 + rh) * 16 + nn) * 64 + g * 16);
+        acc[mt][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b0, acc[mt][0], 0, 0, 0);
+        acc[mt][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b1, acc[mt][1], 0, 0, 0);
+      }
+    };
+    auto quad = [&](const uint8_t* ab, const Piece& pc) {
       if (!active) return;
-      const uint32_t prior = (uint32_t)__shfl((int)pc.w, src_lane, 64);
+      if constexpr (KB == 4) {
+        const uint32_t prior = (uint32_t)__shfl((int)pc.w, src_lane, 64);
 #pragma unroll
-      for (int rh = 0; rh < 2; rh++) {
-        f16x2 qv[2][4];
-        if (rh == 0)
-          decode_pair_words_f16<2, 2>(pc.x, pc.y, prior, tab, qv);
-        else
-          decode_pair_words_f16<2, 2>(pc.z, pc.w, pc.y, tab, qv);
-        const f16x8 b0 = frag(qv[0][0], qv[0][1], qv[1][0], qv[1][1]);
-        const f16x8 b1 = frag(qv[0][2], qv[0][3], qv[1][2], qv[1][3]);
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++) {
-          const f16x8 av = *reinterpret_cast<const f16x8*>(ab + ((mt * 2 + rh) * 16 + nn) * 64 + g * 16);
-          acc[mt][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b0, acc[mt][0], 0, 0, 0);
-          acc[mt][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b1, acc[mt][1], 0, 0, 0);
+        for (int rh = 0; rh < 2; rh++) {
+          f16x2 qv[2][4];
+          if (rh == 0)
+            decode_pair_words_f16<2, 2>(pc.x, pc.y, prior, tab, qv);
+          else
+            decode_pair_words_f16<2, 2>(pc.z, pc.w, pc.y, tab, qv);
+          mfmas(ab, rh, frag(qv[0][0], qv[0][1], qv[1][0], qv[1][1]), frag(qv[0][2], qv[0][3], qv[1][2], qv[1][3]));
         }
+      } else {
+        f16x8 bf[2][2];
+        kp_generic_frags<KB>(pc, bo, tab, bf);
+        mfmas(ab, 0, bf[0][0], bf[0][1]);
+        mfmas(ab, 1, bf[1][0], bf[1][1]);
       }
     };
     for (int q = 0; q < nq; q += 2) {  // nq is even (K % 128 == 0)
@@ -307,20 +388,27 @@ KpWorkspace kp_carve(void* base, int64_t n, int h, int m, int64_t experts) {
   return w;
 }
 
-int launch_kp_gemm(const KpGemm& g, hipStream_t s) {
+template <int KB>
+int launch_kp_gemm_k(const KpGemm& g, hipStream_t s) {
   // persistent blocks, items strided over them.  The classes of up to 4 M-tiles fit two blocks per
   // CU (68-80 KB of LDS) and get 4 blocks per CU queued, so the CUs stay busy to the end of the
   // launch; the 8-tile class (96 KB) runs one block per CU.
   const int blocks = device_cus() > 0 ? device_cus() : 256;
-  hipLaunchKernelGGL(kp_gemm_kernel<1>, dim3(4 * blocks), dim3(kKpThreads), 0, s, g);
+  hipLaunchKernelGGL((kp_gemm_kernel<1, KB>), dim3(4 * blocks), dim3(kKpThreads), 0, s, g);
   MOE_HIP(hipGetLastError());
-  hipLaunchKernelGGL(kp_gemm_kernel<2>, dim3(4 * blocks), dim3(kKpThreads), 0, s, g);
+  hipLaunchKernelGGL((kp_gemm_kernel<2, KB>), dim3(4 * blocks), dim3(kKpThreads), 0, s, g);
   MOE_HIP(hipGetLastError());
-  hipLaunchKernelGGL(kp_gemm_kernel<4>, dim3(4 * blocks), dim3(kKpThreads), 0, s, g);
+  hipLaunchKernelGGL((kp_gemm_kernel<4, KB>), dim3(4 * blocks), dim3(kKpThreads), 0, s, g);
   MOE_HIP(hipGetLastError());
-  hipLaunchKernelGGL(kp_gemm_kernel<8>, dim3(blocks), dim3(kKpThreads), 0, s, g);
+  hipLaunchKernelGGL((kp_gemm_kernel<8, KB>), dim3(blocks), dim3(kKpThreads), 0, s, g);
   MOE_HIP(hipGetLastError());
   return MOE_OK;
+}
+
+int launch_kp_gemm(const KpGemm& g, hipStream_t s) {
+  if (g.bits == 4) return launch_kp_gemm_k<4>(g, s);
+  if (g.bits == 3) return launch_kp_gemm_k<3>(g, s);
+  return launch_kp_gemm_k<2>(g, s);
 }
 
 }  // namespace
@@ -335,20 +423,22 @@ size_t moe_k4_grouped_mlp_workspace_bytes(int rows, int slots, int hidden, int i
   return kp_carve(nullptr, (int64_t)rows * slots, hidden, intermediate, experts).bytes;
 }
 
-int moe_k4_grouped_mlp(const uint16_t* x, const uint32_t* ids, int rows, int slots, const void* packed_gate,
-                       const void* packed_up, const void* packed_down, int64_t packed_bytes, const uint16_t* in_gate,
-                       const uint16_t* out_gate, const uint16_t* in_up, const uint16_t* out_up,
-                       const uint16_t* in_down, const uint16_t* out_down, int hidden, int intermediate,
-                       uint16_t* values, void* workspace, size_t workspace_bytes, moe_stream_t stream) {
+int moe_trellis_grouped_mlp(int k, const uint16_t* x, const uint32_t* ids, int rows, int slots,
+                            const void* packed_gate, const void* packed_up, const void* packed_down,
+                            int64_t packed_bytes, const uint16_t* in_gate, const uint16_t* out_gate,
+                            const uint16_t* in_up, const uint16_t* out_up, const uint16_t* in_down,
+                            const uint16_t* out_down, int hidden, int intermediate, uint16_t* values, void* workspace,
+                            size_t workspace_bytes, moe_stream_t stream) {
+  MOE_ARG(k >= 2 && k <= 4, "EXLR8 trellis width must be 2, 3, or 4 (got %d)", k);
   MOE_ARG(x && ids && packed_gate && packed_up && packed_down && in_gate && out_gate && in_up && out_up && in_down &&
               out_down && values && workspace,
           "null pointer argument");
   MOE_ARG(rows >= 1 && slots >= 1, "rows and slots must be positive");
   MOE_ARG(hidden > 0 && intermediate > 0 && hidden % 128 == 0 && intermediate % 128 == 0,
           "hidden and intermediate must be positive multiples of 128 (got %d, %d)", hidden, intermediate);
-  const int64_t per = (int64_t)hidden * intermediate / 2;
-  MOE_ARG(packed_bytes > 0 && packed_bytes % per == 0, "packed size %lld is not a whole number of K4 experts",
-          (long long)packed_bytes);
+  const int64_t per = (int64_t)hidden * intermediate * k / 8;
+  MOE_ARG(packed_bytes > 0 && packed_bytes % per == 0, "packed size %lld is not a whole number of K%d experts",
+          (long long)packed_bytes, k);
   const int64_t experts = packed_bytes / per;
   MOE_ARG(experts <= 1024, "at most 1024 experts (got %lld)", (long long)experts);
   const int64_t n = (int64_t)rows * slots;
@@ -365,7 +455,7 @@ int moe_k4_grouped_mlp(const uint16_t* x, const uint32_t* ids, int rows, int slo
     return rc;
   const int64_t pw = n * (hidden / 128) * 2;
   hipLaunchKernelGGL(kp_prep_kernel, dim3((unsigned)((pw + 3) / 4)), dim3(256), 0, s, x, ids, w.order, w.counts, w.starts,
-                     (int)experts, (int)n, slots, hidden, in_gate, in_up, w.a_gate, w.a_up);
+                     (int)experts, (int)n, slots, hidden, 2, 0, in_gate, in_up, w.a_gate, w.a_up);
   MOE_HIP(hipGetLastError());
   const uint8_t* table = codebook_device_table();
   if (!table) return fail(MOE_ENOTSUP, "code table not initialised on this device");
@@ -386,6 +476,7 @@ int moe_k4_grouped_mlp(const uint16_t* x, const uint32_t* ids, int rows, int slo
   g.nblk = w.nblk;
   g.inner = w.inner_gu;
   g.inner_stride = 2 * intermediate;
+  g.bits = k;
   if ((rc = launch_kp_gemm(g, s))) return rc;
   const int64_t fw = n * (intermediate / 128);
   hipLaunchKernelGGL(kp_gate_finish_kernel, dim3((unsigned)((fw + 3) / 4)), dim3(256), 0, s, w.inner_gu, ids, w.order,
@@ -405,12 +496,85 @@ int moe_k4_grouped_mlp(const uint16_t* x, const uint32_t* ids, int rows, int slo
   d.nblk = w.nblk;
   d.inner = w.inner_d;
   d.inner_stride = hidden;
+  d.bits = k;
   if ((rc = launch_kp_gemm(d, s))) return rc;
   const int64_t vw = n * (hidden / 128);
   hipLaunchKernelGGL(kp_value_finish_kernel, dim3((unsigned)((vw + 3) / 4)), dim3(256), 0, s, w.inner_d, ids, w.order,
                      w.counts, w.starts, (int)experts, (int)n, hidden, out_down, values);
   MOE_HIP(hipGetLastError());
   return MOE_OK;
+}
+
+size_t moe_trellis_grouped_linear_workspace_bytes(int rows, int slots, int in_features, int out_features,
+                                                  int64_t experts) {
+  if (rows <= 0 || slots <= 0 || in_features <= 0 || out_features <= 0 || experts <= 0) return 0;
+  return kp_carve(nullptr, (int64_t)rows * slots, max(in_features, out_features), 128, experts).bytes;
+}
+
+int moe_trellis_grouped_linear(int k, const uint16_t* x, int x_per_slot, const uint32_t* ids, int rows, int slots,
+                               const void* packed, int64_t packed_bytes, const uint16_t* in_scale,
+                               const uint16_t* out_scale, int in_features, int out_features, int side, uint16_t* y,
+                               void* workspace, size_t workspace_bytes, moe_stream_t stream) {
+  MOE_ARG(k >= 2 && k <= 4, "EXLR8 trellis width must be 2, 3, or 4 (got %d)", k);
+  MOE_ARG(x && ids && packed && in_scale && out_scale && y && workspace, "null pointer argument");
+  MOE_ARG(rows >= 1 && slots >= 1, "rows and slots must be positive");
+  MOE_ARG(side == 1 || side == 2, "sharded_side must be 1 or 2 (got %d)", side);
+  MOE_ARG(in_features > 0 && out_features > 0 && in_features % 128 == 0 && out_features % 128 == 0,
+          "trellis dimensions must be positive multiples of 128 (got %d, %d)", in_features, out_features);
+  const int64_t per = (int64_t)in_features * out_features * k / 8;
+  MOE_ARG(packed_bytes > 0 && packed_bytes % per == 0, "packed size %lld is not a whole number of K%d experts",
+          (long long)packed_bytes, k);
+  const int64_t experts = packed_bytes / per;
+  MOE_ARG(experts <= 1024, "at most 1024 experts (got %lld)", (long long)experts);
+  const int64_t n = (int64_t)rows * slots;
+  MOE_ARG(n <= (int64_t)1 << 24, "too many slots (%lld)", (long long)n);
+  const KpWorkspace w = kp_carve(workspace, n, max(in_features, out_features), 128, experts);
+  if (workspace_bytes < w.bytes)
+    return fail(MOE_EWORKSPACE, "workspace too small: %zu < %zu bytes", workspace_bytes, w.bytes);
+  int rc = ensure_device_ready();
+  if (rc) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  if ((rc = moe_segment_table(ids, (int)n, (int)experts, kKpRows, w.order, w.counts, w.starts, w.blk, w.cap, w.nblk,
+                              stream)))
+    return rc;
+  const int64_t pw = n * (in_features / 128);
+  hipLaunchKernelGGL(kp_prep_kernel, dim3((unsigned)((pw + 3) / 4)), dim3(256), 0, s, x, ids, w.order, w.counts, w.starts,
+                     (int)experts, (int)n, slots, in_features, 1, x_per_slot ? 1 : 0, in_scale, in_scale, w.a_gate,
+                     w.a_gate);
+  MOE_HIP(hipGetLastError());
+  const uint8_t* table = codebook_device_table();
+  if (!table) return fail(MOE_ENOTSUP, "code table not initialised on this device");
+  KpGemm g{};
+  g.codebook = table;
+  g.packed[0] = static_cast<const uint8_t*>(packed);
+  g.a[0] = w.a_gate;
+  g.col_off[0] = 0;
+  g.nproj = 1;
+  g.side = side;
+  g.K = in_features;
+  g.N = out_features;
+  g.blk = w.blk;
+  g.cap = w.cap;
+  g.nblk = w.nblk;
+  g.inner = w.inner_d;
+  g.inner_stride = out_features;
+  g.bits = k;
+  if ((rc = launch_kp_gemm(g, s))) return rc;
+  const int64_t vw = n * (out_features / 128);
+  hipLaunchKernelGGL(kp_value_finish_kernel, dim3((unsigned)((vw + 3) / 4)), dim3(256), 0, s, w.inner_d, ids, w.order,
+                     w.counts, w.starts, (int)experts, (int)n, out_features, out_scale, y);
+  MOE_HIP(hipGetLastError());
+  return MOE_OK;
+}
+
+int moe_k4_grouped_mlp(const uint16_t* x, const uint32_t* ids, int rows, int slots, const void* packed_gate,
+                       const void* packed_up, const void* packed_down, int64_t packed_bytes, const uint16_t* in_gate,
+                       const uint16_t* out_gate, const uint16_t* in_up, const uint16_t* out_up,
+                       const uint16_t* in_down, const uint16_t* out_down, int hidden, int intermediate,
+                       uint16_t* values, void* workspace, size_t workspace_bytes, moe_stream_t stream) {
+  return moe_trellis_grouped_mlp(4, x, ids, rows, slots, packed_gate, packed_up, packed_down, packed_bytes, in_gate,
+                                 out_gate, in_up, out_up, in_down, out_down, hidden, intermediate, values, workspace,
+                                 workspace_bytes, stream);
 }
 
 }  // extern "C"

@@ -350,13 +350,17 @@ __device__ __forceinline__ void decode_pair_words_f16(uint32_t w0, uint32_t w1, 
 }
 
 // ---------------------------------------------------------------- K4 storage and MFMA fragments
-// 1 KB chunk (8 tiles of 128 B) of expert e, output block ob (128 columns), input tile tk of a
-// packed projection with `it` input tiles and `obs` output blocks (side 1: gate/up order, side 2:
-// down order)
+// Chunk of 8 tiles (256 K bytes at K bits: 1 KB at K4) of expert e, output block ob (128 columns),
+// input tile tk of a packed projection with `it` input tiles and `obs` output blocks (side 1:
+// gate/up order, side 2: down order); chunk_offset is its K4 byte offset
+__device__ __forceinline__ uint64_t chunk_index(int side, uint64_t e, uint32_t ob, uint32_t tk, uint32_t it,
+                                                uint32_t obs) {
+  if (side == 2) return (((e * (it / 8u) + tk / 8u) * obs + ob) * 8u + tk % 8u);
+  return ((e * obs + ob) * it + tk);
+}
 __device__ __forceinline__ uint64_t chunk_offset(int side, uint64_t e, uint32_t ob, uint32_t tk, uint32_t it,
                                                  uint32_t obs) {
-  if (side == 2) return ((((e * (it / 8u) + tk / 8u) * obs + ob) * 8u + tk % 8u) << 10);
-  return (((e * obs + ob) * it + tk) << 10);
+  return chunk_index(side, e, ob, tk, it, obs) << 10;
 }
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));

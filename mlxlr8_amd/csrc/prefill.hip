@@ -740,6 +740,21 @@ using namespace moe;
 
 extern "C" {
 
+int moe_combine_values(const uint16_t* values, const float* scores, const uint16_t* residual, int rows, int hidden,
+                       uint16_t* out, moe_stream_t stream) {
+  MOE_ARG(values && scores && residual && out, "null pointer argument");
+  MOE_ARG(rows >= 1, "rows must be positive (got %d)", rows);
+  MOE_ARG(hidden > 0 && hidden % 8 == 0, "hidden must be a positive multiple of 8 (got %d)", hidden);
+  MOE_ARG((((uintptr_t)values | (uintptr_t)residual | (uintptr_t)out) & 15) == 0,
+          "values, residual and out must be 16-byte aligned");
+  int rc = ensure_device_ready();
+  if (rc) return rc;
+  hipLaunchKernelGGL(pf_combine_kernel, dim3(rows), dim3(256), 0, (hipStream_t)stream, values, scores, residual,
+                     hidden, out);
+  MOE_HIP(hipGetLastError());
+  return MOE_OK;
+}
+
 int moe_segment_table(const uint32_t* ids, int n, int experts, int block_rows, int32_t* order, int32_t* counts,
                       int32_t* starts, int32_t* table, int capacity, int32_t* num_blocks, moe_stream_t stream) {
   MOE_ARG((ids && order) || n == 0, "null ids/order with n > 0");

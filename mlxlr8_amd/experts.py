@@ -1,4 +1,4 @@
-"""Resident K4 expert layer (mirrors the reference ``exlr8/experts.py`` ExpertLayer).
+"""Resident trellis expert layer (mirrors the reference ``exlr8/experts.py`` ExpertLayer).
 
 The reference loads packed experts from safetensors; this class takes device tensors that
 are already resident in HBM (288 GB per MI355X holds every expert of many layers), so the
@@ -23,8 +23,8 @@ class ExpertLayer:
     """
 
     def __init__(self, packed, scales, hidden, intermediate, k=4, number=0):
-        if k != 4:
-            raise ValueError(f"Layer {number} is not uniform K4")
+        if k not in (2, 3, 4):
+            raise ValueError("EXLR8 trellis width must be 2, 3, or 4")
         self.k, self.hidden, self.intermediate, self.number = k, hidden, intermediate, number
         self.expert_bytes = hidden * intermediate * k // 8
         self.store = SimpleNamespace(resident=True, optimize=True)
@@ -44,7 +44,8 @@ class ExpertLayer:
 
     def __call__(self, x, ids):
         """values[*ids.shape, hidden] for the selected experts (exlr8/experts.py:150-188): up to 16
-        rows through the decode MLP, more through the grouped (sorted-by-expert) prefill MLP."""
+        rows through the decode MLP, more through the grouped (sorted-by-expert) prefill MLP (K2/K3
+        experts take the grouped MLP at every row count)."""
         if self.affine is not None:
             return self.affine.slots(x, ids)
         mlp = fast_expert_mlp if ids.numel() // ids.shape[-1] <= 16 else grouped_expert_mlp
@@ -63,8 +64,8 @@ class ExpertLayer:
         decode block (one C call, no per-call tensor work); results land in `.out`, `.ids`, `.scores`."""
         h = self.hidden
         rows = x.numel() // h
-        if rows > 8 or self.experts != 257 or x.dtype != BF16:
-            raise ValueError("prepare_decode needs <= 8 bf16 rows and 256 routed + 1 shared experts")
+        if rows > 8 or self.experts != 257 or x.dtype != BF16 or self.k != 4:
+            raise ValueError("prepare_decode needs <= 8 bf16 rows and 256 routed + 1 shared K4 experts")
         require_cuda(x, residual, router_weight, bias)
         call = SimpleNamespace()
         call.x = x.reshape(rows, h).contiguous()
@@ -93,8 +94,8 @@ class ExpertLayer:
         by reference, so a stack can feed one layer's `.out` to the next layer's `x`."""
         h = self.hidden
         rows = x.numel() // h
-        if rows > 8 or self.experts != 257 or x.dtype != BF16:
-            raise ValueError("prepare_layer_decode needs <= 8 bf16 rows and 256 routed + 1 shared experts")
+        if rows > 8 or self.experts != 257 or x.dtype != BF16 or self.k != 4:
+            raise ValueError("prepare_layer_decode needs <= 8 bf16 rows and 256 routed + 1 shared K4 experts")
         if not x.is_contiguous():
             raise ValueError("the layer input must be contiguous (it is bound by address)")
         require_cuda(x, norm_weight, router_weight, bias)
@@ -133,8 +134,8 @@ class ExpertLayer:
         rows = x.numel() // h
         if rows > 8:
             raise ValueError("decode_block handles up to 8 token rows")
-        if self.experts != 257:
-            raise ValueError("decode_block needs 256 routed experts plus the shared expert")
+        if self.experts != 257 or self.k != 4:
+            raise ValueError("decode_block needs 256 routed K4 experts plus the shared expert")
         if x.dtype != BF16:
             raise ValueError("this build computes bf16 activations")
         require_cuda(x, residual, router_weight, bias)
@@ -177,9 +178,6 @@ def layer_arrays(path, number):
     k = 3 if number == 78 else 4
     if widths != {k}:
         raise ValueError(f"Layer {number} is not uniform K{k}")
-    if k != 4:
-        raise ValueError(f"Layer {number} is K3: its experts decode (trellis.decode_inner) but this build "
-                         "has no K3 expert GEMV")
     directory = path / "experts"
     weights = SafeTensorFile(directory / f"exlr8-layer-{number:03d}.k{k}.safetensors")
     index = SafeTensorFile(directory / f"exlr8-layer-{number:03d}.index.safetensors")
@@ -235,8 +233,8 @@ class ExpertStore:
 
 def _from_store(cls, store, number):
     """ExpertLayer of layer `number` of an ExpertStore, resident on the store's device; with
-    ``optimize`` and the GLM-5.3 shape (6144, 2048) its experts are converted to joined MXFP4 and
-    served by them (exlr8/experts.py:132-148)."""
+    ``optimize``, K4 and the GLM-5.3 shape (6144, 2048) its experts are converted to joined MXFP4
+    and served by them (exlr8/experts.py:132-148); K3 layers stay trellis."""
     k, hidden, intermediate, packed, scales = layer_arrays(store.path, number)
     dev = store.device
     layer = cls({p: torch.from_numpy(a).to(dev) for p, a in packed.items()},
@@ -245,7 +243,7 @@ def _from_store(cls, store, number):
     layer.store = store
     store.resident_bytes += sum(a.nbytes for a in packed.values())
     store.resident_bytes += sum(v.nbytes for pair in scales.values() for v in pair)
-    if store.optimize and (hidden, intermediate) == (6144, 2048):
+    if store.optimize and k == 4 and (hidden, intermediate) == (6144, 2048):
         from .joined_mxfp4 import JoinedMXFP4
         layer.affine = JoinedMXFP4(layer)
         store.resident_bytes += (sum(a.numel() * a.element_size() for v in layer.affine.weights.values() for a in v)

@@ -1,13 +1,15 @@
-"""Selected-expert K4 MLP on MI355X (mirrors the reference ``exlr8/fast_decode.py``).
+"""Selected-expert trellis MLP on MI355X (mirrors the reference ``exlr8/fast_decode.py``).
 
 ``fast_expert_mlp`` returns per-slot expert values; ``compiled_expert_mlp_finish`` returns
-the combined ``residual + (routed + shared)`` output.  Both run gate/up, typed SwiGLU and
-down as decode-fused GEMVs in ``libmoe_mi355x.so``.
+the combined ``residual + (routed + shared)`` output.  K4 experts run gate/up, typed SwiGLU and
+down as decode-fused GEMVs in ``libmoe_mi355x.so``; K2/K3 experts (the K3 multi-token-prediction
+layer) run through the library's generic-window grouped trellis MLP and its combine kernel.
 """
 import torch
 
 from ._lib import check, lib, ptr, require_cuda, stream, workspace
-from .trellis import BF16, _check_format, _nbytes, _require_k4, _rows_for, expert_linear
+from .fast_prefill import grouped_expert_mlp
+from .trellis import BF16, _check_format, _nbytes, _rows_for, expert_linear
 
 MAX_ROWS = 8  # token rows per kernel call; larger batches are split on the host
 
@@ -18,7 +20,6 @@ def fast_expert_linear(x, indices, packed, in_scale, out_scale, k, in_features, 
 
 
 def _validate(x, indices, packed, scales, k, hidden, intermediate):
-    _require_k4(k)
     if _rows_for(x, indices, hidden):
         raise ValueError("the expert MLP takes one activation row per token")
     for projection in ("gate", "up", "down"):
@@ -48,6 +49,8 @@ def fast_expert_mlp(x, indices, packed, scales, k, hidden, intermediate, *, reus
     if fp8 is not None or expert_to_slot is not None:
         raise NotImplementedError("FP8 expert caches are not part of the MI355X build")
     _validate(x, indices, packed, scales, k, hidden, intermediate)
+    if k != 4:
+        return grouped_expert_mlp(x, indices, packed, scales, k, hidden, intermediate)
     slots = indices.shape[-1]
     ids = indices.reshape(-1, slots).to(torch.int32).contiguous()
     rows = ids.shape[0]
@@ -64,9 +67,30 @@ def fast_expert_mlp(x, indices, packed, scales, k, hidden, intermediate, *, reus
     return values.reshape(*indices.shape, hidden)
 
 
-def mlp_finish(x, indices, scores, residual, packed, scales, hidden, intermediate):
+def combine_values(values, scores, residual):
+    """exlr8/model.py:415-418: residual + T(T(sum_i values_i * scores_i) + values_8), bf16."""
+    hidden = values.shape[-1]
+    rows = values.numel() // (9 * hidden)
+    if values.dtype != BF16 or values.numel() != rows * 9 * hidden or rows < 1:
+        raise ValueError("values must be bf16 [..., 9, hidden]")
+    if scores.numel() != rows * 8 or residual.numel() != rows * hidden:
+        raise ValueError("scores and residual do not match the values")
+    require_cuda(values, scores, residual)
+    v = values.reshape(rows * 9, hidden).contiguous()
+    sc = scores.reshape(rows, 8).to(torch.float32).contiguous()
+    res = residual.reshape(rows, hidden).to(BF16).contiguous()
+    out = torch.empty((rows, hidden), dtype=BF16, device=values.device)
+    check(lib().moe_combine_values(ptr(v), ptr(sc), ptr(res), rows, hidden, ptr(out), stream(values.device)))
+    return out.reshape(residual.shape)
+
+
+def mlp_finish(x, indices, scores, residual, packed, scales, hidden, intermediate, k=4):
     """Expert MLP plus the weighted combine with the shared expert (slot 8) and the residual."""
-    _validate(x.reshape(-1, hidden), indices.reshape(-1, 9), packed, scales, 4, hidden, intermediate)
+    _validate(x.reshape(-1, hidden), indices.reshape(-1, 9), packed, scales, k, hidden, intermediate)
+    if k != 4:
+        values = grouped_expert_mlp(x.reshape(-1, hidden), indices.reshape(-1, 9), packed, scales, k, hidden,
+                                    intermediate)
+        return combine_values(values, scores, residual)
     rows = x.numel() // hidden
     xr = x.reshape(rows, hidden).contiguous()
     ids = indices.reshape(rows, 9).to(torch.int32).contiguous()
@@ -90,6 +114,6 @@ def compiled_expert_mlp_finish(expert):
     h, m = expert.hidden, expert.intermediate
 
     def apply(x, indices, scores, residual):
-        return mlp_finish(x, indices, scores, residual, expert.packed, expert.scales, h, m)
+        return mlp_finish(x, indices, scores, residual, expert.packed, expert.scales, h, m, expert.k)
 
     return apply

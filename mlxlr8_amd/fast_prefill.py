@@ -3,8 +3,9 @@
 ``plan(indices, experts, block_rows)`` returns ``(sorted_ids, order, table, count)`` as the
 reference's ``_plan``: ``order`` sorts the flat ids (stable within an expert), ``table`` is the
 ``[3, blocks]`` (expert, first, length) block table and ``count`` the number of used blocks.
-The table is computed on the GPU by ``moe_segment_table``.  ``grouped_expert_mlp`` runs the K4
-expert MLP of every slot with one weight stream per sorted expert block (``moe_k4_grouped_mlp``).
+The table is computed on the GPU by ``moe_segment_table``.  ``grouped_expert_mlp`` runs the K2/K3/K4
+expert MLP of every slot with one weight stream per sorted expert block
+(``moe_trellis_grouped_mlp``).
 """
 import torch
 
@@ -45,16 +46,16 @@ def block_rows(rows, experts):
 
 
 def grouped_expert_mlp(x, indices, packed, scales, k, hidden, intermediate, *, half_dot=False):
-    """values[*indices.shape, hidden] of the K4 expert MLPs (exlr8/fast_prefill.py:188-211).
+    """values[*indices.shape, hidden] of the K-bit expert MLPs (exlr8/fast_prefill.py:188-211).
 
-    ``packed``/``scales`` are the ``ExpertLayer`` dictionaries.  ``x`` holds one row per row of
-    ``indices`` (the row's slots share it).  The matrix operands are fp16 hi/lo splits of the
-    fp32 activations with fp32 accumulation (``half_dot`` is accepted for signature parity; the
-    result is the float32-dot one either way).
+    ``packed``/``scales`` are the ``ExpertLayer`` dictionaries; ``k`` is 2, 3 or 4.  ``x`` holds
+    one row per row of ``indices`` (the row's slots share it).  The matrix operands are fp16
+    hi/lo splits of the fp32 activations with fp32 accumulation (``half_dot`` is accepted for
+    signature parity; the result is the float32-dot one either way).
     """
     del half_dot
-    if k != 4:
-        raise ValueError(f"this build decodes K4 trellis only (got k={k})")
+    if k not in (2, 3, 4):
+        raise ValueError("EXLR8 trellis width must be 2, 3, or 4")
     if x.dtype != BF16:
         raise ValueError("this build computes bf16 activations")
     require_cuda(x, indices, *packed.values())
@@ -67,7 +68,7 @@ def grouped_expert_mlp(x, indices, packed, scales, k, hidden, intermediate, *, h
     xr = xr.contiguous()
     pg, pu, pd = (packed[p].contiguous() for p in ("gate", "up", "down"))
     nbytes = pg.numel() * pg.element_size()
-    experts = nbytes // (hidden * intermediate // 2)
+    experts = nbytes // (hidden * intermediate * k // 8)
     sc = {p: tuple(v.to(torch.float16).contiguous() for v in scales[p]) for p in ("gate", "up", "down")}
     values = torch.empty((rows * slots, hidden), dtype=BF16, device=x.device)
     need = lib().moe_k4_grouped_mlp_workspace_bytes(rows, slots, hidden, intermediate, experts)
@@ -76,8 +77,8 @@ def grouped_expert_mlp(x, indices, packed, scales, k, hidden, intermediate, *, h
     if ws is None or ws.numel() < need:
         ws = torch.empty(need, dtype=torch.uint8, device=x.device)
         _grouped_ws[key] = ws
-    check(lib().moe_k4_grouped_mlp(ptr(xr), ptr(ids), rows, slots, ptr(pg), ptr(pu), ptr(pd), nbytes,
-                                   ptr(sc["gate"][0]), ptr(sc["gate"][1]), ptr(sc["up"][0]), ptr(sc["up"][1]),
-                                   ptr(sc["down"][0]), ptr(sc["down"][1]), hidden, intermediate, ptr(values),
-                                   ptr(ws), ws.numel(), stream(x.device)))
+    check(lib().moe_trellis_grouped_mlp(k, ptr(xr), ptr(ids), rows, slots, ptr(pg), ptr(pu), ptr(pd), nbytes,
+                                        ptr(sc["gate"][0]), ptr(sc["gate"][1]), ptr(sc["up"][0]),
+                                        ptr(sc["up"][1]), ptr(sc["down"][0]), ptr(sc["down"][1]), hidden,
+                                        intermediate, ptr(values), ptr(ws), ws.numel(), stream(x.device)))
     return values.reshape(*indices.shape, hidden)

@@ -50,10 +50,11 @@ def router(device, seed, hidden=HIDDEN, experts=256, zipf=False):
     return w.contiguous(), bias.contiguous()
 
 
-def k4_layer(device, seed, hidden=HIDDEN, intermediate=INTER, experts=EXPERTS):
-    """dict(packed={gate,up,down}, scales={gate:(in,out), up:(in,out), down:(in,out)})."""
+def k4_layer(device, seed, hidden=HIDDEN, intermediate=INTER, experts=EXPERTS, k=4):
+    """dict(packed={gate,up,down}, scales={gate:(in,out), up:(in,out), down:(in,out)}) of k-bit
+    trellis experts (every bitstream is a valid trellis)."""
     g = _gen(device, seed)
-    nbytes = experts * hidden * intermediate // 2
+    nbytes = experts * hidden * intermediate * k // 8
     packed = {p: torch.randint(0, 256, (nbytes,), generator=g, device=device, dtype=torch.uint8)
               for p in ("gate", "up", "down")}
     mu = math.log(1.0 / math.sqrt(hidden))

@@ -1,4 +1,4 @@
-"""EXL3/QTIP-style trellis operators on MI355X (K4 GEMVs; K2/K3/K4 decode).
+"""EXL3/QTIP-style trellis operators on MI355X (K4 GEMVs; K2/K3 grouped linears; K2/K3/K4 decode).
 
 Mirrors the operator surface of the reference module ``exlr8/trellis.py`` (format check,
 decode, ``trellis_linear``, ``expert_linear``, ``dequantize_trellis``) on PyTorch-ROCm
@@ -36,10 +36,6 @@ def _check_format(packed, k, in_features, out_features, sharded_side):
     return nbytes // size
 
 
-def _require_k4(k):
-    if k != 4:
-        raise NotImplementedError("the trellis GEMVs of this build are K4; K2/K3 weights decode "
-                                  "(decode_inner, dequantize_trellis) but have no fused linear")
 
 
 def decode_inner(packed, k, in_features, out_features, sharded_side=1, expert=0):
@@ -99,7 +95,6 @@ def expert_linear(x, indices, packed, in_scale, out_scale, k, in_features, out_f
     ``x`` is bf16 with one row per token ([..., in]) or per expert slot ([..., slots, in]).
     """
     experts = _check_format(packed, k, in_features, out_features, sharded_side)
-    _require_k4(k)
     per_slot = _rows_for(x, indices, in_features)
     if tuple(in_scale.shape) != (experts, in_features) or tuple(out_scale.shape) != (experts, out_features):
         raise ValueError("expert side vectors must contain full signed channel scales")
@@ -111,6 +106,17 @@ def expert_linear(x, indices, packed, in_scale, out_scale, k, in_features, out_f
     rows = ids.shape[0]
     xr = x.reshape(-1, in_features).contiguous()
     y = torch.empty((rows * slots, out_features), dtype=BF16, device=x.device)
+    if k != 4:
+        # K2/K3: the generic-window grouped trellis kernel (all rows in one call)
+        if sharded_side not in (1, 2):
+            raise ValueError("K2/K3 expert linears take side 1 or 2 storage")
+        need = lib().moe_trellis_grouped_linear_workspace_bytes(rows, slots, in_features, out_features, experts)
+        ws = torch.empty(need, dtype=torch.uint8, device=x.device)
+        check(lib().moe_trellis_grouped_linear(k, ptr(xr), int(per_slot), ptr(ids), rows, slots, ptr(packed),
+                                               _nbytes(packed), ptr(in_scale), ptr(out_scale), in_features,
+                                               out_features, sharded_side, ptr(y), ptr(ws), ws.numel(),
+                                               stream(x.device)))
+        return y.reshape(*indices.shape, out_features)
     ws = workspace(x.device, max(in_features, out_features), max(in_features, out_features))
     step = max(1, 72 // slots)
     st = stream(x.device)

@@ -43,6 +43,7 @@ class _Oracle:
             "orc_mx_quantize_row": (None, [vp, i32, vp, vp]),
             "orc_k4_to_mxfp4": (None, [vp, i32, i32, i32, i64, vp, vp, vp, vp, i32, i32]),
             "orc_k4_moe": (None, [vp, vp, vp, vp, i32, i32, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]),
+            "orc_trellis_moe": (None, [i32, vp, vp, vp, vp, i32, i32, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]),
             "orc_mxfp4_moe": (None, [vp, vp, vp, vp, i32, i32, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]),
             "orc_residual_rmsnorm": (None, [vp, vp, vp, i32, i32, f32, vp, vp]),
             "orc_segment_table": (i32, [vp, i32, i32, i32, vp, vp, vp, vp, vp, vp]),
@@ -133,15 +134,16 @@ class _Oracle:
                                None if ins is None else _p(ins), None if un is None else _p(un),
                                _p(codes), _p(scales), codes.shape[1], row_offset)
 
-    def k4_moe(self, x, idx9, scores8, residual, h, m, pg, pu, pd, in_g, out_g, in_u, out_u, in_d, out_d, want_values=False):
+    def k4_moe(self, x, idx9, scores8, residual, h, m, pg, pu, pd, in_g, out_g, in_u, out_u, in_d, out_d, want_values=False,
+               k=4):
         x = np.ascontiguousarray(x, np.uint16).reshape(-1, h)
         rows = x.shape[0]
         out = np.empty((rows, h), np.uint16)
         values = np.empty((rows, 9, h), np.uint16) if want_values else None
         c = lambda a, t: np.ascontiguousarray(a, t)
-        self.h.orc_k4_moe(_p(x), _p(c(idx9, np.uint32)), _p(c(scores8, np.float32)), _p(c(residual, np.uint16)), rows, h, m,
-                          _p(c(pg, np.uint8)), _p(c(pu, np.uint8)), _p(c(pd, np.uint8)),
-                          *[_p(c(a, np.uint16)) for a in (in_g, out_g, in_u, out_u, in_d, out_d)], _p(out), _p(values))
+        self.h.orc_trellis_moe(k, _p(x), _p(c(idx9, np.uint32)), _p(c(scores8, np.float32)), _p(c(residual, np.uint16)),
+                               rows, h, m, _p(c(pg, np.uint8)), _p(c(pu, np.uint8)), _p(c(pd, np.uint8)),
+                               *[_p(c(a, np.uint16)) for a in (in_g, out_g, in_u, out_u, in_d, out_d)], _p(out), _p(values))
         return (out, values) if want_values else out
 
     def mxfp4_moe(self, x, idx9, scores8, residual, h, m, gu_codes, gu_scales, d_codes, d_scales, unit, out_g, out_u, in_d, out_d,

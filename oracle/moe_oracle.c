@@ -415,13 +415,14 @@ static void combine_row(const float* y9 /* [9][h], bf16-valued */, const float* 
   }
 }
 
-/* ---------------- full K4 MoE layer (A.5 cast points) ----------------
-   x [rows, h] bf16, idx9 [rows, 9], scores8 [rows, 8], residual [rows, h] bf16 -> out [rows, h] bf16.
-   values (optional) receives the per-slot expert outputs [rows, 9, h] as bf16. */
-void orc_k4_moe(const uint16_t* x, const uint32_t* idx9, const float* scores8, const uint16_t* residual, int rows,
-                int h, int m, const uint8_t* pg, const uint8_t* pu, const uint8_t* pd,
-                const uint16_t* in_g, const uint16_t* out_g, const uint16_t* in_u, const uint16_t* out_u,
-                const uint16_t* in_d, const uint16_t* out_d, uint16_t* out, uint16_t* values) {
+/* ---------------- full trellis MoE layer (A.5 cast points) ----------------
+   k-bit experts (k = 2..4); x [rows, h] bf16, idx9 [rows, 9], scores8 [rows, 8], residual [rows, h]
+   bf16 -> out [rows, h] bf16.  values (optional) receives the per-slot expert outputs [rows, 9, h]
+   as bf16.  exlr8/experts.py:150-188 (reference chain) + exlr8/model.py:415-418. */
+void orc_trellis_moe(int k, const uint16_t* x, const uint32_t* idx9, const float* scores8, const uint16_t* residual,
+                     int rows, int h, int m, const uint8_t* pg, const uint8_t* pu, const uint8_t* pd,
+                     const uint16_t* in_g, const uint16_t* out_g, const uint16_t* in_u, const uint16_t* out_u,
+                     const uint16_t* in_d, const uint16_t* out_d, uint16_t* out, uint16_t* values) {
   ensure_codebook();
   int slots = rows * 9;
   float* y = (float*)malloc((size_t)slots * h * sizeof(float));
@@ -434,10 +435,10 @@ void orc_k4_moe(const uint16_t* x, const uint32_t* idx9, const float* scores8, c
     float* g = (float*)malloc((size_t)m * sizeof(float));
     float* u = (float*)malloc((size_t)m * sizeof(float));
     for (int i = 0; i < h; i++) xf[i] = bf16_to_f32(x[(int64_t)r * h + i]);
-    k4_linear_one(xf, pg, 4, h, m, 1, e, in_g, out_g, g, tmp);
-    k4_linear_one(xf, pu, 4, h, m, 1, e, in_u, out_u, u, tmp);
+    k4_linear_one(xf, pg, k, h, m, 1, e, in_g, out_g, g, tmp);
+    k4_linear_one(xf, pu, k, h, m, 1, e, in_u, out_u, u, tmp);
     for (int i = 0; i < m; i++) g[i] = orc_swiglu_bf16(g[i], u[i]);
-    k4_linear_one(g, pd, 4, m, h, 2, e, in_d, out_d, y + (int64_t)s * h, tmp);
+    k4_linear_one(g, pd, k, m, h, 2, e, in_d, out_d, y + (int64_t)s * h, tmp);
     for (int i = 0; i < h; i++) y[(int64_t)s * h + i] = round_bf16(y[(int64_t)s * h + i]);
     free(xf); free(tmp); free(g); free(u);
   }
@@ -446,6 +447,14 @@ void orc_k4_moe(const uint16_t* x, const uint32_t* idx9, const float* scores8, c
   for (int r = 0; r < rows; r++)
     combine_row(y + (int64_t)r * 9 * h, scores8 + (int64_t)r * 8, residual + (int64_t)r * h, h, out + (int64_t)r * h);
   free(y);
+}
+
+void orc_k4_moe(const uint16_t* x, const uint32_t* idx9, const float* scores8, const uint16_t* residual, int rows,
+                int h, int m, const uint8_t* pg, const uint8_t* pu, const uint8_t* pd,
+                const uint16_t* in_g, const uint16_t* out_g, const uint16_t* in_u, const uint16_t* out_u,
+                const uint16_t* in_d, const uint16_t* out_d, uint16_t* out, uint16_t* values) {
+  orc_trellis_moe(4, x, idx9, scores8, residual, rows, h, m, pg, pu, pd, in_g, out_g, in_u, out_u, in_d, out_d, out,
+                  values);
 }
 
 /* ---------------- joined MXFP4 MoE layer (joined_mxfp4.py:90-165) ----------------

@@ -96,3 +96,29 @@ def test_encode_and_grouped_argument_errors_without_device():
     assert L.moe_k4_grouped_mlp(*args, 128, 128, p, p, 16, None) == -3
     assert b"workspace" in L.moe_last_error()
     assert L.moe_k4_grouped_mlp_workspace_bytes(512, 9, 6144, 2048, 257) > 0
+
+
+def test_trellis_grouped_and_combine_argument_errors_without_device():
+    from mlxlr8_amd._lib import lib
+    L = lib()
+    p = ctypes.c_void_p(256)
+    k3 = 128 * 128 * 3 // 8
+    args = [p, p, 4, 9, p, p, p, k3] + [p] * 6
+    assert L.moe_trellis_grouped_mlp(5, *args, 128, 128, p, p, 1 << 30, None) == -1
+    assert b"2, 3, or 4" in L.moe_last_error()
+    # K4 byte count is not a whole number of K3 experts
+    assert L.moe_trellis_grouped_mlp(3, *args[:7], 128 * 128 // 2, *args[8:], 128, 128, p, p, 1 << 30, None) == -1
+    assert b"K3 experts" in L.moe_last_error()
+    assert L.moe_trellis_grouped_mlp(3, *args, 128, 128, p, p, 16, None) == -3
+    lin = [p, 0, p, 4, 9, p, k3, p, p]
+    assert L.moe_trellis_grouped_linear(3, *lin, 128, 128, 3, p, p, 1 << 30, None) == -1
+    assert b"sharded_side" in L.moe_last_error()
+    assert L.moe_trellis_grouped_linear(3, *lin, 128, 100, 1, p, p, 1 << 30, None) == -1
+    assert b"multiples of 128" in L.moe_last_error()
+    assert L.moe_trellis_grouped_linear(3, *lin, 128, 128, 1, p, p, 16, None) == -3
+    need = L.moe_trellis_grouped_linear_workspace_bytes(4, 9, 6144, 2048, 257)
+    assert 0 < need < L.moe_k4_grouped_mlp_workspace_bytes(4, 9, 6144, 2048, 257)
+    assert L.moe_combine_values(p, p, p, 0, 128, p, None) == -1
+    assert b"rows" in L.moe_last_error()
+    assert L.moe_combine_values(ctypes.c_void_p(258), p, p, 1, 128, p, None) == -1
+    assert b"aligned" in L.moe_last_error()

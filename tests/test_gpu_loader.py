@@ -47,3 +47,30 @@ def test_store_layer_resident_bytes_and_forward(cuda, orc, tmp_path, rows):
     err = rel_l2(bits_to_f32(bf16_bits(values)), bits_to_f32(want))
     say(f"  rel_l2={err:.3e}")
     assert err <= 1e-3
+
+
+@pytest.mark.parametrize("rows", [2, 20])
+def test_store_k3_layer_forward(cuda, orc, tmp_path, rows):
+    """Layer 78 (K3): resident trellis experts (no MXFP4 conversion), values against the oracle."""
+    from mlxlr8_amd.experts import ExpertStore
+    say(f"case: store K3 layer 78 rows={rows}")
+    write_checkpoint(tmp_path, layer=78, widths=3, width=3)
+    store = ExpertStore(tmp_path, resident=True, optimize=True)
+    layer = store.layer(78)
+    assert layer.k == 3 and layer.affine is None
+    assert store.stats()["resident_bytes"] == 3 * 257 * (6144 + 2 * 128 * 2)
+    rng = np.random.default_rng(40 + rows)
+    ids_np = rng.integers(0, 257, (rows, 9)).astype(np.int32)
+    ids_np[:, 8] = 256
+    x = torch.from_numpy(rng.normal(size=(rows, 128)).astype(np.float32)).to(cuda).to(torch.bfloat16)
+    values = layer(x, torch.from_numpy(ids_np).to(cuda))
+    torch.cuda.synchronize()
+    sc = {p: tuple(f16_bits(v) for v in layer.scales[p]) for p in ("gate", "up", "down")}
+    host = {p: layer.packed[p].cpu().numpy() for p in ("gate", "up", "down")}
+    _, want = orc.k4_moe(bf16_bits(x), ids_np.astype(np.uint32), np.zeros((rows, 8), np.float32),
+                         np.zeros((rows, 128), np.uint16), 128, 128, host["gate"], host["up"], host["down"],
+                         sc["gate"][0], sc["gate"][1], sc["up"][0], sc["up"][1], sc["down"][0], sc["down"][1],
+                         want_values=True, k=3)
+    err = rel_l2(bits_to_f32(bf16_bits(values)), bits_to_f32(want))
+    say(f"  rel_l2={err:.3e}")
+    assert err <= 1e-3

@@ -66,3 +66,20 @@ def test_manifest_and_width_errors(tmp_path):
     m.write_text(json.dumps(data))
     with pytest.raises(ValueError, match="up1 manifest"):
         layer_arrays(tmp_path, 5)
+
+
+def test_k3_layer_78(tmp_path):
+    """Layer 78 is the K3 layer: its k3 file and k3 side vectors load with k = 3."""
+    from mlxlr8_amd.experts import layer_arrays
+    raw, index = write_checkpoint(tmp_path, layer=78, widths=3, width=3)
+    k, hidden, inter, packed, scales = layer_arrays(tmp_path, 78)
+    assert (k, hidden, inter) == (3, 128, 128)
+    for projection in ("gate", "up", "down"):
+        assert packed[projection].size == 257 * 128 * 128 * 3 // 8
+        np.testing.assert_array_equal(packed[projection][:256 * 6144], raw["trellis." + projection])
+    np.testing.assert_array_equal(scales["gate"][1][:256], index["k3.gate.svh"])
+    np.testing.assert_array_equal(scales["down"][0][256], index["shared.k3.down.suh"][0])
+    # a K4 manifest row at layer 78 is rejected
+    write_checkpoint(tmp_path, layer=78, widths=4, width=4)
+    with pytest.raises(ValueError, match="not uniform K3"):
+        layer_arrays(tmp_path, 78)

@@ -1,6 +1,7 @@
 """Pin the oracle's linear algebra (trellis linear, MXFP4 linear, full MoE layer) against dense
 numpy matrices built independently from per-tile symbols (no GPU)."""
 import numpy as np
+import pytest
 
 import refmath
 from conftest import bits_to_f32
@@ -12,10 +13,10 @@ def _bf16(x):
     return bits_to_f32(u.astype(np.uint32))
 
 
-def _k4_matrix(rng, experts, in_f, out_f, side):
-    nibs = [rng.integers(0, 16, (in_f // 16, out_f // 16, 256), dtype=np.uint32) for _ in range(experts)]
-    packed = np.concatenate([refmath.build_trellis_matrix(n, side) for n in nibs])
-    return packed, [refmath.expected_inner(n) for n in nibs]
+def _k4_matrix(rng, experts, in_f, out_f, side, k=4):
+    nibs = [rng.integers(0, 1 << k, (in_f // 16, out_f // 16, 256), dtype=np.uint32) for _ in range(experts)]
+    packed = np.concatenate([refmath.build_trellis_matrix(n, side, k) for n in nibs])
+    return packed, [refmath.expected_inner(n, k) for n in nibs]
 
 
 def test_k4_linear_matches_dense_public_matrix(orc):
@@ -56,12 +57,14 @@ def test_mxfp4_linear_matches_dequantised_matrix(orc):
     assert orc.h.orc_f32_to_bf16(1.0) == 0x3F80
 
 
-def test_k4_moe_layer_matches_dense_composition(orc):
-    rng = np.random.default_rng(181)
+@pytest.mark.parametrize("k", [4, 3, 2])
+def test_k4_moe_layer_matches_dense_composition(orc, k):
+    """The oracle's MoE layer (K4, and the K3/K2 experts of the same chain) against dense maths."""
+    rng = np.random.default_rng(181 + k)
     h, m, E = 256, 128, 3
-    pg, ig = _k4_matrix(rng, E, h, m, 1)
-    pu, iu = _k4_matrix(rng, E, h, m, 1)
-    pd, idd = _k4_matrix(rng, E, m, h, 2)
+    pg, ig = _k4_matrix(rng, E, h, m, 1, k)
+    pu, iu = _k4_matrix(rng, E, h, m, 1, k)
+    pd, idd = _k4_matrix(rng, E, m, h, 2, k)
     sc = {k: rng.uniform(-.3, .3, shape).astype(np.float16) for k, shape in
           (("in_g", (E, h)), ("out_g", (E, m)), ("in_u", (E, h)), ("out_u", (E, m)), ("in_d", (E, m)), ("out_d", (E, h)))}
     rows = 2
@@ -71,8 +74,8 @@ def test_k4_moe_layer_matches_dense_composition(orc):
     scores = rng.uniform(.03, .4, (rows, 8)).astype(np.float32)
     bits = lambda a: (a.view(np.uint32) >> 16).astype(np.uint16)
     out, values = orc.k4_moe(bits(x), idx, scores, bits(res), h, m, pg, pu, pd,
-                             *[sc[k].view(np.uint16) for k in ("in_g", "out_g", "in_u", "out_u", "in_d", "out_d")],
-                             want_values=True)
+                             *[sc[n].view(np.uint16) for n in ("in_g", "out_g", "in_u", "out_u", "in_d", "out_d")],
+                             want_values=True, k=k)
 
     def lin(v, inner, s_in, s_out):
         return refmath.block_hadamard(refmath.block_hadamard(v * s_in.astype(np.float64)) @ inner.astype(np.float64)) \
