@@ -34,6 +34,7 @@
 namespace moe {
 
 __device__ uint8_t g_codebook_e4m3[65536];
+__device__ uint16_t g_codebook_f16[65536];
 
 // ============================================================== codebook
 
@@ -44,6 +45,10 @@ __global__ void build_codebook_kernel() {
   const uint32_t bytes = decode_pair_fp8(a, b);
   g_codebook_e4m3[a] = (uint8_t)(bytes & 0xFFu);
   g_codebook_e4m3[b] = (uint8_t)(bytes >> 8);
+  // widened one byte at a time (exact): element extraction from the packed fp8 -> f16 conversion
+  // has been compiled into a store of the first element twice
+  g_codebook_f16[a] = __builtin_bit_cast(uint16_t, (_Float16)fp8_to_f32(bytes & 0xFFu));
+  g_codebook_f16[b] = __builtin_bit_cast(uint16_t, (_Float16)fp8_to_f32((bytes >> 8) & 0xFFu));
 }
 
 __global__ void copy_codebook_kernel(uint8_t* dst) {
@@ -75,7 +80,7 @@ __global__ __launch_bounds__(128) void plan_kernel(const uint32_t* __restrict__ 
 // device code as the GEMVs: thread = one 16 B piece (4 consecutive words of a tile), words
 // decoded in pairs by decode_pair_words_f16.  Each block uses one of four arithmetic/table mixes,
 // so a full decode exercises every route of the GEMV decoder.
-template <int NE, int NO>
+template <int NE, int NO, bool T16 = false>
 __device__ __forceinline__ void decode_piece_to_inner(const uint32_t* __restrict__ tw, int qg, const uint8_t* tab,
                                                       uint16_t* __restrict__ inner, int out_f, uint32_t row0,
                                                       uint32_t col0) {
@@ -85,9 +90,9 @@ __device__ __forceinline__ void decode_piece_to_inner(const uint32_t* __restrict
   for (int h = 0; h < 2; h++) {
     f16x2 q[2][4];
     if (h == 0)
-      decode_pair_words_f16<NE, NO>(v.x, v.y, prior, tab, q);
+      decode_pair_words_f16<NE, NO, T16>(v.x, v.y, prior, tab, q);
     else
-      decode_pair_words_f16<NE, NO>(v.z, v.w, v.y, tab, q);
+      decode_pair_words_f16<NE, NO, T16>(v.z, v.w, v.y, tab, q);
 #pragma unroll
     for (int i = 0; i < 2; i++)
 #pragma unroll
@@ -101,10 +106,17 @@ __device__ __forceinline__ void decode_piece_to_inner(const uint32_t* __restrict
   }
 }
 
+// T16: the blocks with odd index, decoded through the fp16 table (the even blocks, with T16 false,
+// through the E4M3 byte table); the launch of the other kind leaves a block alone.
+template <bool T16>
 __global__ __launch_bounds__(1024) void trellis_decode_kernel(const uint32_t* __restrict__ packed, int in_f, int out_f,
                                                               int side, int64_t expert, uint16_t* __restrict__ inner) {
-  __shared__ __attribute__((aligned(16))) uint8_t tab[65536];
-  load_codebook_lds(tab);
+  if ((int)(blockIdx.x & 1) != (int)T16) return;
+  __shared__ __attribute__((aligned(16))) uint8_t tab[T16 ? 131072 : 65536];
+  if (T16)
+    load_codebook16_lds<1024>(tab);
+  else
+    load_codebook_lds_t<1024>(tab);
   __syncthreads();
   const int64_t pieces = (int64_t)in_f * out_f / 32;  // 8 pieces per 256-weight tile
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -118,11 +130,11 @@ __global__ __launch_bounds__(1024) void trellis_decode_kernel(const uint32_t* __
   const uint64_t tile = side == 2 ? ((((e * (it / 8u) + tk / 8u) * (ot / 8u) + tn / 8u) * 8u + tk % 8u) * 8u + tn % 8u)
                                   : (((e * (ot / 8u) + tn / 8u) * it + tk) * 8u + tn % 8u);
   const uint32_t* tw = packed + tile * 32u;
-  switch (blockIdx.x & 3) {
-    case 0: decode_piece_to_inner<0, 0>(tw, qg, tab, inner, out_f, 16u * tk, 16u * tn); break;
-    case 1: decode_piece_to_inner<1, 2>(tw, qg, tab, inner, out_f, 16u * tk, 16u * tn); break;
-    case 2: decode_piece_to_inner<2, 2>(tw, qg, tab, inner, out_f, 16u * tk, 16u * tn); break;
-    default: decode_piece_to_inner<4, 4>(tw, qg, tab, inner, out_f, 16u * tk, 16u * tn); break;
+  switch ((blockIdx.x >> 1) & 3) {
+    case 0: decode_piece_to_inner<0, 0, T16>(tw, qg, tab, inner, out_f, 16u * tk, 16u * tn); break;
+    case 1: decode_piece_to_inner<1, 2, T16>(tw, qg, tab, inner, out_f, 16u * tk, 16u * tn); break;
+    case 2: decode_piece_to_inner<2, 2, T16>(tw, qg, tab, inner, out_f, 16u * tk, 16u * tn); break;
+    default: decode_piece_to_inner<4, 4, T16>(tw, qg, tab, inner, out_f, 16u * tk, 16u * tn); break;
   }
 }
 
@@ -427,26 +439,38 @@ __device__ __forceinline__ void complete_visit(const GemvArgs& a, const Plan* __
 // The kernel body takes its LDS regions as distinct restrict pointers (table, the wave's A
 // fragments), so the compiler knows they never alias.
 template <int IM, int FM, int NT, int ALU_EVEN, int ALU_ODD, int WV>
-__device__ __forceinline__ void k4_mfma_body(const GemvArgs& a, const uint8_t* __restrict__ tab,
-                                             _Float16* __restrict__ xw);
+__device__ __forceinline__ void k4_mfma_body(const GemvArgs& a, const Plan* __restrict__ P,
+                                             const uint8_t* __restrict__ tab, _Float16* __restrict__ xw);
+
+// Single-token units keep the code table as fp16 in LDS (128 KB; the lookups then need no fp8
+// widening); batched units, whose A fragments need more LDS, keep the 64 KB E4M3 byte table.
+template <int NT>
+struct TableKind {
+  static constexpr bool kF16 = NT == 1;
+  static constexpr int kBytes = kF16 ? 131072 : 65536;
+};
 
 template <int IM, int FM, int NT, int ALU_EVEN, int ALU_ODD, int WV>
 __global__ __launch_bounds__(WV * 64) void k4_mfma_kernel(GemvArgs a) {
-  __shared__ __attribute__((aligned(16))) uint8_t tab[65536];
+  __shared__ __attribute__((aligned(16))) uint8_t tab[TableKind<NT>::kBytes];
   // per wave: A fragments for the two quads of the current 128-row block [Qb][rh][m][g][8]
   __shared__ __attribute__((aligned(16))) _Float16 xa[WV * 2 * 2 * (2 * NT) * 4 * 8];
 
-  load_codebook_lds(tab);
+  if (TableKind<NT>::kF16)
+    load_codebook16_lds<WV * 64>(tab);
+  else
+    load_codebook_lds_t<WV * 64>(tab);
   __syncthreads();
   const int wv = wave_id_uniform();
-  k4_mfma_body<IM, FM, NT, ALU_EVEN, ALU_ODD, WV>(a, tab, xa + wv * (2 * 2 * (2 * NT) * 4 * 8));
+  k4_mfma_body<IM, FM, NT, ALU_EVEN, ALU_ODD, WV>(a, a.plan, tab, xa + wv * (2 * 2 * (2 * NT) * 4 * 8));
 }
 
 template <int IM, int FM, int NT, int ALU_EVEN, int ALU_ODD, int WV>
-__device__ __forceinline__ void k4_mfma_body(const GemvArgs& a, const uint8_t* __restrict__ tab,
-                                             _Float16* __restrict__ xw) {
-  const Plan* __restrict__ P = a.plan;
-  const int U = P->units;
+__device__ __forceinline__ void k4_mfma_body(const GemvArgs& a, const Plan* __restrict__ P,
+                                             const uint8_t* __restrict__ tab, _Float16* __restrict__ xw) {
+  // plan fields are read as wave-uniform values (the plan may sit in LDS), so the work split and
+  // the loop bounds stay scalar
+  const int U = uniform(P->units);
   const int it = a.in_f / 16;
   const int ups = it / 4;  // quads per segment
   const int obs = a.out_f / 128;
@@ -473,8 +497,8 @@ __device__ __forceinline__ void k4_mfma_body(const GemvArgs& a, const uint8_t* _
     const int proj = seg % nproj;
     const int ob = (seg / nproj) % obs;
     const int u = seg / (nproj * obs);
-    const int e = P->expert[u];
-    const int ntok = P->ntok[u];
+    const int e = uniform(P->expert[u]);
+    const int ntok = uniform(P->ntok[u]);
     const uint8_t* __restrict__ base = a.packed[proj];
 
     f32x4 acc[4][2];
@@ -600,9 +624,9 @@ __device__ __forceinline__ void k4_mfma_body(const GemvArgs& a, const uint8_t* _
           // words 2rh, 2rh+1 = rows of row half rh; h = 0: slots (0,1),(2,3) ; h = 1: slots (4,5),(6,7)
           f16x2 q[2][4];  // [word][pair]: (c0,c1), (c2,c3), (c4,c5), (c6,c7)
           if (rh == 0)
-            decode_pair_words_f16<ALU_EVEN, ALU_ODD>(v.x, v.y, prior[s4], tab, q);
+            decode_pair_words_f16<ALU_EVEN, ALU_ODD, TableKind<NT>::kF16>(v.x, v.y, prior[s4], tab, q);
           else
-            decode_pair_words_f16<ALU_EVEN, ALU_ODD>(v.z, v.w, v.y, tab, q);
+            decode_pair_words_f16<ALU_EVEN, ALU_ODD, TableKind<NT>::kF16>(v.z, v.w, v.y, tab, q);
           if (rh == 1) pc[s4] = *reinterpret_cast<const u32x4*>(np + 256 * s4);
           const f16x8 b0 = frag(q[0][0], q[0][1], q[1][0], q[1][1]);
           const f16x8 b1 = frag(q[0][2], q[0][3], q[1][2], q[1][3]);
@@ -752,8 +776,10 @@ int launch_gemv(const GemvArgs& a, int max_ntok, int max_units, hipStream_t stre
     return fail(MOE_ENOTSUP, "too many (unit, column block) segments: %lld > %d", (long long)nseg_max, kMaxWaves);
   {
     const int WV = max_ntok <= 1 ? MOE_K4_WAVES_1 : MOE_K4_WAVES_8;
-    // 16 waves per CU (4 per SIMD: the decode's VALU results arrive 16 clocks after issue)
-    int mblocks = grid_blocks() * (WV < 16 ? 16 / WV : 1);
+    // 16 waves per CU (4 per SIMD: the decode's VALU results arrive 16 clocks after issue) when
+    // two blocks fit a CU; a block with the 128 KB fp16 table has a CU to itself
+    const bool f16_table = max_ntok <= 1 ? TableKind<1>::kF16 : TableKind<kMaxRows>::kF16;
+    int mblocks = grid_blocks() * (WV < 16 && !f16_table ? 16 / WV : 1);
     // at least one wave per segment, so no wave's range spans more than two segments
     const int mneed = (int)((nseg_max + WV - 1) / WV);
     if (mblocks < mneed) mblocks = mneed;
@@ -833,8 +859,12 @@ int moe_trellis_decode_f16(const void* packed, int64_t packed_bytes, int k, int 
     return MOE_OK;
   }
   const int64_t pieces = (int64_t)in_f * out_f / 32;
-  hipLaunchKernelGGL(trellis_decode_kernel, dim3((unsigned)((pieces + 1023) / 1024)), dim3(1024), 0,
-                     (hipStream_t)stream, (const uint32_t*)packed, in_f, out_f, side, expert, inner);
+  const dim3 grid((unsigned)((pieces + 1023) / 1024));
+  hipLaunchKernelGGL(trellis_decode_kernel<false>, grid, dim3(1024), 0, (hipStream_t)stream,
+                     (const uint32_t*)packed, in_f, out_f, side, expert, inner);
+  if (grid.x > 1)
+    hipLaunchKernelGGL(trellis_decode_kernel<true>, grid, dim3(1024), 0, (hipStream_t)stream,
+                       (const uint32_t*)packed, in_f, out_f, side, expert, inner);
   MOE_HIP(hipGetLastError());
   return MOE_OK;
 }

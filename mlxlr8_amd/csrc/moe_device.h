@@ -64,15 +64,52 @@ __device__ __forceinline__ float fp8_to_f32(uint32_t byte) { return __builtin_am
 // The E4M3 code table for all 65536 states (64 KB).  Filled once per device by
 // moe_build_codebook_kernel; copied into LDS by the decode GEMVs.
 extern __device__ uint8_t g_codebook_e4m3[65536];
+// The same table as fp16 values (128 KB), for decoders that keep it in LDS as fp16.
+extern __device__ uint16_t g_codebook_f16[65536];
 
 // Cooperative copy of the 64 KB table into LDS (blockDim threads, 16 B each), from the table of
 // this translation unit or, in other ones, from its device address (codebook_device_table()).
-__device__ __forceinline__ void load_codebook_lds(uint8_t* lds, const uint8_t* table) {
+// Copy of a table into LDS by THREADS threads (the block size): each thread issues its loads in
+// batches of 8 x 16 B before storing them (one memory round trip per batch, 32 VGPRs).
+template <int BYTES, int THREADS>
+__device__ __forceinline__ void copy_table_lds(uint8_t* lds, const void* table) {
   const u32x4* src = reinterpret_cast<const u32x4*>(table);
   u32x4* dst = reinterpret_cast<u32x4*>(lds);
-  for (int i = threadIdx.x; i < 65536 / 16; i += blockDim.x) dst[i] = src[i];
+  constexpr int n = BYTES / 16;
+  constexpr int per = (n + THREADS - 1) / THREADS;
+  const int t = (int)threadIdx.x;
+#pragma unroll
+  for (int b = 0; b < per; b += 8) {
+    u32x4 v[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const int i = (b + j) * THREADS + t;
+      if (b + j < per && i < n) v[j] = src[i];
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const int i = (b + j) * THREADS + t;
+      if (b + j < per && i < n) dst[i] = v[j];
+    }
+  }
+}
+// Any block size (one 16 B load and store at a time).
+template <int BYTES>
+__device__ __forceinline__ void copy_table_lds_any(uint8_t* lds, const void* table) {
+  const u32x4* src = reinterpret_cast<const u32x4*>(table);
+  u32x4* dst = reinterpret_cast<u32x4*>(lds);
+  for (int i = threadIdx.x; i < BYTES / 16; i += blockDim.x) dst[i] = src[i];
+}
+__device__ __forceinline__ void load_codebook_lds(uint8_t* lds, const uint8_t* table) {
+  copy_table_lds_any<65536>(lds, table);
 }
 __device__ __forceinline__ void load_codebook_lds(uint8_t* lds) { load_codebook_lds(lds, g_codebook_e4m3); }
+template <int THREADS>
+__device__ __forceinline__ void load_codebook_lds_t(uint8_t* lds) { copy_table_lds<65536, THREADS>(lds, g_codebook_e4m3); }
+template <int THREADS>
+__device__ __forceinline__ void load_codebook16_lds(uint8_t* lds) {
+  copy_table_lds<131072, THREADS>(lds, g_codebook_f16);
+}
 
 // ---------------------------------------------------------------- K4 word layout
 // Word w of a tile with its circular predecessor p holds 8 codewords (A.1 direct form):
@@ -225,7 +262,22 @@ __device__ __forceinline__ void add_halves_hi(uint32_t& s, uint32_t m) {
                : "v"(m));
 }
 
-template <int NE, int NO>
+// fp16 code table (128 KB of LDS, entry s at byte 2s): the byte offset of the codeword in half H of r
+// is one SDWA shift, and two lookups meet in one register with a byte permute -- no fp8 widening.
+template <int H>
+__device__ __forceinline__ uint32_t tab16_off(uint32_t r) {
+  uint32_t o;
+  asm("v_lshlrev_b32_sdwa %0, 1, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:WORD_%2"
+      : "=v"(o)
+      : "v"(r), "n"(H));
+  return o;
+}
+__device__ __forceinline__ uint16_t tab16_at(const uint8_t* tab, uint32_t off) {
+  return *reinterpret_cast<const uint16_t*>(tab + off);
+}
+
+// TAB16: `tab` is the fp16 table (else the 64 KB E4M3 byte table).
+template <int NE, int NO, bool TAB16 = false>
 __device__ __forceinline__ void decode_pair_words_f16(uint32_t w0, uint32_t w1, uint32_t prior0, const uint8_t* tab,
                                                       f16x2 (&q)[2][4]) {
   using piece_detail::kOut;
@@ -251,8 +303,13 @@ __device__ __forceinline__ void decode_pair_words_f16(uint32_t w0, uint32_t w1, 
 #pragma unroll
     for (int i = 0; i < 2; i++)
       if (k >= nalu(i)) {
-        bx[i][k] = tab[(k & 1) ? (xr(i, k) >> 16) : (xr(i, k) & 0xFFFFu)];
-        by[i][k] = tab[(k & 1) ? (yr(i, k) >> 16) : (yr(i, k) & 0xFFFFu)];
+        if (TAB16) {
+          bx[i][k] = tab16_at(tab, (k & 1) ? tab16_off<1>(xr(i, k)) : tab16_off<0>(xr(i, k)));
+          by[i][k] = tab16_at(tab, (k & 1) ? tab16_off<1>(yr(i, k)) : tab16_off<0>(yr(i, k)));
+        } else {
+          bx[i][k] = tab[(k & 1) ? (xr(i, k) >> 16) : (xr(i, k) & 0xFFFFu)];
+          by[i][k] = tab[(k & 1) ? (yr(i, k) >> 16) : (yr(i, k) & 0xFFFFu)];
+        }
       }
   __builtin_amdgcn_sched_barrier(0);
 
@@ -323,6 +380,15 @@ __device__ __forceinline__ void decode_pair_words_f16(uint32_t w0, uint32_t w1, 
 
   __builtin_amdgcn_sched_barrier(0);
 
+  // ---- table route, fp16 entries: one permute per pair
+  if (TAB16) {
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+#pragma unroll
+      for (int i = 0; i < 2; i++)
+        if (k >= nalu(i)) q[i][kOut[k]] = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(by[i][k], bx[i][k], 0x05040100u));
+    return;
+  }
   // ---- table route: [b_x, 0, b_y, 0] per pair, two pairs joined per permute, widened to fp16
   {
     uint32_t lb[2][4];

@@ -32,21 +32,48 @@ __device__ __forceinline__ uint32_t float_key(float f) {
 // "top 8 by descending choice, ties to the lower id" is exactly "the 8 largest keys".  Each of
 // the 40 bisection steps counts candidates with wave ballots (no LDS round trip); the 8 winners
 // are then ranked against each other and the scores summed in rank order.
+// The row's logits and the bias as lane l holds them (experts l + 64 i), loaded ahead of the
+// selection so a caller can overlap the round trip with other work.
+struct RouteInput {
+  float logit[4], bias[4];
+};
+template <bool COHERENT = false>
+__device__ __forceinline__ RouteInput route_load(const float* __restrict__ logits, const float* __restrict__ bias,
+                                                 int row) {
+  const int lane = lane_id();
+  RouteInput in;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int e = lane + 64 * i;
+    const float* lp = logits + (int64_t)row * 256 + e;
+    in.logit[i] = COHERENT ? __hip_atomic_load(const_cast<float*>(lp), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM)
+                           : *lp;
+    in.bias[i] = bias[e];
+  }
+  return in;
+}
+
+__device__ __forceinline__ void route_select(const RouteInput& in, int row, uint32_t* __restrict__ ids,
+                                             float* __restrict__ scores, int32_t* sid, bool store_global);
+
 template <bool COHERENT = false>
 __device__ __forceinline__ void route_row(const float* __restrict__ logits, const float* __restrict__ bias, int row,
                                           uint32_t* __restrict__ ids, float* __restrict__ scores,
                                           int32_t* sid = nullptr, bool store_global = true) {
+  route_select(route_load<COHERENT>(logits, bias, row), row, ids, scores, sid, store_global);
+}
+
+// Selection of one row from its loaded logits (see route_row).
+__device__ __forceinline__ void route_select(const RouteInput& in, int row, uint32_t* __restrict__ ids,
+                                             float* __restrict__ scores, int32_t* sid, bool store_global) {
   const int lane = lane_id();
   float orig[4];
   uint64_t key[4];
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const int e = lane + 64 * i;
-    const float* lp = logits + (int64_t)row * 256 + e;
-    const float lv = COHERENT ? __hip_atomic_load(const_cast<float*>(lp), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM)
-                              : *lp;
-    orig[i] = router_sigmoid(lv);
-    const float choice = orig[i] + bias[e];
+    orig[i] = router_sigmoid(in.logit[i]);
+    const float choice = orig[i] + in.bias[i];
     key[i] = ((uint64_t)float_key(choice) << 8) | (uint64_t)(255 - e);
   }
   uint64_t thr = 0;
@@ -57,34 +84,40 @@ __device__ __forceinline__ void route_row(const float* __restrict__ logits, cons
     for (int i = 0; i < 4; i++) cnt += __popcll(__ballot(key[i] >= cand));
     if (cnt >= 8) thr = cand;
   }
-  // exactly 8 keys are >= thr; rank each winner among the winners (descending)
-  int rank[4] = {-1, -1, -1, -1};
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    uint64_t m = __ballot(key[i] >= thr);
-    while (m) {
-      const int src = __builtin_ctzll(m);
-      m &= m - 1;
-      const uint64_t other = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(key[i] >> 32), src) << 32) |
-                             (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)key[i], src);
-#pragma unroll
-      for (int j = 0; j < 4; j++)
-        if (key[j] >= thr) rank[j] += (other >= key[j]) ? 1 : 0;
-    }
-  }
-  // rank[j] = (number of winners >= key[j]) - 1: 0 for the largest
+  // exactly 8 keys are >= thr.  The winners are packed into 8 LDS entries (position = winners in
+  // earlier slots and lower lanes); lane l < 8 then ranks entry l against the other seven
+  // (descending, keys are unique) and places its sigmoid score and id at that rank.
+  __shared__ uint64_t wkey_lds[kMaxRows][8];
+  __shared__ float worig_lds[kMaxRows][8];
   __shared__ float sel_lds[kMaxRows][8];
   __shared__ int id_lds[kMaxRows][8];
-  const int wv = wave_id_in_block();
-  (void)wv;
-  float* sel = sel_lds[row & (kMaxRows - 1)];
-  int* idl = id_lds[row & (kMaxRows - 1)];
+  const int rs = row & (kMaxRows - 1);
+  uint64_t* wk = wkey_lds[rs];
+  float* wo = worig_lds[rs];
+  float* sel = sel_lds[rs];
+  int* idl = id_lds[rs];
+  int before = 0;
 #pragma unroll
-  for (int j = 0; j < 4; j++) {
-    if (key[j] >= thr) {
-      sel[rank[j]] = orig[j];
-      idl[rank[j]] = lane + 64 * j;
+  for (int i = 0; i < 4; i++) {
+    const uint64_t m = __ballot(key[i] >= thr);
+    const int pos = before + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                            __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+    if (key[i] >= thr) {
+      wk[pos] = key[i];
+      wo[pos] = orig[i];
     }
+    before += __popcll(m);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if (lane < 8) {
+    const uint64_t mine = wk[lane];
+    int rank = 0;
+#pragma unroll
+    for (int j = 0; j < 8; j++) rank += wk[j] > mine ? 1 : 0;
+    sel[rank] = wo[lane];
+    idl[rank] = 255 - (int)(mine & 0xFFu);
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
