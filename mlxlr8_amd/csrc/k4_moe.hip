@@ -194,6 +194,11 @@ enum FinMode { FIN_GATE = 0, FIN_VALUES = 1, FIN_COMBINE = 2 };
 #define MOE_K4_WAVES_8 8
 #endif
 
+// wave issue priority raised for waves that are behind on their range (measured per build)
+#ifndef MOE_K4_PRIO
+#define MOE_K4_PRIO 1
+#endif
+
 constexpr int kWaves = 16;            // waves per block (one block per CU)
 constexpr int kThreads = kWaves * 64;
 constexpr int kMaxBlocks = 256;
@@ -598,6 +603,17 @@ __device__ __forceinline__ void k4_mfma_body(const GemvArgs& a, const Plan* __re
     load_quad(pc, tq0);
     fetch_block(tq0 >> 1);
     for (int tq = tq0; tq < tq1; tq++) {
+      if (MOE_K4_PRIO) {
+        // issue priority from the wave's remaining share of its range: the SIMD's arbiter favours
+        // older waves, so without this the waves of a SIMD finish one after another
+        const int left = q_end - (c + (tq - tq0));
+        switch (min(3, (4 * left) / (q_end - q_begin + 1))) {
+          case 3: __builtin_amdgcn_s_setprio(3); break;
+          case 2: __builtin_amdgcn_s_setprio(2); break;
+          case 1: __builtin_amdgcn_s_setprio(1); break;
+          default: __builtin_amdgcn_s_setprio(0); break;
+        }
+      }
       if (tq == tq0 || (tq & 1) == 0) {
         stage_block();
         fetch_block(min((tq >> 1) + 1, tl >> 1));

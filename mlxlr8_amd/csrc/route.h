@@ -28,12 +28,8 @@ __device__ __forceinline__ uint32_t float_key(float f) {
 // One wave per row.  Lane l owns experts l, l+64, l+128, l+192.  COHERENT reads logits that
 // other blocks of the same launch wrote (L2-bypassing loads).
 //
-// Selection is a radix select on 40-bit keys (choice key << 8 | 255 - id): keys are unique, so
-// "top 8 by descending choice, ties to the lower id" is exactly "the 8 largest keys".  Each of
-// the 40 bisection steps counts candidates with wave ballots (no LDS round trip); the 8 winners
-// are then ranked against each other and the scores summed in rank order.
-// The row's logits and the bias as lane l holds them (experts l + 64 i), loaded ahead of the
-// selection so a caller can overlap the round trip with other work.
+// The row's logits and the bias as lane l holds them, loaded ahead of the selection so a caller
+// can overlap the round trip with other work.
 struct RouteInput {
   float logit[4], bias[4];
 };
@@ -63,7 +59,11 @@ __device__ __forceinline__ void route_row(const float* __restrict__ logits, cons
   route_select(route_load<COHERENT>(logits, bias, row), row, ids, scores, sid, store_global);
 }
 
-// Selection of one row from its loaded logits (see route_row).
+// Selection of one row from its loaded logits: a radix select on 40-bit keys (choice key << 8 |
+// 255 - id).  Keys are unique, so "top 8 by descending choice, ties to the lower id" is exactly
+// "the 8 largest keys".  Each of the 40 bisection steps counts candidates with wave ballots (no
+// LDS round trip); the 8 winners are then ranked against each other and the scores summed in
+// rank order.
 __device__ __forceinline__ void route_select(const RouteInput& in, int row, uint32_t* __restrict__ ids,
                                              float* __restrict__ scores, int32_t* sid, bool store_global) {
   const int lane = lane_id();
