@@ -136,6 +136,13 @@ __global__ __launch_bounds__(64) void route_kernel(const float* __restrict__ log
   if (row < rows) route_row(logits, bias, row, ids, scores);
 }
 
+// logits per decode-router block: single-row launches use 4 (fewer, larger blocks dispatch
+// faster); the 8-row kernel keeps one (its x rows already fill the registers)
+template <int R>
+struct RouterGroups {
+  static constexpr int value = R == 1 ? 4 : 1;
+};
+
 // Decode batches in one launch: block e computes logit e of every row; the last block to finish
 // routes all rows (one wave per row) and builds the token -> expert dispatch plan.  With a null
 // counter only the logits (and the normalised rows) are produced.
@@ -147,7 +154,7 @@ __global__ __launch_bounds__(64) void route_kernel(const float* __restrict__ log
 // itself); block r also stores row r's h (the layer residual) and normalised input for the
 // expert kernels.  Same arithmetic as moe_residual_rmsnorm.
 template <int R, int KI, bool NORM>
-__global__ __launch_bounds__(256) void router_decode_kernel(const uint16_t* __restrict__ x,
+__global__ __launch_bounds__(256 * RouterGroups<R>::value) void router_decode_kernel(const uint16_t* __restrict__ x,
                                                             const float* __restrict__ w,
                                                             const float* __restrict__ bias, int rows, int hidden,
                                                             int experts, int max_users, float* logits,
@@ -156,7 +163,10 @@ __global__ __launch_bounds__(256) void router_decode_kernel(const uint16_t* __re
                                                             const uint16_t* __restrict__ norm_w, float eps,
                                                             uint16_t* __restrict__ h_out,
                                                             uint16_t* __restrict__ xn_out) {
-  const int e = blockIdx.x;
+  // kRouterGroups groups of 256 threads per block, group gi computing logit e
+  constexpr int kRouterGroups = RouterGroups<R>::value;
+  const int gi = (int)threadIdx.x >> 8, tx = (int)threadIdx.x & 255;
+  const int e = (int)blockIdx.x * kRouterGroups + gi;
   const float* __restrict__ we = w + (int64_t)e * hidden;
   float acc[R];
 #pragma unroll
@@ -171,17 +181,17 @@ __global__ __launch_bounds__(256) void router_decode_kernel(const uint16_t* __re
     f32x4 wv[KI > 0 ? KI : 1];
     u32x2 xv[R][KI > 0 ? KI : 1];
 #pragma unroll
-    for (int i = 0; i < KI; i++) wv[i] = *reinterpret_cast<const f32x4*>(we + threadIdx.x * 4 + i * 1024);
+    for (int i = 0; i < KI; i++) wv[i] = *reinterpret_cast<const f32x4*>(we + tx * 4 + i * 1024);
 #pragma unroll
     for (int r = 0; r < R; r++)
 #pragma unroll
       for (int i = 0; i < KI; i++)
-        if (r < rows) xv[r][i] = *reinterpret_cast<const u32x2*>(x + (int64_t)r * hidden + threadIdx.x * 4 + i * 1024);
+        if (r < rows) xv[r][i] = *reinterpret_cast<const u32x2*>(x + (int64_t)r * hidden + tx * 4 + i * 1024);
     if (NORM) {
-      __shared__ float nred[R][4];
+      __shared__ float nred[kRouterGroups][R][4];
       u32x2 nw[KI > 0 ? KI : 1];
 #pragma unroll
-      for (int i = 0; i < KI; i++) nw[i] = *reinterpret_cast<const u32x2*>(norm_w + threadIdx.x * 4 + i * 1024);
+      for (int i = 0; i < KI; i++) nw[i] = *reinterpret_cast<const u32x2*>(norm_w + tx * 4 + i * 1024);
       auto lo = [](uint32_t v) { return bf16_to_f32((uint16_t)(v & 0xFFFFu)); };
       auto hi = [](uint32_t v) { return bf16_to_f32((uint16_t)(v >> 16)); };
       auto pk = [](float a, float b) { return (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16); };
@@ -193,7 +203,7 @@ __global__ __launch_bounds__(256) void router_decode_kernel(const uint16_t* __re
         for (int i = 0; i < KI; i++)
           if (r < rows) {
             u32x2 av = u32x2{0, 0};
-            if (attn) av = *reinterpret_cast<const u32x2*>(attn + (int64_t)r * hidden + threadIdx.x * 4 + i * 1024);
+            if (attn) av = *reinterpret_cast<const u32x2*>(attn + (int64_t)r * hidden + tx * 4 + i * 1024);
             const float h0 = round_bf16(lo(xv[r][i].x) + lo(av.x)), h1 = round_bf16(hi(xv[r][i].x) + hi(av.x));
             const float h2 = round_bf16(lo(xv[r][i].y) + lo(av.y)), h3 = round_bf16(hi(xv[r][i].y) + hi(av.y));
             ss[r] = fmaf(h0, h0, ss[r]);
@@ -203,13 +213,13 @@ __global__ __launch_bounds__(256) void router_decode_kernel(const uint16_t* __re
             xv[r][i] = u32x2{pk(h0, h1), pk(h2, h3)};
           }
         const float v = wave_sum(ss[r]);
-        if (lane_id() == 63) nred[r][wave_id_in_block()] = v;
+        if (lane_id() == 63) nred[gi][r][tx >> 6] = v;
       }
       __syncthreads();
 #pragma unroll
       for (int r = 0; r < R; r++) {
         if (r < rows) {
-          const float inv = 1.0f / sqrtf(((nred[r][0] + nred[r][1]) + (nred[r][2] + nred[r][3])) / (float)hidden + eps);
+          const float inv = 1.0f / sqrtf(((nred[gi][r][0] + nred[gi][r][1]) + (nred[gi][r][2] + nred[gi][r][3])) / (float)hidden + eps);
 #pragma unroll
           for (int i = 0; i < KI; i++) {
             const u32x2 hv = xv[r][i];
@@ -217,8 +227,8 @@ __global__ __launch_bounds__(256) void router_decode_kernel(const uint16_t* __re
                                       round_bf16(hi(nw[i].x) * round_bf16(hi(hv.x) * inv))),
                                    pk(round_bf16(lo(nw[i].y) * round_bf16(lo(hv.y) * inv)),
                                       round_bf16(hi(nw[i].y) * round_bf16(hi(hv.y) * inv)))};
-            if ((int)blockIdx.x == r) {
-              const int64_t off = (int64_t)r * hidden + threadIdx.x * 4 + i * 1024;
+            if (e == r) {
+              const int64_t off = (int64_t)r * hidden + tx * 4 + i * 1024;
               *reinterpret_cast<u32x2*>(h_out + off) = hv;
               *reinterpret_cast<u32x2*>(xn_out + off) = xn;
             }
@@ -233,14 +243,14 @@ __global__ __launch_bounds__(256) void router_decode_kernel(const uint16_t* __re
       for (int r = 0; r < R; r++)
         if (r < rows) fma4(r, wv[i], xv[r][i]);
   } else {
-    for (int k = threadIdx.x * 4; k < hidden; k += 256 * 4) {
+    for (int k = tx * 4; k < hidden; k += 256 * 4) {
       const f32x4 wv = *reinterpret_cast<const f32x4*>(we + k);
 #pragma unroll
       for (int r = 0; r < R; r++)
         if (r < rows) fma4(r, wv, *reinterpret_cast<const u32x2*>(x + (int64_t)r * hidden + k));
     }
   }
-  __shared__ float red[R][4];
+  __shared__ float red[kRouterGroups][R][4];
   __shared__ int last;
   __shared__ int32_t sid[kMaxUnits];
   __shared__ int32_t open[kMaxUnits];
@@ -248,12 +258,12 @@ __global__ __launch_bounds__(256) void router_decode_kernel(const uint16_t* __re
 #pragma unroll
   for (int r = 0; r < R; r++) {
     const float v = wave_sum(acc[r]);
-    if (lane == 63) red[r][wv] = v;
+    if (lane == 63) red[gi][r][tx >> 6] = v;
   }
   __syncthreads();
-  if (threadIdx.x < R && (int)threadIdx.x < rows) {
-    const int r = threadIdx.x;
-    const float lg = (red[r][0] + red[r][1]) + (red[r][2] + red[r][3]);
+  if (tx < R && tx < rows) {
+    const int r = tx;
+    const float lg = (red[gi][r][0] + red[gi][r][1]) + (red[gi][r][2] + red[gi][r][3]);
     __hip_atomic_store(logits + (int64_t)r * 256 + e, lg, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   }
   // without a counter the routing is left to the expert kernels (they read the logits after
@@ -287,7 +297,7 @@ __global__ __launch_bounds__(256) void router_decode_kernel(const uint16_t* __re
       }
     }
   } else {
-    for (int row = wv; row < rows; row += 4) route_row<true>(logits, bias, row, ids, scores, sid);
+    for (int row = wv; row < rows; row += 4 * kRouterGroups) route_row<true>(logits, bias, row, ids, scores, sid);
     __syncthreads();
     build_plan_parallel(sid, rows, kSlots, max_users, plan, open);
   }
@@ -329,7 +339,9 @@ int moe_router_fused_plan(const uint16_t* x, const float* w, const float* bias, 
     xin = xn_out;
   }
 #define MOE_ROUTER_LAUNCH(R, KI, N)                                                                                 \
-  hipLaunchKernelGGL((router_decode_kernel<R, KI, N>), dim3(256), dim3(256), 0, s, xin, w, bias, rows, hidden,      \
+  hipLaunchKernelGGL((router_decode_kernel<R, KI, N>), dim3(256 / RouterGroups<R>::value),                       \
+                     dim3(256 * RouterGroups<R>::value), 0, s,                                                        \
+                     xin, w, bias, rows, hidden,                                                                      \
                      experts, max_users, logits, ids, scores, plan, counter, attn, norm_w, eps, h_out, xn_out)
   if (fused_norm && rows == 1)
     MOE_ROUTER_LAUNCH(1, 6, true);
