@@ -193,6 +193,17 @@ enum FinMode { FIN_GATE = 0, FIN_VALUES = 1, FIN_COMBINE = 2 };
 #ifndef MOE_K4_WAVES_8
 #define MOE_K4_WAVES_8 8
 #endif
+// the single-token gate/up GEMV runs 12 waves per block (3 per SIMD): measured faster than 16
+// (47 vs 51 us) and than 8, with the fp16 table and the progress-based wave priority
+#ifndef MOE_K4_WAVES_1_GU
+#define MOE_K4_WAVES_1_GU 12
+#endif
+#ifndef MOE_K4_ALU_EVEN_1_DN
+#define MOE_K4_ALU_EVEN_1_DN MOE_K4_ALU_EVEN_1
+#endif
+#ifndef MOE_K4_ALU_ODD_1_DN
+#define MOE_K4_ALU_ODD_1_DN MOE_K4_ALU_ODD_1
+#endif
 
 // wave issue priority raised for waves that are behind on their range (measured per build)
 #ifndef MOE_K4_PRIO
@@ -791,7 +802,12 @@ int launch_gemv(const GemvArgs& a, int max_ntok, int max_units, hipStream_t stre
   if (nseg_max > kMaxWaves)
     return fail(MOE_ENOTSUP, "too many (unit, column block) segments: %lld > %d", (long long)nseg_max, kMaxWaves);
   {
-    const int WV = max_ntok <= 1 ? MOE_K4_WAVES_1 : MOE_K4_WAVES_8;
+    // single-token launches: the gate/up GEMV (IN_PREP) and the down GEMV may use their own
+    // wave count and decode mix
+    constexpr int kWv1 = IM == IN_PREP ? MOE_K4_WAVES_1_GU : MOE_K4_WAVES_1;
+    constexpr int kEven1 = IM == IN_PREP ? MOE_K4_ALU_EVEN_1 : MOE_K4_ALU_EVEN_1_DN;
+    constexpr int kOdd1 = IM == IN_PREP ? MOE_K4_ALU_ODD_1 : MOE_K4_ALU_ODD_1_DN;
+    const int WV = max_ntok <= 1 ? kWv1 : MOE_K4_WAVES_8;
     // 16 waves per CU (4 per SIMD: the decode's VALU results arrive 16 clocks after issue) when
     // two blocks fit a CU; a block with the 128 KB fp16 table has a CU to itself
     const bool f16_table = max_ntok <= 1 ? TableKind<1>::kF16 : TableKind<kMaxRows>::kF16;
@@ -802,8 +818,7 @@ int launch_gemv(const GemvArgs& a, int max_ntok, int max_units, hipStream_t stre
     if (mblocks * WV > kMaxWaves)
       return fail(MOE_ENOTSUP, "too many waves for the partial buffer (%d)", mblocks * WV);
     if (max_ntok <= 1)
-      hipLaunchKernelGGL((k4_mfma_kernel<IM, FM, 1, MOE_K4_ALU_EVEN_1, MOE_K4_ALU_ODD_1, MOE_K4_WAVES_1>), dim3(mblocks),
-                         dim3(WV * 64), 0, stream, a);
+      hipLaunchKernelGGL((k4_mfma_kernel<IM, FM, 1, kEven1, kOdd1, kWv1>), dim3(mblocks), dim3(WV * 64), 0, stream, a);
     else
       hipLaunchKernelGGL((k4_mfma_kernel<IM, FM, kMaxRows, MOE_K4_ALU_EVEN_8, MOE_K4_ALU_ODD_8, MOE_K4_WAVES_8>),
                          dim3(mblocks), dim3(WV * 64), 0, stream, a);
