@@ -94,8 +94,14 @@ __device__ __forceinline__ float dot8_fp4(uint32_t w, float scale, const float* 
 __device__ __forceinline__ float e8m0_to_f32(uint32_t s) { return __uint_as_float(s == 0 ? 0x00400000u : s << 23); }
 
 // KC = K / 2048 (16-byte chunks per lane per row): 3 for K = 6144 (gate/up), 1 for K = 2048 (down).
+// down launches (K = 2048): kept within 128 VGPRs so two 8-wave blocks share a CU, and launched
+// with that many blocks per CU (more rows in flight per CU)
+#ifndef MOE_MX_DOWN_BPC
+#define MOE_MX_DOWN_BPC 2
+#endif
 template <int MODE, int KC>
-__global__ __launch_bounds__(kMxThreads) void mx_gemv_kernel(MxArgs a) {
+__global__ __launch_bounds__(kMxThreads) __attribute__((amdgpu_waves_per_eu(KC == 1 && MOE_MX_DOWN_BPC > 1 ? 4 : 1)))
+void mx_gemv_kernel(MxArgs a) {
   __shared__ __attribute__((aligned(16))) float xs[2][KC * 2048];
   const int K = KC * 2048;
   const int N = a.N;
@@ -385,7 +391,7 @@ int mx_common(const uint16_t* x, const uint32_t* ids, const float* scores, const
   d.x_f32 = w.hidden;
   d.rowout = w.rowout; d.counter_blk = w.counter_blk; d.counter_grp = w.counter_grp;
   d.out_down = out_down;
-  const dim3 grid(mx_blocks((int64_t)slots * h, h));
+  const dim3 grid(mx_blocks((int64_t)slots * h, h) * MOE_MX_DOWN_BPC);
   if (out) {
     MOE_ARG(slots_per_row == kSlots && scores && residual, "the combined finish needs 9 slots, scores and residual");
     d.scores = scores; d.residual = residual; d.out = out;
