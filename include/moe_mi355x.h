@@ -210,6 +210,20 @@ int moe_mxfp4_prefill(const uint16_t* x, const uint16_t* residual, int rows, con
                       float* scores, void* workspace, size_t workspace_bytes, moe_stream_t stream);
 size_t moe_mxfp4_prefill_workspace_bytes(int rows, int hidden, int intermediate, int64_t experts);
 
+/* Sorted grouped joined-MXFP4 expert MLP for many rows: per-slot values [rows*slots, h] bf16 of
+ * ids [rows, slots] (x [rows, h] bf16 shared by a row's slots) through the same segment table,
+ * activation terms and MX-MFMA grouped GEMMs as moe_mxfp4_prefill, with no router and no combine.
+ * Slots whose id is outside [0, experts) get no position in the work order and are not written.
+ * Weights/side vectors as moe_mxfp4_mlp; workspace: moe_mxfp4_grouped_mlp_workspace_bytes (no zeroing).
+ * Replaces: exlr8/joined_mxfp4.py:98-134 _inner on the sorted-RHS gather_qmm branch (grouped, >= 1028
+ * slots in the reference) and exlr8/joined_mxfp4.py:143-147 JoinedMXFP4.slots for prefill rows. */
+int moe_mxfp4_grouped_mlp(const uint16_t* x, const uint32_t* ids, int rows, int slots, const uint8_t* gate_up_codes,
+                          const uint8_t* gate_up_scales, const uint8_t* down_codes, const uint8_t* down_scales,
+                          int64_t experts, const uint16_t* unit, const uint16_t* out_gate, const uint16_t* out_up,
+                          const uint16_t* in_down, const uint16_t* out_down, int hidden, int intermediate,
+                          uint16_t* values, void* workspace, size_t workspace_bytes, moe_stream_t stream);
+size_t moe_mxfp4_grouped_mlp_workspace_bytes(int rows, int slots, int hidden, int intermediate, int64_t experts);
+
 /* Grouped K4 expert MLP over many rows (prefill): values[slot] = T(out_down[e] * H(H(h) @ down_e))
  * with h = H(swiglu_T(gate, up) * in_down[e]), gate/up = out_scale * H(H(x * in_scale[e]) @ inner_e),
  * for ids [rows, slots] (flat ids < experts; x [rows, hidden] bf16 shared by a row's slots).

@@ -49,6 +49,9 @@ _SIGNATURES = {
     "moe_mxfp4_prefill": (_I32, [_VP, _VP, _I32, _VP, _VP, _VP, _VP, _VP, _VP, _I64] + [_VP] * 5
                           + [_I32, _I32, _VP, _VP, _VP, _VP, _SZ, _VP]),
     "moe_mxfp4_prefill_workspace_bytes": (_SZ, [_I32, _I32, _I32, _I64]),
+    "moe_mxfp4_grouped_mlp": (_I32, [_VP, _VP, _I32, _I32, _VP, _VP, _VP, _VP, _I64] + [_VP] * 5
+                              + [_I32, _I32, _VP, _VP, _SZ, _VP]),
+    "moe_mxfp4_grouped_mlp_workspace_bytes": (_SZ, [_I32, _I32, _I32, _I32, _I64]),
     "moe_k4_to_mxfp4": (_I32, [_VP, _I64, _I32, _I32, _I32, _VP, _VP, _VP, _VP, _I32, _I32, _VP, _SZ, _VP]),
     "moe_k4_to_mxfp4_workspace_bytes": (_SZ, [_I32, _I32]),
     "moe_k4_grouped_mlp": (_I32, [_VP, _VP, _I32, _I32, _VP, _VP, _VP, _I64] + [_VP] * 6 + [_I32, _I32, _VP, _VP, _SZ,

@@ -530,7 +530,7 @@ __device__ __forceinline__ void k4_mfma_body(const GemvArgs& a, const Plan* __re
     auto load_quad = [&](u32x4(&pc)[4], int tq) {
       const uint8_t* qp = quad_ptr(tq);
 #pragma unroll
-      for (int s4 = 0; s4 < 4; s4++) pc[s4] = *reinterpret_cast<const u32x4*>(qp + 256 * s4);
+      for (int s4 = 0; s4 < 4; s4++) pc[s4] = load_stream16(qp + 256 * s4);
     };
     // x of one 128-row block for every token of the unit is fetched one block ahead of its use
     // (raw words in registers) and turned into A fragments when its block starts.
@@ -654,7 +654,7 @@ __device__ __forceinline__ void k4_mfma_body(const GemvArgs& a, const Plan* __re
             decode_pair_words_f16<ALU_EVEN, ALU_ODD, TableKind<NT>::kF16>(v.x, v.y, prior[s4], tab, q);
           else
             decode_pair_words_f16<ALU_EVEN, ALU_ODD, TableKind<NT>::kF16>(v.z, v.w, v.y, tab, q);
-          if (rh == 1) pc[s4] = *reinterpret_cast<const u32x4*>(np + 256 * s4);
+          if (rh == 1) pc[s4] = load_stream16(np + 256 * s4);
           const f16x8 b0 = frag(q[0][0], q[0][1], q[1][0], q[1][1]);
           const f16x8 b1 = frag(q[0][2], q[0][3], q[1][2], q[1][3]);
           acc[s4][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[rh], b0, acc[s4][0], 0, 0, 0);

@@ -132,7 +132,7 @@ void mx_gemv_kernel(MxArgs a) {
     const uint8_t* srow = a.scales + ((int64_t)e * N + n) * (K / 32);
 #pragma unroll
     for (int i = 0; i < KC; i++) {
-      wr[j][i] = *reinterpret_cast<const u32x4*>(crow + 1024 * i + 16 * lane);
+      wr[j][i] = load_stream16(crow + 1024 * i + 16 * lane);
       sr[j][i] = srow[64 * i + lane];
     }
   };

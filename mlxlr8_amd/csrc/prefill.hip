@@ -699,9 +699,10 @@ struct PfWorkspace {
 
 int pf_cap(int64_t n, int64_t experts) { return (int)(n / kPfItemRows + experts + 1); }
 
-PfWorkspace pf_carve(void* base, int rows, int h, int m, int64_t experts) {
+// n = rows * slots expert slots
+PfWorkspace pf_carve(void* base, int rows, int slots, int h, int m, int64_t experts) {
   PfWorkspace w{};
-  const int64_t n = (int64_t)rows * kSlots;
+  const int64_t n = (int64_t)rows * slots;
   w.cap = pf_cap(n, experts);
   size_t off = 0;
   char* p = static_cast<char*>(base);
@@ -772,20 +773,30 @@ int moe_segment_table(const uint32_t* ids, int n, int experts, int block_rows, i
 
 size_t moe_mxfp4_prefill_workspace_bytes(int rows, int hidden, int intermediate, int64_t experts) {
   if (rows <= 0 || hidden <= 0 || intermediate <= 0 || experts <= 0) return 0;
-  return pf_carve(nullptr, rows, hidden, intermediate, experts).bytes;
+  return pf_carve(nullptr, rows, kSlots, hidden, intermediate, experts).bytes;
 }
 
-int moe_mxfp4_prefill(const uint16_t* x, const uint16_t* residual, int rows, const float* router_w,
-                      const float* bias, const uint8_t* gate_up_codes, const uint8_t* gate_up_scales,
-                      const uint8_t* down_codes, const uint8_t* down_scales, int64_t experts, const uint16_t* unit,
-                      const uint16_t* out_gate, const uint16_t* out_up, const uint16_t* in_down,
-                      const uint16_t* out_down, int hidden, int intermediate, uint16_t* out, uint32_t* indices,
-                      float* scores, void* workspace, size_t workspace_bytes, moe_stream_t stream) {
-  MOE_ARG(x && residual && router_w && bias && gate_up_codes && gate_up_scales && down_codes && down_scales && unit &&
-              out_gate && out_up && in_down && out_down && out,
+size_t moe_mxfp4_grouped_mlp_workspace_bytes(int rows, int slots, int hidden, int intermediate, int64_t experts) {
+  if (rows <= 0 || slots <= 0 || hidden <= 0 || intermediate <= 0 || experts <= 0) return 0;
+  return pf_carve(nullptr, rows, slots, hidden, intermediate, experts).bytes;
+}
+
+}  // extern "C"
+
+namespace moe {
+namespace {
+
+// Argument checks shared by the grouped MXFP4 entry points (all before any launch).
+int mx_grouped_check(const uint16_t* x, const uint8_t* gate_up_codes, const uint8_t* gate_up_scales,
+                     const uint8_t* down_codes, const uint8_t* down_scales, int64_t experts, const uint16_t* unit,
+                     const uint16_t* out_gate, const uint16_t* out_up, const uint16_t* in_down,
+                     const uint16_t* out_down, int rows, int slots, int hidden, int intermediate, const void* workspace,
+                     size_t workspace_bytes, PfWorkspace* w) {
+  MOE_ARG(x && gate_up_codes && gate_up_scales && down_codes && down_scales && unit && out_gate && out_up &&
+              in_down && out_down,
           "null pointer argument");
-  MOE_ARG(rows >= 1, "rows must be positive");
-  MOE_ARG(experts == 257, "the routed block needs 256 routed experts plus the shared expert (got %lld)",
+  MOE_ARG(rows >= 1 && slots >= 1, "rows and slots must be positive (got %d, %d)", rows, slots);
+  MOE_ARG(experts >= 1 && experts <= kPfMaxExperts, "experts must be in 1..%d (got %lld)", kPfMaxExperts,
           (long long)experts);
   MOE_ARG(hidden % 1024 == 0 && hidden > 0, "hidden must be a positive multiple of 1024 (got %d)", hidden);
   MOE_ARG(intermediate % 256 == 0 && intermediate > 0, "intermediate must be a positive multiple of 256 (got %d)",
@@ -795,22 +806,25 @@ int moe_mxfp4_prefill(const uint16_t* x, const uint16_t* residual, int rows, con
           "hidden %d / intermediate %d too large for the prefill GEMM's LDS", hidden, intermediate);
   MOE_ARG(((uintptr_t)gate_up_scales | (uintptr_t)down_scales) % 16 == 0, "weight scale arrays must be 16-byte aligned");
   MOE_ARG(workspace != nullptr, "workspace must not be NULL");
-  const PfWorkspace w = pf_carve(workspace, rows, hidden, intermediate, experts);
-  if (workspace_bytes < w.bytes)
-    return fail(MOE_EWORKSPACE, "workspace too small: %zu < %zu bytes", workspace_bytes, w.bytes);
-  int rc = ensure_device_ready();
+  *w = pf_carve(const_cast<void*>(workspace), rows, slots, hidden, intermediate, experts);
+  if (workspace_bytes < w->bytes)
+    return fail(MOE_EWORKSPACE, "workspace too small: %zu < %zu bytes", workspace_bytes, w->bytes);
+  return ensure_device_ready();
+}
+
+// Sorted grouped MXFP4 expert MLP of ids [rows, slots] (a row's slots share x [rows, hidden]):
+// segment table, activation terms, gate/up GEMM + gate finish, down GEMM + value finish into
+// values [rows * slots, hidden] bf16 (slot order).  Slots whose id is outside [0, experts) get no
+// position in the work order and are not written.
+int mx_grouped_body(const uint16_t* x, int rows, int slots, const uint32_t* ids, const uint8_t* gate_up_codes,
+                    const uint8_t* gate_up_scales, const uint8_t* down_codes, const uint8_t* down_scales,
+                    int64_t experts, const uint16_t* unit, const uint16_t* out_gate, const uint16_t* out_up,
+                    const uint16_t* in_down, const uint16_t* out_down, int hidden, int intermediate, uint16_t* values,
+                    const PfWorkspace& w, hipStream_t s) {
+  const int n = rows * slots;
+  int rc = launch_segment_table(ids, n, (int)experts, kPfItemRows, w.order, w.counts, w.starts, w.blk, w.cap, w.nblk,
+                                s);
   if (rc) return rc;
-  hipStream_t s = (hipStream_t)stream;
-  const int n = rows * kSlots;
-  uint32_t* ids = indices ? indices : w.ids;
-  float* sc = scores ? scores : w.scores;
-  // routing: router GEMV, then top-8 + shared slot per row
-  if ((rc = moe_router_logits(x, router_w, rows, hidden, 256, w.logits, stream))) return rc;
-  if ((rc = moe_route_f32(w.logits, bias, rows, ids, sc, stream))) return rc;
-  // sorted work order in blocks of <= kPfItemRows rows
-  if ((rc = launch_segment_table(ids, n, (int)experts, kPfItemRows, w.order, w.counts, w.starts, w.blk, w.cap,
-                                 w.nblk, s)))
-    return rc;
   // activation terms
   const int64_t pwaves = (int64_t)rows * (hidden / 128);
   hipLaunchKernelGGL(prep_terms_kernel, dim3((unsigned)((pwaves + 3) / 4)), dim3(256), 0, s, x, unit, rows, hidden,
@@ -827,7 +841,7 @@ int moe_mxfp4_prefill(const uint16_t* x, const uint16_t* residual, int rows, con
   g.as = w.xs;
   g.arows = rows;
   g.rowmap = w.order;
-  g.rowdiv = kSlots;
+  g.rowdiv = slots;
   g.blk = w.blk;
   g.cap = w.cap;
   g.nblk = w.nblk;
@@ -859,8 +873,51 @@ int moe_mxfp4_prefill(const uint16_t* x, const uint16_t* residual, int rows, con
   d.order = w.order;
   d.m = intermediate;
   d.out_down = out_down;
-  d.values = w.values;
-  if ((rc = launch_pf_gemm<false>(d, s))) return rc;
+  d.values = values;
+  return launch_pf_gemm<false>(d, s);
+}
+
+}  // namespace
+}  // namespace moe
+
+extern "C" {
+
+int moe_mxfp4_grouped_mlp(const uint16_t* x, const uint32_t* ids, int rows, int slots, const uint8_t* gate_up_codes,
+                          const uint8_t* gate_up_scales, const uint8_t* down_codes, const uint8_t* down_scales,
+                          int64_t experts, const uint16_t* unit, const uint16_t* out_gate, const uint16_t* out_up,
+                          const uint16_t* in_down, const uint16_t* out_down, int hidden, int intermediate,
+                          uint16_t* values, void* workspace, size_t workspace_bytes, moe_stream_t stream) {
+  MOE_ARG(ids && values, "null pointer argument");
+  PfWorkspace w{};
+  int rc = mx_grouped_check(x, gate_up_codes, gate_up_scales, down_codes, down_scales, experts, unit, out_gate, out_up,
+                            in_down, out_down, rows, slots, hidden, intermediate, workspace, workspace_bytes, &w);
+  if (rc) return rc;
+  return mx_grouped_body(x, rows, slots, ids, gate_up_codes, gate_up_scales, down_codes, down_scales, experts, unit,
+                         out_gate, out_up, in_down, out_down, hidden, intermediate, values, w, (hipStream_t)stream);
+}
+
+int moe_mxfp4_prefill(const uint16_t* x, const uint16_t* residual, int rows, const float* router_w,
+                      const float* bias, const uint8_t* gate_up_codes, const uint8_t* gate_up_scales,
+                      const uint8_t* down_codes, const uint8_t* down_scales, int64_t experts, const uint16_t* unit,
+                      const uint16_t* out_gate, const uint16_t* out_up, const uint16_t* in_down,
+                      const uint16_t* out_down, int hidden, int intermediate, uint16_t* out, uint32_t* indices,
+                      float* scores, void* workspace, size_t workspace_bytes, moe_stream_t stream) {
+  MOE_ARG(residual && router_w && bias && out, "null pointer argument");
+  MOE_ARG(experts == 257, "the routed block needs 256 routed experts plus the shared expert (got %lld)",
+          (long long)experts);
+  PfWorkspace w{};
+  int rc = mx_grouped_check(x, gate_up_codes, gate_up_scales, down_codes, down_scales, experts, unit, out_gate, out_up,
+                            in_down, out_down, rows, kSlots, hidden, intermediate, workspace, workspace_bytes, &w);
+  if (rc) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  uint32_t* ids = indices ? indices : w.ids;
+  float* sc = scores ? scores : w.scores;
+  // routing: router GEMV, then top-8 + shared slot per row
+  if ((rc = moe_router_logits(x, router_w, rows, hidden, 256, w.logits, stream))) return rc;
+  if ((rc = moe_route_f32(w.logits, bias, rows, ids, sc, stream))) return rc;
+  if ((rc = mx_grouped_body(x, rows, kSlots, ids, gate_up_codes, gate_up_scales, down_codes, down_scales, experts,
+                            unit, out_gate, out_up, in_down, out_down, hidden, intermediate, w.values, w, s)))
+    return rc;
   hipLaunchKernelGGL(pf_combine_kernel, dim3(rows), dim3(256), 0, s, w.values, sc, residual, hidden, out);
   MOE_HIP(hipGetLastError());
   return MOE_OK;

@@ -9,8 +9,7 @@ from types import SimpleNamespace
 import torch
 
 from ._lib import check, lib, ptr, require_cuda, stream, workspace
-from .fast_decode import _weights, fast_expert_mlp
-from .fast_prefill import grouped_expert_mlp
+from .fast_decode import _weights, expert_values
 from .trellis import BF16, _check_format
 
 
@@ -48,8 +47,7 @@ class ExpertLayer:
         experts take the grouped MLP at every row count)."""
         if self.affine is not None:
             return self.affine.slots(x, ids)
-        mlp = fast_expert_mlp if ids.numel() // ids.shape[-1] <= 16 else grouped_expert_mlp
-        return mlp(x, ids, self.packed, self.scales, self.k, self.hidden, self.intermediate)
+        return expert_values(x, ids, self.packed, self.scales, self.k, self.hidden, self.intermediate)
 
     def decode_block(self, x, residual, router_weight, bias):
         """Router GEMV + route + expert MLP + combine in one C call (decode batches, <= 8 rows).

@@ -84,26 +84,33 @@ def combine_values(values, scores, residual):
     return out.reshape(residual.shape)
 
 
+def expert_values(x, indices, packed, scales, k, hidden, intermediate):
+    """Per-slot values by the reference's row-count rule (exlr8/experts.py:170-175): up to 16 token
+    rows through the decode MLP, more through the sorted grouped MLP (K2/K3 always grouped)."""
+    rows = indices.numel() // indices.shape[-1]
+    if k == 4 and rows <= 16:
+        return fast_expert_mlp(x, indices, packed, scales, k, hidden, intermediate)
+    return grouped_expert_mlp(x, indices, packed, scales, k, hidden, intermediate)
+
+
 def mlp_finish(x, indices, scores, residual, packed, scales, hidden, intermediate, k=4):
-    """Expert MLP plus the weighted combine with the shared expert (slot 8) and the residual."""
+    """Expert MLP plus the weighted combine with the shared expert (slot 8) and the residual:
+    one fused call for K4 decode batches (<= 8 rows), else per-slot values and the combine."""
     _validate(x.reshape(-1, hidden), indices.reshape(-1, 9), packed, scales, k, hidden, intermediate)
-    if k != 4:
-        values = grouped_expert_mlp(x.reshape(-1, hidden), indices.reshape(-1, 9), packed, scales, k, hidden,
-                                    intermediate)
-        return combine_values(values, scores, residual)
     rows = x.numel() // hidden
+    require_cuda(scores, residual)
+    if k != 4 or rows > MAX_ROWS:
+        values = expert_values(x.reshape(rows, hidden), indices.reshape(rows, 9), packed, scales, k, hidden,
+                               intermediate)
+        return combine_values(values, scores, residual)
     xr = x.reshape(rows, hidden).contiguous()
     ids = indices.reshape(rows, 9).to(torch.int32).contiguous()
     sc = scores.reshape(rows, 8).to(torch.float32).contiguous()
     res = residual.reshape(rows, hidden).to(BF16).contiguous()
     out = torch.empty((rows, hidden), dtype=BF16, device=x.device)
     ws = workspace(x.device, hidden, intermediate)
-    w = _weights(packed, scales)
-    st = stream(x.device)
-    for r0 in range(0, rows, MAX_ROWS):
-        r1 = min(rows, r0 + MAX_ROWS)
-        check(lib().moe_k4_mlp_finish(ptr(xr[r0:r1]), ptr(ids[r0:r1]), ptr(sc[r0:r1]), ptr(res[r0:r1]), r1 - r0,
-                                      *w, hidden, intermediate, ptr(out[r0:r1]), ptr(ws), ws.numel(), st))
+    check(lib().moe_k4_mlp_finish(ptr(xr), ptr(ids), ptr(sc), ptr(res), rows, *_weights(packed, scales), hidden,
+                                  intermediate, ptr(out), ptr(ws), ws.numel(), stream(x.device)))
     return out.reshape(residual.shape)
 
 

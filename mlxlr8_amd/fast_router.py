@@ -33,8 +33,10 @@ def route(logits, bias):
 def compiled_finish(experts, gate, bias):
     """exlr8/fast_router.py:27-37: call(x, residual) = experts' finish(x, route(gate(x)), residual).
 
-    ``gate`` is the fp32 router weight [256, hidden] (or a callable returning logits).
-    Trellis experts use the single fused decode entry point; others route then finish.
+    ``gate`` is the fp32 router weight [256, hidden] (or a callable returning logits).  With the
+    weight given, one library call covers router, routing, experts and combine: joined-MXFP4
+    experts take the decode block for <= 8 rows and the grouped prefill block beyond; K4 experts
+    the decode block for <= 8 rows.  Otherwise routing is followed by the experts' finish.
     """
     from .fast_decode import compiled_expert_mlp_finish
 
@@ -44,8 +46,12 @@ def compiled_finish(experts, gate, bias):
     def call(x, residual):
         h = x.shape[-1]
         rows = x.numel() // h
-        if weight is not None and getattr(experts, "affine", None) is None and getattr(experts, "k", None) == 4 \
-                and rows <= 8:
+        affine = getattr(experts, "affine", None)
+        if weight is not None and affine is not None and getattr(affine, "experts", 0) == 257:
+            if rows <= affine.DECODE_ROWS:
+                return affine.decode_block(x, residual, weight, bias)[0]
+            return affine.prefill(x, residual, weight, bias)[0]
+        if weight is not None and affine is None and getattr(experts, "k", None) == 4 and rows <= 8:
             return experts.decode_block(x, residual, weight, bias)
         logits = router_logits(x, weight) if weight is not None else gate(x.float())
         indices, scores = route(logits, bias)

@@ -79,6 +79,11 @@ class JoinedMXFP4:
         return [ptr(gc), ptr(gs), ptr(dc), ptr(ds), self.experts, ptr(self.unit), ptr(self.scales["gate"][1]),
                 ptr(self.scales["up"][1]), ptr(self.scales["down"][0]), ptr(self.scales["down"][1])]
 
+    # decode batches (<= 8 token rows) run the MXFP4 GEMVs; larger batches the sorted grouped
+    # GEMM on the MX matrix cores (the reference switches to its sorted gather_qmm for prefill
+    # sizes, exlr8/joined_mxfp4.py:98-113)
+    DECODE_ROWS = 8
+
     def slots(self, x, ids):
         """values [*ids.shape, h] (exlr8/joined_mxfp4.py:143-147)."""
         h = self.hidden
@@ -86,13 +91,20 @@ class JoinedMXFP4:
             raise ValueError("activation rows do not match the expert indices")
         if x.dtype != BF16:
             raise ValueError("this build computes bf16 activations")
+        require_cuda(x, ids)
         slots = ids.shape[-1]
         idx = ids.reshape(-1, slots).to(torch.int32).contiguous()
         rows = idx.shape[0]
         xr = x.reshape(rows, h).contiguous()
         values = torch.empty((rows * slots, h), dtype=BF16, device=x.device)
-        ws = workspace(x.device, h, self.intermediate, "mxfp4")
         st = stream(x.device)
+        if rows > self.DECODE_ROWS:
+            nbytes = lib().moe_mxfp4_grouped_mlp_workspace_bytes(rows, slots, h, self.intermediate, self.experts)
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+            check(lib().moe_mxfp4_grouped_mlp(ptr(xr), ptr(idx), rows, slots, *self._args(), h, self.intermediate,
+                                              ptr(values), ptr(ws), nbytes, st))
+            return values.reshape(*ids.shape, h)
+        ws = workspace(x.device, h, self.intermediate, "mxfp4")
         step = max(1, 72 // slots)
         for r0 in range(0, rows, step):
             r1 = min(rows, r0 + step)
@@ -106,18 +118,18 @@ class JoinedMXFP4:
         rows = x.numel() // h
         if x.dtype != BF16:
             raise ValueError("this build computes bf16 activations")
+        require_cuda(x, ids, scores, residual)
+        if rows > self.DECODE_ROWS:
+            from .fast_decode import combine_values
+            return combine_values(self.slots(x.reshape(rows, h), ids.reshape(rows, 9)), scores, residual)
         xr = x.reshape(rows, h).contiguous()
         idx = ids.reshape(rows, 9).to(torch.int32).contiguous()
         sc = scores.reshape(rows, 8).to(torch.float32).contiguous()
         res = residual.reshape(rows, h).to(BF16).contiguous()
         out = torch.empty((rows, h), dtype=BF16, device=x.device)
         ws = workspace(x.device, h, self.intermediate, "mxfp4")
-        st = stream(x.device)
-        for r0 in range(0, rows, 8):
-            r1 = min(rows, r0 + 8)
-            check(lib().moe_mxfp4_mlp_finish(ptr(xr[r0:r1]), ptr(idx[r0:r1]), ptr(sc[r0:r1]), ptr(res[r0:r1]), r1 - r0,
-                                             *self._args(), h, self.intermediate, ptr(out[r0:r1]), ptr(ws), ws.numel(),
-                                             st))
+        check(lib().moe_mxfp4_mlp_finish(ptr(xr), ptr(idx), ptr(sc), ptr(res), rows, *self._args(), h,
+                                         self.intermediate, ptr(out), ptr(ws), ws.numel(), stream(x.device)))
         return out.reshape(residual.shape)
 
     def prepare_decode(self, x, residual, router_weight, bias):

@@ -7,7 +7,7 @@ from dataclasses import dataclass
 
 import torch
 
-from .fast_decode import compiled_expert_mlp_finish
+from .fast_decode import combine_values
 from .fast_router import compiled_finish, route, router_logits
 
 
@@ -50,27 +50,30 @@ def route_experts(logits, bias, args):
 
 
 class MoEBlock:
-    """`DecoderLayer.__call__`'s sparse branch: returns h + routed + shared (exlr8/model.py:385-418)."""
+    """`DecoderLayer.__call__`'s sparse branch: returns h + routed + shared (exlr8/model.py:385-418).
+
+    With the GLM router configuration every row count goes through ``compiled_finish`` (one
+    library call for decode batches and for joined-MXFP4 prefill chunks; K4 prefill rows are
+    routed, run through the grouped trellis MLP and combined).  Other configurations take the
+    reference's general branch: route_experts, experts(x, indices), then the model combine.
+    """
 
     def __init__(self, args, router_weight, bias, experts):
         self.args, self.gate, self.bias, self.experts = args, router_weight, bias, experts
         self._routed_finish = None
-        self._expert_finish = None
 
     def __call__(self, x, h):
         a = self.args
-        rows = x.numel() // x.shape[-1]
-        if 1 <= rows <= 8 and _fast_router_args(a) and getattr(self.experts, "k", None) == 4 \
-                and x.dtype == torch.bfloat16 and self.bias.shape == (256,):
+        if _fast_router_args(a) and x.dtype == torch.bfloat16 and self.bias.shape == (256,):
             if self._routed_finish is None:
                 self._routed_finish = compiled_finish(self.experts, self.gate, self.bias)
             return self._routed_finish(x, h)
-        ids, scores = route_experts(router_logits(x, self.gate), self.bias, a)
+        logits = router_logits(x, self.gate) if isinstance(self.gate, torch.Tensor) else self.gate(x.float())
+        ids, scores = route_experts(logits, self.bias, a)
         shared = torch.full(ids.shape[:-1] + (1,), a.n_routed_experts, dtype=ids.dtype, device=ids.device)
         indices = torch.cat([ids, shared], dim=-1)
-        if self._expert_finish is None:
-            self._expert_finish = compiled_expert_mlp_finish(self.experts)
-        return self._expert_finish(x, indices, scores, h)
+        values = self.experts(x, indices)
+        return combine_values(values, scores, h)
 
 
 class DecoderMoELayer:

@@ -1,6 +1,6 @@
 """Seeded synthetic MoE layers (random-init weights of the GLM-5.3 expert shapes).
 
-There is no checkpoint access; every tensor is drawn on the device from a seeded
+There is no checkpoint access; expert weights are drawn on the device from a seeded
 ``torch.Generator`` so a seed reproduces the same layer on any MI355X.
 
 K4 trellis layer (the reference's resident K4 expert layout, exlr8/experts.py:99-124):
@@ -10,6 +10,8 @@ K4 trellis layer (the reference's resident K4 expert layout, exlr8/experts.py:99
 Joined MXFP4 layer (exlr8/joined_mxfp4.py:12-47 layout): random e2m1 codes with e8m0 scales
   chosen so dequantised values have std ~ 1/sqrt(h).
 Router: fp32 weight ~ N(0, 0.02), bias ~ N(0, 0.01), optional Zipf(1.1) ranked offset.
+Router weights and activations are drawn on the host generator, so a seed gives the same routing
+inputs on any device (and on the CPU).
 """
 import math
 
@@ -41,13 +43,21 @@ def zipf_offset(n, seed, s=1.1, scale=0.08, device="cpu"):
     return (scale * rank.pow(-s)).float().to(device)
 
 
+def _host_gen(seed):
+    g = torch.Generator(device="cpu")
+    g.manual_seed(int(seed))
+    return g
+
+
 def router(device, seed, hidden=HIDDEN, experts=256, zipf=False):
-    g = _gen(device, seed)
-    w = torch.randn((experts, hidden), generator=g, device=device) * 0.02
-    bias = torch.randn((experts,), generator=g, device=device) * 0.01
+    """fp32 router weight [experts, hidden] ~ N(0, 0.02) and bias [experts] ~ N(0, 0.01), drawn on the
+    host generator (the same values on every device) and moved to ``device``."""
+    g = _host_gen(seed)
+    w = torch.randn((experts, hidden), generator=g) * 0.02
+    bias = torch.randn((experts,), generator=g) * 0.01
     if zipf:
-        bias = bias + zipf_offset(experts, seed, device=device)
-    return w.contiguous(), bias.contiguous()
+        bias = bias + zipf_offset(experts, seed)
+    return w.to(device).contiguous(), bias.to(device).contiguous()
 
 
 def k4_layer(device, seed, hidden=HIDDEN, intermediate=INTER, experts=EXPERTS, k=4):
@@ -88,13 +98,18 @@ def mxfp4_layer(device, seed, hidden=HIDDEN, intermediate=INTER, experts=EXPERTS
 
 
 def activations(device, seed, rows, hidden=HIDDEN, correlated=False):
-    """x, residual bf16 [rows, hidden] ~ N(0,1); correlated=True shares a base vector so that
-    about 30% of routed experts repeat across the rows."""
-    g = _gen(device, seed + 1)
+    """x, residual bf16 [rows, hidden] ~ N(0, 1), drawn on the host generator and moved to ``device``.
+
+    correlated=True is the speculative-verify batch: consecutive token pairs share a base vector
+    ~ N(0, 1) and each token adds its own N(0, 0.5^2) noise.  Through the GLM router this gives
+    ~47 distinct experts per 8 tokens (8 routed + 1 shared each), i.e. ~30% of the routed experts
+    repeat across tokens; one base vector for all 8 tokens gives only ~25 distinct experts.
+    """
+    g = _host_gen(seed + 1)
     if correlated:
-        base = torch.randn((1, hidden), generator=g, device=device)
-        x = base + 0.5 * torch.randn((rows, hidden), generator=g, device=device)
+        base = torch.randn(((rows + 1) // 2, hidden), generator=g)
+        x = base[torch.arange(rows) // 2] + 0.5 * torch.randn((rows, hidden), generator=g)
     else:
-        x = torch.randn((rows, hidden), generator=g, device=device)
-    residual = torch.randn((rows, hidden), generator=g, device=device)
-    return x.to(torch.bfloat16), residual.to(torch.bfloat16)
+        x = torch.randn((rows, hidden), generator=g)
+    residual = torch.randn((rows, hidden), generator=g)
+    return x.to(torch.bfloat16).to(device), residual.to(torch.bfloat16).to(device)

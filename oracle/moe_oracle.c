@@ -459,36 +459,106 @@ void orc_k4_moe(const uint16_t* x, const uint32_t* idx9, const float* scores8, c
 
 /* ---------------- joined MXFP4 MoE layer (joined_mxfp4.py:90-165) ----------------
    gate_up codes [E, 2m, h/2], scales [E, 2m, h/32]; down codes [E, h, m/2], scales [E, h, m/32];
-   unit [h] fp16 (+-1); out_g/out_u [E, m], in_d [E, m], out_d [E, h] fp16. */
+   unit [h] fp16 (+-1); out_g/out_u [E, m], in_d [E, m], out_d [E, h] fp16.
+   Slots are taken expert by expert: each weight row is dequantised once (e2m1 x 2^(s-127), exact
+   in double) and dotted in double with every slot of that expert, rows split over the threads. */
+static double g_e2m1_d[16], g_e8m0_d[256];
+static int g_mx_tables_ready = 0;
+static void ensure_mx_tables(void) {
+  if (g_mx_tables_ready) return;
+  for (int i = 0; i < 16; i++) g_e2m1_d[i] = (double)orc_e2m1((uint32_t)i);
+  for (int i = 0; i < 256; i++) g_e8m0_d[i] = (double)orc_e8m0((uint32_t)i);
+  g_mx_tables_ready = 1;
+}
+static void dequant_row(const uint8_t* codes, const uint8_t* scales, int K, double* w) {
+  for (int g = 0; g < K / 32; g++) {
+    const double sc = g_e8m0_d[scales[g]];
+    for (int j = 0; j < 16; j++) {
+      const uint8_t b = codes[g * 16 + j];
+      w[g * 32 + 2 * j] = g_e2m1_d[b & 15u] * sc;
+      w[g * 32 + 2 * j + 1] = g_e2m1_d[b >> 4] * sc;
+    }
+  }
+}
+static double dot_d(const double* a, const double* b, int n) {
+  double s = 0.0;
+#pragma omp simd reduction(+ : s)
+  for (int k = 0; k < n; k++) s += a[k] * b[k];
+  return s;
+}
+/* y[j][n] = row n of the expert's matrix . x[j] for its `cnt` slot vectors x [cnt][K]; rows are
+   dequantised in blocks of 32 per thread so each slot vector is read once per block */
+static void mx_expert_rows(const uint8_t* codes, const uint8_t* scales, int K, int N, const double* x, int cnt,
+                           float* y) {
+  enum { RB = 32 };
+#pragma omp parallel
+  {
+    double* w = (double*)malloc(sizeof(double) * (size_t)K * RB);
+#pragma omp for schedule(dynamic)
+    for (int n0 = 0; n0 < N; n0 += RB) {
+      const int nr = N - n0 < RB ? N - n0 : RB;
+      for (int r = 0; r < nr; r++)
+        dequant_row(codes + (int64_t)(n0 + r) * (K / 2), scales + (int64_t)(n0 + r) * (K / 32), K, w + (int64_t)r * K);
+      for (int j = 0; j < cnt; j++)
+        for (int r = 0; r < nr; r++)
+          y[(int64_t)j * N + n0 + r] = (float)dot_d(x + (int64_t)j * K, w + (int64_t)r * K, K);
+    }
+    free(w);
+  }
+}
+
 void orc_mxfp4_moe(const uint16_t* x, const uint32_t* idx9, const float* scores8, const uint16_t* residual, int rows,
                    int h, int m, const uint8_t* gu_codes, const uint8_t* gu_scales, const uint8_t* d_codes,
                    const uint8_t* d_scales, const uint16_t* unit, const uint16_t* out_g, const uint16_t* out_u,
                    const uint16_t* in_d, const uint16_t* out_d, uint16_t* out, uint16_t* values) {
-  int slots = rows * 9;
+  const int slots = rows * 9;
+  ensure_mx_tables();
   float* y = (float*)malloc((size_t)slots * h * sizeof(float));
-#pragma omp parallel for schedule(dynamic)
-  for (int s = 0; s < slots; s++) {
-    int r = s / 9;
-    int64_t e = idx9[s];
-    float* xh = (float*)malloc((size_t)h * sizeof(float));
-    float* gu = (float*)malloc((size_t)2 * m * sizeof(float));
-    float* a = (float*)malloc((size_t)m * sizeof(float));
-    for (int i = 0; i < h; i++) xh[i] = bf16_to_f32(x[(int64_t)r * h + i]) * f16_to_f32(unit[i]);
-    orc_hadamard128(xh, h);
-    mxfp4_linear_one(xh, gu_codes + e * 2 * m * (h / 2), gu_scales + e * 2 * m * (h / 32), h, 2 * m, gu);
-    orc_hadamard128(gu, m);
-    orc_hadamard128(gu + m, m);
-    for (int i = 0; i < m; i++) {
-      float gv = gu[i] * f16_to_f32(out_g[e * m + i]), uv = gu[m + i] * f16_to_f32(out_u[e * m + i]);
-      a[i] = orc_swiglu_bf16(gv, uv) * f16_to_f32(in_d[e * m + i]);
-    }
-    orc_hadamard128(a, m);
-    float* v = y + (int64_t)s * h;
-    mxfp4_linear_one(a, d_codes + e * h * (m / 2), d_scales + e * h * (m / 32), m, h, v);
-    orc_hadamard128(v, h);
-    for (int i = 0; i < h; i++) v[i] = round_bf16(v[i] * f16_to_f32(out_d[e * h + i]));
-    free(xh); free(gu); free(a);
+  /* shared prep: xh = H128(x * unit) per token row */
+  float* xh = (float*)malloc((size_t)rows * h * sizeof(float));
+  for (int r = 0; r < rows; r++) {
+    for (int i = 0; i < h; i++) xh[(int64_t)r * h + i] = bf16_to_f32(x[(int64_t)r * h + i]) * f16_to_f32(unit[i]);
+    orc_hadamard128(xh + (int64_t)r * h, h);
   }
+  uint32_t emax = 0;
+  for (int s = 0; s < slots; s++) emax = idx9[s] > emax ? idx9[s] : emax;
+  int* list = (int*)malloc(sizeof(int) * (size_t)slots);
+  double* xs = (double*)malloc(sizeof(double) * (size_t)slots * h);
+  float* gu = (float*)malloc(sizeof(float) * (size_t)slots * 2 * m);
+  double* as = (double*)malloc(sizeof(double) * (size_t)slots * m);
+  for (uint32_t e = 0; e <= emax; e++) {
+    int cnt = 0;
+    for (int s = 0; s < slots; s++)
+      if (idx9[s] == e) list[cnt++] = s;
+    if (!cnt) continue;
+    for (int j = 0; j < cnt; j++)
+      for (int i = 0; i < h; i++) xs[(int64_t)j * h + i] = (double)xh[(int64_t)(list[j] / 9) * h + i];
+    mx_expert_rows(gu_codes + (int64_t)e * 2 * m * (h / 2), gu_scales + (int64_t)e * 2 * m * (h / 32), h, 2 * m, xs,
+                   cnt, gu);
+    for (int j = 0; j < cnt; j++) {
+      float* g = gu + (int64_t)j * 2 * m;
+      float* a = (float*)malloc(sizeof(float) * (size_t)m);
+      orc_hadamard128(g, m);
+      orc_hadamard128(g + m, m);
+      for (int i = 0; i < m; i++) {
+        float gv = g[i] * f16_to_f32(out_g[e * m + i]), uv = g[m + i] * f16_to_f32(out_u[e * m + i]);
+        a[i] = orc_swiglu_bf16(gv, uv) * f16_to_f32(in_d[e * m + i]);
+      }
+      orc_hadamard128(a, m);
+      for (int i = 0; i < m; i++) as[(int64_t)j * m + i] = (double)a[i];
+      free(a);
+    }
+    float* v = (float*)malloc(sizeof(float) * (size_t)cnt * h);
+    mx_expert_rows(d_codes + (int64_t)e * h * (m / 2), d_scales + (int64_t)e * h * (m / 32), m, h, as, cnt, v);
+    for (int j = 0; j < cnt; j++) {
+      float* vj = v + (int64_t)j * h;
+      orc_hadamard128(vj, h);
+      float* dst = y + (int64_t)list[j] * h;
+      for (int i = 0; i < h; i++) dst[i] = round_bf16(vj[i] * f16_to_f32(out_d[e * h + i]));
+    }
+    free(v);
+  }
+  free(list); free(xs); free(gu); free(as); free(xh);
   if (values)
     for (int64_t i = 0; i < (int64_t)slots * h; i++) values[i] = f32_to_bf16(y[i]);
   for (int r = 0; r < rows; r++)
