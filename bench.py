@@ -370,11 +370,8 @@ def bench_stack(args):
     n = 20
     calls, x = [], synth.activations(dev, args.seed + 4000, 1)[0].contiguous()
     for i in range(n):
-        lay = ExpertLayer(**synth.k4_layer(dev, args.seed + 101 * i), hidden=H, intermediate=M)
-        w, bias = synth.router(dev, args.seed + 101 * i, zipf=True)
-        g = torch.Generator(device=dev)
-        g.manual_seed(args.seed + 7 * i)
-        norm = (0.5 + torch.rand(H, generator=g, device=dev)).to(torch.bfloat16)
+        spec, w, bias, norm = synth.stack_layer(dev, args.seed, i)
+        lay = ExpertLayer(**spec, hidden=H, intermediate=M)
         c = lay.prepare_layer_decode(x, norm, w, bias)
         calls.append(c)
         x = c.out

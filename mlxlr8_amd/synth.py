@@ -113,3 +113,17 @@ def activations(device, seed, rows, hidden=HIDDEN, correlated=False):
         x = torch.randn((rows, hidden), generator=g)
     residual = torch.randn((rows, hidden), generator=g)
     return x.to(torch.bfloat16).to(device), residual.to(torch.bfloat16).to(device)
+
+
+def norm_weight(device, seed, hidden=HIDDEN):
+    """RMSNorm weight bf16 [hidden] ~ U(0.5, 1.5)."""
+    g = _gen(device, seed)
+    return (0.5 + torch.rand(hidden, generator=g, device=device)).to(torch.bfloat16)
+
+
+def stack_layer(device, seed, index, hidden=HIDDEN, intermediate=INTER):
+    """Layer `index` of the 20-layer K4 decode stack: independently seeded experts, a Zipf-skewed
+    router bias and an RMSNorm weight.  Returns (k4_layer dict, router weight, bias, norm weight)."""
+    lay = k4_layer(device, seed + 101 * index, hidden, intermediate)
+    w, bias = router(device, seed + 101 * index, hidden, zipf=True)
+    return lay, w, bias, norm_weight(device, seed + 7 * index, hidden)
