@@ -152,49 +152,81 @@ class ExpertLayer:
 
 
 # ---------------------------------------------------------------- checkpoint loading
-def layer_arrays(path, number):
-    """Host arrays of one up1 layer (exlr8/experts.py:80-131): ``(k, hidden, intermediate, packed,
-    scales)`` with ``packed[p]`` = routed experts then the shared expert (uint8) and ``scales[p]`` =
-    (in, out) fp16 [257, features]: gate/up in = su_block per 128-block x signs.in, out = svh;
-    down in = suh, out = sv_block per 128-block x signs.out."""
+#
+# The up1 expert checkpoint (the reference's layout, README.md:62-72 and exlr8/experts.py:77-131):
+#   manifests/exlr8-manifest-up1.json     {"name": "up1", "layers": {"<n>": plan}}; every trellis
+#                                          width listed in a layer's plan must be that layer's K
+#   experts/exlr8-layer-<nnn>.k<K>.safetensors    trellis.<p> (256 routed experts, concatenated)
+#                                                  and shared.trellis.<p> (the shared expert)
+#   experts/exlr8-layer-<nnn>.index.safetensors   signs.in [hidden], signs.out [hidden] (int8),
+#                                                  per projection a per-128-block magnitude and a
+#                                                  per-channel vector, routed (k<K>.*) and shared
+#                                                  (shared.k<K>.*)
+# Every layer is K4 except the multi-token-prediction layer 78, which is K3.
+
+MTP_LAYER, MTP_WIDTH, MAIN_WIDTH = 78, 3, 4
+
+# Per projection: (block tensor, channel tensor, signs tensor, side the block vector scales).
+# The block vector, repeated over its 128 channels and signed, is the in-scale of gate/up and the
+# out-scale of down; the channel vector is the other side (exlr8/experts.py:99-115).
+SIDE_VECTORS = {
+    "gate": ("su_block", "svh", "signs.in", "in"),
+    "up": ("su_block", "svh", "signs.in", "in"),
+    "down": ("sv_block", "suh", "signs.out", "out"),
+}
+
+
+def _widths(node):
+    """Every trellis width mentioned anywhere in a manifest layer plan."""
+    if isinstance(node, dict):
+        return set().union(*(_widths(v) for v in node.values())) if node else set()
+    if isinstance(node, (list, tuple)):
+        return set().union(*(_widths(v) for v in node)) if node else set()
+    return {int(node)}
+
+
+def _manifest(path):
     import json
+    manifest = json.loads((path / "manifests" / "exlr8-manifest-up1.json").read_text())
+    if manifest.get("name") != "up1":
+        raise ValueError("This loader requires the up1 manifest")
+    return manifest
+
+
+def layer_arrays(path, number):
+    """Host arrays of up1 layer `number`: ``(k, hidden, intermediate, packed, scales)``.
+
+    ``packed[p]`` is uint8 [257 * expert_bytes] (routed experts, then the shared expert);
+    ``scales[p]`` = (in_scale, out_scale) fp16 [257, features] built from SIDE_VECTORS.
+    """
     from pathlib import Path
 
     import numpy as np
 
-    from .weights import SafeTensorFile
+    from .weights import SafetensorsFile
     path = Path(path)
-    manifest = json.loads((path / "manifests/exlr8-manifest-up1.json").read_text())
-    if manifest["name"] != "up1":
-        raise ValueError("This loader requires the up1 manifest")
-    plan = manifest["layers"][str(number)]
-    widths = {v for rows in (plan["gate"], plan["up"]) for row in rows for v in row}
-    widths.update(plan["down"])
-    widths.update(plan["shared"]["gate"])
-    widths.update(plan["shared"]["up"])
-    widths.add(plan["shared"]["down"])
-    k = 3 if number == 78 else 4
+    k = MTP_WIDTH if number == MTP_LAYER else MAIN_WIDTH
+    widths = _widths(_manifest(path)["layers"][str(number)])
     if widths != {k}:
         raise ValueError(f"Layer {number} is not uniform K{k}")
-    directory = path / "experts"
-    weights = SafeTensorFile(directory / f"exlr8-layer-{number:03d}.k{k}.safetensors")
-    index = SafeTensorFile(directory / f"exlr8-layer-{number:03d}.index.safetensors")
-    hidden = index.header["signs.in"]["shape"][0]
-    intermediate = index.header[f"k{k}.gate.svh"]["shape"][-1]
-    signs_in = index.raw("signs.in").astype(np.float16)
-    signs_out = index.raw("signs.out").astype(np.float16)
-    scales, packed = {}, {}
-    for projection in ("gate", "up", "down"):
-        down = projection == "down"
-        block_name, channel_name = ("sv_block", "suh") if down else ("su_block", "svh")
-        block = np.concatenate([index.raw(f"k{k}.{projection}.{block_name}"),
-                                index.raw(f"shared.k{k}.{projection}.{block_name}")])
-        channel = np.concatenate([index.raw(f"k{k}.{projection}.{channel_name}"),
-                                  index.raw(f"shared.k{k}.{projection}.{channel_name}")])
-        hidden_scale = np.repeat(block, 128, axis=-1) * (signs_out if down else signs_in)
-        scales[projection] = (channel, hidden_scale) if down else (hidden_scale, channel)
-        packed[projection] = np.concatenate([weights.raw("trellis." + projection),
-                                             weights.raw("shared.trellis." + projection)])
+    stem = path / "experts" / f"exlr8-layer-{number:03d}"
+    trellis = SafetensorsFile(f"{stem}.k{k}.safetensors")
+    index = SafetensorsFile(f"{stem}.index.safetensors")
+    hidden = index.shape("signs.in")[0]
+    intermediate = index.shape(f"k{k}.gate.svh")[-1]
+    signs = {name: index.array(name).astype(np.float16) for name in ("signs.in", "signs.out")}
+
+    def both(name):  # routed rows then the shared expert's row
+        return np.concatenate([index.array(f"k{k}.{name}"), index.array(f"shared.k{k}.{name}")])
+
+    packed, scales = {}, {}
+    for projection, (block, channel, sign, block_side) in SIDE_VECTORS.items():
+        mags = both(f"{projection}.{block}")                       # [257, features / 128]
+        expanded = (mags[:, :, None] * np.ones(128, np.float16)).reshape(len(mags), -1) * signs[sign]
+        per_channel = both(f"{projection}.{channel}")
+        scales[projection] = (expanded, per_channel) if block_side == "in" else (per_channel, expanded)
+        packed[projection] = np.concatenate([trellis.array(f"trellis.{projection}"),
+                                             trellis.array(f"shared.trellis.{projection}")])
     return k, hidden, intermediate, packed, scales
 
 
@@ -204,13 +236,10 @@ class ExpertStore:
     ``resident=False`` loads resident as well (the reference's SSD cache is not built)."""
 
     def __init__(self, path, cache_gib=32, resident=False, optimize=True, device=None):
-        import json
         from pathlib import Path
         self.path = Path(path)
         self.resident, self.optimize = True, optimize
-        self.manifest = json.loads((self.path / "manifests/exlr8-manifest-up1.json").read_text())
-        if self.manifest["name"] != "up1":
-            raise ValueError("This loader requires the up1 manifest")
+        self.manifest = _manifest(self.path)
         if cache_gib < 0:
             raise ValueError("cache_gib must be nonnegative")
         self.limit = int(cache_gib * 1024 ** 3)
@@ -229,28 +258,32 @@ class ExpertStore:
                 "resident_bytes": self.resident_bytes, "hits": self.hits, "misses": self.misses}
 
 
+def _nbytes(t):
+    return 0 if t is None else t.numel() * t.element_size()
+
+
 def _from_store(cls, store, number):
-    """ExpertLayer of layer `number` of an ExpertStore, resident on the store's device; with
-    ``optimize``, K4 and the GLM-5.3 shape (6144, 2048) its experts are converted to joined MXFP4
-    and served by them (exlr8/experts.py:132-148); K3 layers stay trellis."""
+    """ExpertLayer of layer `number` of an ExpertStore, resident on the store's device.  With
+    ``optimize``, K4 and the GLM-5.3 shape (6144, 2048) the experts are served as joined MXFP4 and
+    the trellis tensors and gate/up in-scales are released (exlr8/experts.py:132-148); K3 layers stay
+    trellis.  The store counts the bytes of what stays resident."""
     k, hidden, intermediate, packed, scales = layer_arrays(store.path, number)
     dev = store.device
     layer = cls({p: torch.from_numpy(a).to(dev) for p, a in packed.items()},
                 {p: tuple(torch.from_numpy(v).to(dev) for v in pair) for p, pair in scales.items()},
                 hidden, intermediate, k=k, number=number)
     layer.store = store
-    store.resident_bytes += sum(a.nbytes for a in packed.values())
-    store.resident_bytes += sum(v.nbytes for pair in scales.values() for v in pair)
     if store.optimize and k == 4 and (hidden, intermediate) == (6144, 2048):
         from .joined_mxfp4 import JoinedMXFP4
         layer.affine = JoinedMXFP4(layer)
-        store.resident_bytes += (sum(a.numel() * a.element_size() for v in layer.affine.weights.values() for a in v)
-                                 - sum(a.nbytes for a in packed.values()) + layer.affine.unit.numel() * 2)
         for projection in ("gate", "up"):
-            incoming, outgoing = layer.scales[projection]
-            store.resident_bytes -= incoming.numel() * incoming.element_size()
-            layer.scales[projection] = (None, outgoing)
+            layer.scales[projection] = (None, layer.scales[projection][1])
         del layer.packed
+        resident = [t for pair in layer.affine.weights.values() for t in pair] + [layer.affine.unit]
+    else:
+        resident = list(layer.packed.values())
+    resident += [t for pair in layer.scales.values() for t in pair]
+    store.resident_bytes += sum(_nbytes(t) for t in resident)
     return layer
 
 

@@ -69,7 +69,7 @@ def test_moe_block_prefill_mxfp4_every_row(cuda, orc):
     row_err = np.linalg.norm(got - wantf, axis=1) / np.linalg.norm(wantf, axis=1)
     say(f"  experts used={int((counts > 0).sum())} max tokens/expert={counts[:256].max()} rel_l2={err:.3e} "
         f"moe-part={err_moe:.3e} worst row={row_err.max():.3e} routing mismatches={int(mism.sum())}")
-    assert err <= 1e-3 and err_moe <= 1e-2
+    assert err <= 1e-3 and err_moe <= 1e-3
     assert row_err.max() <= 2e-3
 
 
@@ -110,7 +110,7 @@ def test_moe_block_k4_grouped_rows(cuda, orc):
     got, wantf, r = bits_to_f32(bf16_bits(out)), bits_to_f32(want), bits_to_f32(bf16_bits(res))
     err, err_moe = rel_l2(got, wantf), rel_l2(got - r, wantf - r)
     say(f"  rel_l2={err:.3e} moe-part={err_moe:.3e}")
-    assert err <= 1e-3 and err_moe <= 1e-2
+    assert err <= 1e-3 and err_moe <= 1e-3
 
 
 def test_resident_decode_never_synchronises(cuda):

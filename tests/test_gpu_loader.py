@@ -1,5 +1,6 @@
-"""ExpertStore / ExpertLayer.from_store on the MI355X with the reference's synthetic up1 checkpoint
-(its tests/test_experts.py:13-48 format and resident-bytes known answer)."""
+"""ExpertStore / ExpertLayer.from_store on the MI355X with a synthetic layer in the up1 on-disk
+layout (hidden = intermediate = 128) and the reference's resident-bytes known answer for that shape
+(its tests/test_experts.py:116)."""
 import sys
 
 import numpy as np
@@ -7,7 +8,7 @@ import pytest
 import torch
 
 from conftest import bf16_bits, bits_to_f32, f16_bits, rel_l2
-from loader_fixture import write_checkpoint
+from loader_fixture import write_up1_layer
 
 pytestmark = pytest.mark.gpu
 
@@ -21,7 +22,7 @@ def say(*a):
 def test_store_layer_resident_bytes_and_forward(cuda, orc, tmp_path, rows):
     from mlxlr8_amd.experts import ExpertStore
     say(f"case: store layer rows={rows}")
-    raw, index = write_checkpoint(tmp_path)
+    raw, index = write_up1_layer(tmp_path)
     store = ExpertStore(tmp_path, resident=True)
     layer = store.layer(3)
     assert store.layer(3) is layer
@@ -54,7 +55,7 @@ def test_store_k3_layer_forward(cuda, orc, tmp_path, rows):
     """Layer 78 (K3): resident trellis experts (no MXFP4 conversion), values against the oracle."""
     from mlxlr8_amd.experts import ExpertStore
     say(f"case: store K3 layer 78 rows={rows}")
-    write_checkpoint(tmp_path, layer=78, widths=3, width=3)
+    write_up1_layer(tmp_path, layer=78, k=3)
     store = ExpertStore(tmp_path, resident=True, optimize=True)
     layer = store.layer(78)
     assert layer.k == 3 and layer.affine is None

@@ -94,7 +94,7 @@ def _check_layer(orc, layer, hidden, inter, x_bits, attn_bits, got_out, got_ids,
     err, err_moe = rel_l2(got, wantf), rel_l2(got - res, wantf - res)
     say(f"  {tag}: rel_l2={err:.3e} moe-part rel_l2={err_moe:.3e} routing mismatches={int(mism.sum())}")
     assert err <= 1e-3
-    assert err_moe <= 1e-2
+    assert err_moe <= 1e-3
 
 
 def test_layer_decode_small_width(cuda, orc):

@@ -43,7 +43,7 @@ def test_stack_20_layers_every_layer_vs_oracle(cuda, orc):
         err, err_moe = rel_l2(got, wantf), rel_l2(got - r, wantf - r)
         say(f"  layer {i:2d}: experts {sorted(set(ids.ravel().tolist()))[:3]}... rel_l2={err:.3e} "
             f"moe-part={err_moe:.3e} routing mismatches={int(mism.sum())}")
-        assert err <= 1e-3 and err_moe <= 1e-2
+        assert err <= 1e-3 and err_moe <= 1e-3
         h = out
     # second pass through the prepared (one call per layer) stack: bit-identical final output
     calls, xin = [], x.clone()
