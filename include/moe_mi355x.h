@@ -170,6 +170,22 @@ int moe_mxfp4_moe_decode(const uint16_t* x, const uint16_t* residual, int rows, 
 /* Workspace bytes for the three MXFP4 decode entry points above. */
 size_t moe_mxfp4_workspace_bytes(int hidden, int intermediate);
 
+/* moe_mxfp4_moe_decode with no workspace argument and no allocation of any kind: the workspace is
+ * the library's fixed per-GPU scratch array (4 MiB, held by each GPU the library runs on until the
+ * process ends; its address is resolved on the first call on a device, so call moe_init() and this
+ * entry once before capturing it in a graph).  Its counters are cleared by a fill kernel at the start
+ * of every call.  Shapes whose workspace exceeds the scratch are rejected with MOE_ENOTSUP.  Every
+ * call on one GPU shares that GPU's scratch: calls that overlap on one GPU (several streams or
+ * threads) race.
+ * No counterpart in the reference: for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). */
+int moe_mxfp4_moe_decode_noalloc(const uint16_t* x, const uint16_t* residual, int rows, const float* router_w,
+                                 const float* bias, const uint8_t* gate_up_codes, const uint8_t* gate_up_scales,
+                                 const uint8_t* down_codes, const uint8_t* down_scales, int64_t experts,
+                                 const uint16_t* unit, const uint16_t* out_gate, const uint16_t* out_up,
+                                 const uint16_t* in_down, const uint16_t* out_down, int hidden, int intermediate,
+                                 uint16_t* out, uint32_t* indices, float* scores, moe_stream_t stream);
+
 /* ---------------------------------------------------------------- profiling */
 
 /* Arm HIP events (hipEvent_t handles, NULL entries skipped) for the next K4 layer call made by

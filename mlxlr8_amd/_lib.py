@@ -45,6 +45,8 @@ _SIGNATURES = {
     "moe_mxfp4_moe_decode": (_I32, [_VP, _VP, _I32, _VP, _VP, _VP, _VP, _VP, _VP, _I64] + [_VP] * 5
                              + [_I32, _I32, _VP, _VP, _VP, _VP, _SZ, _VP]),
     "moe_mxfp4_workspace_bytes": (_SZ, [_I32, _I32]),
+    "moe_mxfp4_moe_decode_noalloc": (_I32, [_VP, _VP, _I32, _VP, _VP, _VP, _VP, _VP, _VP, _I64] + [_VP] * 5
+                                     + [_I32, _I32, _VP, _VP, _VP, _VP]),
     "moe_segment_table": (_I32, [_VP, _I32, _I32, _I32, _VP, _VP, _VP, _VP, _I32, _VP, _VP]),
     "moe_mxfp4_prefill": (_I32, [_VP, _VP, _I32, _VP, _VP, _VP, _VP, _VP, _VP, _I64] + [_VP] * 5
                           + [_I32, _I32, _VP, _VP, _VP, _VP, _SZ, _VP]),

@@ -16,6 +16,8 @@
 // K4 path.
 #include <hip/hip_runtime.h>
 
+#include <mutex>
+
 #include "moe_device.h"
 #include "moe_host.h"
 #include "moe_plan.h"
@@ -356,11 +358,11 @@ int mx_blocks(int64_t rows_total, int n) {
   return g;
 }
 
-int mx_common(const uint16_t* x, const uint32_t* ids, const float* scores, const uint16_t* residual, int rows,
-              int slots_per_row, const uint8_t* gu_codes, const uint8_t* gu_scales, const uint8_t* d_codes,
-              const uint8_t* d_scales, int64_t experts, const uint16_t* unit, const uint16_t* out_gate,
-              const uint16_t* out_up, const uint16_t* in_down, const uint16_t* out_down, int h, int m,
-              uint16_t* values, uint16_t* out, void* workspace, size_t workspace_bytes, hipStream_t s) {
+// Argument checks of the MXFP4 decode MLP (no launch).
+int mx_check(const uint16_t* x, const uint32_t* ids, int rows, int slots_per_row, const uint8_t* gu_codes,
+             const uint8_t* gu_scales, const uint8_t* d_codes, const uint8_t* d_scales, int64_t experts,
+             const uint16_t* unit, const uint16_t* out_gate, const uint16_t* out_up, const uint16_t* in_down,
+             const uint16_t* out_down, int h, int m, const void* workspace, size_t workspace_bytes) {
   MOE_ARG(x && ids && gu_codes && gu_scales && d_codes && d_scales && unit && out_gate && out_up && in_down && out_down,
           "null pointer argument");
   MOE_ARG(h == 6144 && m == 2048, "this build's MXFP4 kernels are specialised for hidden 6144, intermediate 2048");
@@ -368,11 +370,19 @@ int mx_common(const uint16_t* x, const uint32_t* ids, const float* scores, const
           "rows*slots must be in 1..%d", kMaxUnits);
   MOE_ARG(experts >= 1 && experts <= 257, "expert count must be in 1..257");
   MOE_ARG(workspace != nullptr, "workspace must not be NULL");
-  MxWorkspace w = mx_carve(nullptr, h, m);
-  if (workspace_bytes < w.bytes) return fail(MOE_EWORKSPACE, "workspace too small: %zu < %zu", workspace_bytes, w.bytes);
-  int rc = ensure_device_ready();
-  if (rc) return rc;
-  w = mx_carve(workspace, h, m);
+  const size_t need = mx_carve(nullptr, h, m).bytes;
+  if (workspace_bytes < need) return fail(MOE_EWORKSPACE, "workspace too small: %zu < %zu", workspace_bytes, need);
+  return MOE_OK;
+}
+
+// The MXFP4 decode MLP (gate/up GEMV + gate finish, down GEMV + values or combine) on a checked
+// workspace.
+int mx_launch(const uint16_t* x, const uint32_t* ids, const float* scores, const uint16_t* residual, int rows,
+              int slots_per_row, const uint8_t* gu_codes, const uint8_t* gu_scales, const uint8_t* d_codes,
+              const uint8_t* d_scales, int64_t experts, const uint16_t* unit, const uint16_t* out_gate,
+              const uint16_t* out_up, const uint16_t* in_down, const uint16_t* out_down, int h, int m,
+              uint16_t* values, uint16_t* out, void* workspace, hipStream_t s) {
+  const MxWorkspace w = mx_carve(workspace, h, m);
   const int slots = rows * slots_per_row;
 
   MxArgs g{};
@@ -393,7 +403,6 @@ int mx_common(const uint16_t* x, const uint32_t* ids, const float* scores, const
   d.out_down = out_down;
   const dim3 grid(mx_blocks((int64_t)slots * h, h) * MOE_MX_DOWN_BPC);
   if (out) {
-    MOE_ARG(slots_per_row == kSlots && scores && residual, "the combined finish needs 9 slots, scores and residual");
     d.scores = scores; d.residual = residual; d.out = out;
     hipLaunchKernelGGL((mx_gemv_kernel<MX_DOWN_COMBINE, 1>), grid, dim3(kMxThreads), 0, s, d);
   } else {
@@ -404,6 +413,57 @@ int mx_common(const uint16_t* x, const uint32_t* ids, const float* scores, const
   return MOE_OK;
 }
 
+int mx_common(const uint16_t* x, const uint32_t* ids, const float* scores, const uint16_t* residual, int rows,
+              int slots_per_row, const uint8_t* gu_codes, const uint8_t* gu_scales, const uint8_t* d_codes,
+              const uint8_t* d_scales, int64_t experts, const uint16_t* unit, const uint16_t* out_gate,
+              const uint16_t* out_up, const uint16_t* in_down, const uint16_t* out_down, int h, int m,
+              uint16_t* values, uint16_t* out, void* workspace, size_t workspace_bytes, hipStream_t s) {
+  int rc = mx_check(x, ids, rows, slots_per_row, gu_codes, gu_scales, d_codes, d_scales, experts, unit, out_gate,
+                    out_up, in_down, out_down, h, m, workspace, workspace_bytes);
+  if (rc) return rc;
+  if (out) MOE_ARG(slots_per_row == kSlots && scores && residual, "the combined finish needs 9 slots, scores and residual");
+  if ((rc = ensure_device_ready())) return rc;
+  return mx_launch(x, ids, scores, residual, rows, slots_per_row, gu_codes, gu_scales, d_codes, d_scales, experts, unit,
+                   out_gate, out_up, in_down, out_down, h, m, values, out, workspace, s);
+}
+
+// Zero two word ranges (counter regions) with one block.
+__global__ __launch_bounds__(256) void zero_counters_kernel(int32_t* a, int na, int32_t* b, int nb) {
+  for (int i = threadIdx.x; i < na; i += 256) a[i] = 0;
+  for (int i = threadIdx.x; i < nb; i += 256) b[i] = 0;
+}
+
+}  // namespace
+}  // namespace moe
+
+// ---------------------------------------------------------------- allocation-free decode block
+// moe_mxfp4_moe_decode_noalloc keeps its workspace in this fixed device array (one copy per GPU,
+// held until the process ends).  Host code never passes the array's name to a kernel: the
+// per-device address comes from hipGetSymbolAddress on the entry point's first call on a device.
+constexpr size_t kScratchBytes = (size_t)4 << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+namespace moe {
+namespace {
+std::mutex g_scratch_mutex;
+void* g_scratch_addr[64];  // per device
+
+int scratch_address(void** out) {
+  int dev = 0;
+  MOE_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= 64) return fail(MOE_ENOTSUP, "device index %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_addr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(e != hipSuccess ? (int)e : MOE_ENOTSUP, "hipGetSymbolAddress(scratch) failed: %s",
+                  hipGetErrorString(e));
+    g_scratch_addr[dev] = p;
+  }
+  *out = g_scratch_addr[dev];
+  return MOE_OK;
+}
 }  // namespace
 }  // namespace moe
 
@@ -438,7 +498,41 @@ int moe_mxfp4_mlp_finish(const uint16_t* x, const uint32_t* ids, const float* sc
                    workspace_bytes, (hipStream_t)stream);
 }
 
-// Router GEMV + route + joined-MXFP4 MLP + combine for decode rows in one call.
+// Router GEMV + route + joined-MXFP4 MLP + combine for decode rows in one call on a checked
+// workspace (every argument is validated before the first launch).
+static int mx_decode_block(const uint16_t* x, const uint16_t* residual, int rows, const float* router_w,
+                           const float* bias, const uint8_t* gate_up_codes, const uint8_t* gate_up_scales,
+                           const uint8_t* down_codes, const uint8_t* down_scales, int64_t experts, const uint16_t* unit,
+                           const uint16_t* out_gate, const uint16_t* out_up, const uint16_t* in_down,
+                           const uint16_t* out_down, int hidden, int intermediate, uint16_t* out, uint32_t* indices,
+                           float* scores, void* workspace, size_t workspace_bytes, hipStream_t s,
+                           bool clear_counters = false) {
+  MOE_ARG(x && residual && router_w && bias && out && workspace, "null pointer argument");
+  MOE_ARG(rows >= 1 && rows <= kMaxRows, "rows must be in 1..%d", kMaxRows);
+  MOE_ARG(experts == 257, "the routed decode block needs 256 routed experts plus the shared expert (got %lld)",
+          (long long)experts);
+  MxWorkspace w = mx_carve(workspace, hidden > 0 ? hidden : 1, intermediate > 0 ? intermediate : 1);
+  uint32_t* ids = indices ? indices : w.ids;
+  float* sc = scores ? scores : w.scores;
+  int rc = mx_check(x, ids, rows, kSlots, gate_up_codes, gate_up_scales, down_codes, down_scales, experts, unit,
+                    out_gate, out_up, in_down, out_down, hidden, intermediate, workspace, workspace_bytes);
+  if (rc) return rc;
+  if ((rc = ensure_device_ready())) return rc;
+  if (clear_counters) {
+    // counters that must start at zero: the router's arrival counter and the MLP's block and group
+    // counters (a fill kernel, not a memset node, so the call can be captured in a graph)
+    hipLaunchKernelGGL(zero_counters_kernel, dim3(1), dim3(256), 0, s, w.counter_blk,
+                       (int)((reinterpret_cast<char*>(w.rowout) - reinterpret_cast<char*>(w.counter_blk)) / 4),
+                       w.router_counter, 64);
+    MOE_HIP(hipGetLastError());
+  }
+  rc = moe_router_fused_plan(x, router_w, bias, rows, hidden, 257, w.logits, ids, sc, w.plan, w.router_counter, s);
+  if (rc) return rc;
+  return mx_launch(x, ids, sc, residual, rows, kSlots, gate_up_codes, gate_up_scales, down_codes, down_scales,
+                   experts, unit, out_gate, out_up, in_down, out_down, hidden, intermediate, nullptr, out, workspace,
+                   s);
+}
+
 int moe_mxfp4_moe_decode(const uint16_t* x, const uint16_t* residual, int rows, const float* router_w,
                          const float* bias, const uint8_t* gate_up_codes, const uint8_t* gate_up_scales,
                          const uint8_t* down_codes, const uint8_t* down_scales, int64_t experts,
@@ -446,24 +540,31 @@ int moe_mxfp4_moe_decode(const uint16_t* x, const uint16_t* residual, int rows, 
                          const uint16_t* in_down, const uint16_t* out_down, int hidden, int intermediate,
                          uint16_t* out, uint32_t* indices, float* scores, void* workspace, size_t workspace_bytes,
                          moe_stream_t stream) {
-  MOE_ARG(x && residual && router_w && bias && out && workspace, "null pointer argument");
-  MOE_ARG(rows >= 1 && rows <= kMaxRows, "rows must be in 1..%d", kMaxRows);
-  MOE_ARG(experts == 257, "the routed decode block needs 256 routed experts plus the shared expert (got %lld)",
-          (long long)experts);
+  return mx_decode_block(x, residual, rows, router_w, bias, gate_up_codes, gate_up_scales, down_codes, down_scales,
+                         experts, unit, out_gate, out_up, in_down, out_down, hidden, intermediate, out, indices, scores,
+                         workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+// The decode block of moe_mxfp4_moe_decode with its workspace in the library's fixed per-device
+// scratch array instead of a caller buffer: no allocation of any kind.  Shapes whose workspace
+// exceeds the scratch are rejected.  Calls on one GPU share the scratch: overlapping calls race.
+int moe_mxfp4_moe_decode_noalloc(const uint16_t* x, const uint16_t* residual, int rows, const float* router_w,
+                                 const float* bias, const uint8_t* gate_up_codes, const uint8_t* gate_up_scales,
+                                 const uint8_t* down_codes, const uint8_t* down_scales, int64_t experts,
+                                 const uint16_t* unit, const uint16_t* out_gate, const uint16_t* out_up,
+                                 const uint16_t* in_down, const uint16_t* out_down, int hidden, int intermediate,
+                                 uint16_t* out, uint32_t* indices, float* scores, moe_stream_t stream) {
   MOE_ARG(hidden > 0 && intermediate > 0, "hidden and intermediate must be positive");
-  MxWorkspace w = mx_carve(nullptr, hidden, intermediate);
-  if (workspace_bytes < w.bytes) return fail(MOE_EWORKSPACE, "workspace too small: %zu < %zu", workspace_bytes, w.bytes);
-  int rc = ensure_device_ready();
+  const size_t need = mx_carve(nullptr, hidden, intermediate).bytes;
+  if (need > kScratchBytes)
+    return fail(MOE_ENOTSUP, "hidden %d / intermediate %d need %zu bytes of scratch; the fixed scratch holds %zu",
+                hidden, intermediate, need, kScratchBytes);
+  void* ws = nullptr;
+  int rc = scratch_address(&ws);
   if (rc) return rc;
-  w = mx_carve(workspace, hidden, intermediate);
-  const hipStream_t s = (hipStream_t)stream;
-  uint32_t* ids = indices ? indices : w.ids;
-  float* sc = scores ? scores : w.scores;
-  rc = moe_router_fused_plan(x, router_w, bias, rows, hidden, 257, w.logits, ids, sc, w.plan, w.router_counter, s);
-  if (rc) return rc;
-  return mx_common(x, ids, sc, residual, rows, kSlots, gate_up_codes, gate_up_scales, down_codes, down_scales, experts,
-                   unit, out_gate, out_up, in_down, out_down, hidden, intermediate, nullptr, out, workspace,
-                   workspace_bytes, s);
+  return mx_decode_block(x, residual, rows, router_w, bias, gate_up_codes, gate_up_scales, down_codes, down_scales,
+                         experts, unit, out_gate, out_up, in_down, out_down, hidden, intermediate, out, indices, scores,
+                         ws, kScratchBytes, (hipStream_t)stream, true);
 }
 
 }  // extern "C"
