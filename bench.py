@@ -35,9 +35,6 @@ TRELLIS = H * M // 2                      # bytes per expert projection (K4 = 4 
 # Algorithmic bytes per token (batch 1): 9 experts x 3 projections of trellis + router weight +
 # side vectors + bias + activations in/out ("Measurement").
 BYTES_TOKEN = 9 * 3 * TRELLIS + 256 * H * 4 + 9 * 3 * (H + M) * 2 + 256 * 4 + 3 * H * 2
-# Dominant kernel: gate/up GEMV of 9 experts (2 projections each) + its side vectors and input.
-BYTES_GATEUP = 9 * 2 * TRELLIS + 9 * 2 * H * 2 + 9 * 2 * M * 2 + 9 * M * 2 + H * 2
-BYTES_DOWN = 9 * TRELLIS + 9 * M * 4 + 9 * H * 2 + 2 * H * 2
 HBM_PEAK_GBPS = 8000.0
 METRIC = "MoE-layer decode µs/token + HBM GB/s (K4 trellis, b=1); prefill tok/s"
 
@@ -63,8 +60,8 @@ def parse():
 
 
 def traffic_from_profiles():
-    """HBM bytes per gate/up launch from the committed rocprofv3 PMC summary, if present."""
-    path = ROOT / "profiles" / "k4_gateup_b1_pmc.txt"
+    """HBM bytes per layer launch from the committed rocprofv3 PMC summary, if present."""
+    path = ROOT / "profiles" / "k4_layer_b1_pmc.txt"
     if not path.exists():
         return None
     for line in path.read_text().splitlines():
@@ -159,8 +156,9 @@ def main():
     per_step_ms = start.elapsed_time(end) / n
     us_tok = per_step_ms * 1e3
 
-    # per-kernel durations: a second pass that records HIP events on the launch stream between the
-    # layer's kernels (the events add gaps, so this pass is not the headline time)
+    # duration of the layer kernel itself: a second pass that records HIP events on the launch
+    # stream around the one cooperative launch (marks 1 and 3 of moe_profile_events); the events
+    # add gaps, so this pass is not the headline time
     import ctypes
     ne = min(n, 100)
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(ne)]
@@ -175,10 +173,8 @@ def main():
         L.moe_profile_events(handles[i], 4)
         step(args.warmup + n + i)
     torch.cuda.synchronize()
-    router_us = sum(evs[i][0].elapsed_time(evs[i][1]) for i in range(ne)) / ne * 1e3
-    gateup_us = sum(evs[i][1].elapsed_time(evs[i][2]) for i in range(ne)) / ne * 1e3
-    down_us = sum(evs[i][2].elapsed_time(evs[i][3]) for i in range(ne)) / ne * 1e3
-    achieved = BYTES_GATEUP / (gateup_us * 1e-6) / 1e9
+    layer_us = sum(evs[i][1].elapsed_time(evs[i][3]) for i in range(ne)) / ne * 1e3
+    achieved = BYTES_TOKEN / (layer_us * 1e-6) / 1e9
     hbm = BYTES_TOKEN / (us_tok * 1e-6) / 1e9
     traffic = traffic_from_profiles()
 
@@ -205,11 +201,12 @@ def main():
         "hbm_GBps": round(hbm, 1),
         "hbm_frac": round(hbm / HBM_PEAK_GBPS, 4),
         "bytes_per_token": BYTES_TOKEN,
-        "kernels_us": {"router": round(router_us, 2), "gate_up": round(gateup_us, 2), "down": round(down_us, 2)},
-        "roofline": {"kernel": "k4_mfma_kernel<0,0,1,...> (fused gate/up decode GEMV, 9 experts)",
+        "kernels_us": {"k4_layer_kernel": round(layer_us, 2)},
+        "roofline": {"kernel": "k4_layer_kernel<1> (router, top-8, 9-unit gate/up and down decode GEMVs and "
+                               "combine in one cooperative launch)",
                      "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                     "algorithmic_bytes": BYTES_GATEUP},
+                     "algorithmic_bytes": BYTES_TOKEN},
         "wall_s": round(wall, 3),
     }
     if args.calibrate_copy:

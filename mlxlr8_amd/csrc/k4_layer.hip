@@ -1,0 +1,1022 @@
+// Fused K4 trellis MoE block for decode batches (1..8 token rows) on gfx950: router, shared expert,
+// routed experts and the weighted combine in ONE persistent launch.
+//
+// Reference semantics (paths relative to the reference root):
+//   router   logits = f32(x) @ W^T, sigmoid, bias-corrected top-8  exlr8/model.py:111-132,
+//                                                                   exlr8/metal/fast_router.metal:1-42
+//   prep     xh = H128(x * in_scale[e])                             exlr8/metal/fast_decode_prep.metal
+//   linear   inner = xh @ decode(packed_e)                          exlr8/metal/fast_decode_linear.metal
+//   gate fin a = H128(swiglu_T(H(g) * og, H(u) * ou) * in_down)     exlr8/metal/fast_decode_gate_finish.metal
+//   finish   T(H128(inner) * out_scale)                             exlr8/metal/fast_decode_finish.metal
+//   combine  routed sum in slot order, shared, residual             exlr8/metal/fast_decode_finish_fused.metal:52-61
+//
+// MI355X design.
+//   * Workers.  One block of kLW waves per CU; every wave takes work items from a queue until the
+//     list is exhausted.  The codebook table enters LDS once per launch (the first item's loads are
+//     already in flight while it is copied).
+//   * Items.  A part is 2 quads (8 KB of K4 weights): 128 input rows x 128 output columns of one
+//     (unit, projection, output block) -- exactly one H128 block of its input.  The list, in
+//     dependency order (an item only ever waits for items before it):
+//         [GU(0)] [router] [route] [GU(1)] [GF(0)] [GU(2)] [GF(1)] ... [GU(U-1)] [GF(U-2)] [GF(U-1)]
+//         [D(0)] [D(1)] [DF(0)] [D(2)] [DF(1)] ... [D(U-1)] [DF(U-2)] [DF(U-1)]
+//     Unit 0 is the shared expert (it needs no routing, so its gate/up parts run beside the
+//     router); GU(u) are unit u's gate/up parts, GF(u) its gate finishes (one per column block:
+//     the down input), D(u) its down parts, DF(u) its down finishes (one per output block; the
+//     last unit's also combine that output block of every row).
+//   * Queue.  The list is dealt round-robin over 8 sub-lists, one per XCD (block b serves sub-list
+//     b mod 8); a wave claims its next item with one atomic on its sub-list's counter a whole item
+//     ahead of use, so a wave that waited or finished something simply claims fewer items.  Any
+//     number of resident blocks makes progress: the lowest unfinished item is always held by a
+//     running wave and all its inputs come from lower items.
+//   * Hand-over without counters or fences.  Every value another wave reads (router logit slices,
+//     part partials, down inputs, slot outputs) is stored as one 64-bit word (value, tag), the tag
+//     being the launch's epoch; a consumer reloads until every word it needs carries the current
+//     tag.  Waits are bounded: an exhausted wait sets the error word and the wave continues.  The
+//     epoch lives in the workspace and advances when the last block leaves, so a replayed launch
+//     (the same arguments) never accepts its predecessor's words.  A stale word is mistaken for a
+//     current one only if exactly a multiple of 2^32 - 1 launches separate them with the word never
+//     rewritten in between.
+//   * Deterministic reductions: a finisher sums its parts' partials in part order; part boundaries
+//     depend only on the layer shape, so a token row gives the same bits alone or in an 8-row
+//     batch.  Router logits are summed over fixed input slices in slice order.
+//   * Per-wave pipeline: while quad 0 of an item is decoded, quad 1 streams in; while quad 1 is
+//     decoded, quad 0 and the input block of the next item stream in.  Partial stores are never
+//     waited for.
+//   * Decode: the piece decoder of the GEMVs (fp16 code table for single-token launches, E4M3 byte
+//     table for batches), fp16 MFMA with x split into hi and lo rows (k4_moe.hip).
+#include <hip/hip_runtime.h>
+
+#include "moe_device.h"
+#include "moe_host.h"
+#include "moe_plan.h"
+#include "route.h"
+
+namespace moe {
+
+#ifndef MOE_LAYER_WAVES
+#define MOE_LAYER_WAVES 12
+#endif
+// arithmetic codeword pairs per word (even, odd words of a piece) in the single-token decode
+#ifndef MOE_LAYER_ALU_EVEN
+#define MOE_LAYER_ALU_EVEN 1
+#endif
+#ifndef MOE_LAYER_ALU_ODD
+#define MOE_LAYER_ALU_ODD 2
+#endif
+
+constexpr int kLW = MOE_LAYER_WAVES;
+constexpr int kRouterSlice = 1024;  // router inputs per work item
+constexpr int kMaxRouteHidden = 8192;  // hidden size limit of the fused router
+constexpr int kSpinLimit = 1 << 14;  // polls of a bounded wait (with the backoff below: ~50 ms)
+constexpr int kXcds = 8;            // queue sub-lists
+constexpr int kQueueStride = 32;    // ints between sub-list counters (one 128 B line each)
+
+enum LayerFin { LFIN_VALUES = 0, LFIN_COMBINE = 1 };
+enum LayerFlag { LF_PLAN = 0, LF_ERROR = 1, LF_EXIT = 2, LF_EPOCH = 3, LF_COUNT = 8 };
+
+struct LayerWs {
+  Plan* plan;
+  int32_t* flags;        // LayerFlag words
+  int32_t* queue;        // [kXcds][kQueueStride] sub-list counters
+  uint64_t* logit_part;  // [kMaxRows][256][h / kRouterSlice] tagged
+  uint64_t* partial;     // [slot][3 (h/128)(m/128) parts][128] tagged
+  uint64_t* down_xh;     // [slot][m] tagged
+  uint64_t* yslot;       // [slot][h] tagged
+  size_t bytes;
+};
+
+struct LayerArgs {
+  const uint8_t* tab8;       // the device's E4M3 code table (64 KB)
+  const uint16_t* tab16;     // the same table as fp16 (128 KB)
+  const uint16_t* x;         // expert (and router) input [rows, h] bf16
+  const uint16_t* residual;  // [rows, h] bf16 (combine)
+  int rows;
+  int route;                 // 1: router items + plan on the device; 0: plan prebuilt from ids
+  const float* router_w;     // [256, h] fp32
+  const float* bias;         // [256] fp32
+  uint32_t* ids;             // route: out [rows, 9]
+  float* scores;             // route: out [rows, 8]; else the caller's [rows, 8] (combine)
+  const uint8_t* packed[3];  // gate, up (side 1), down (side 2)
+  const uint16_t* in_scale[3];
+  const uint16_t* out_scale[3];
+  int h, m;
+  int experts;               // experts per packed projection (ids are clamped below it)
+  int fin;
+  uint16_t* out;             // combine [rows, h]
+  uint16_t* values;          // values [slots, h]
+  LayerWs w;
+};
+
+// ---------------------------------------------------------------- coherent and tagged words
+__device__ __forceinline__ int ld_coh_i(const int32_t* p) {
+  return __hip_atomic_load(const_cast<int32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ void st_coh_i(int32_t* p, int v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ float ld_coh_f(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ uint64_t ld_tag(const uint64_t* p) {
+  return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ void st_tag(uint64_t* p, float v, uint32_t tag) {
+  __hip_atomic_store(p, (uint64_t)__float_as_uint(v) | ((uint64_t)tag << 32), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ bool has_tag(uint64_t w, uint32_t tag) { return (uint32_t)(w >> 32) == tag; }
+__device__ __forceinline__ float tag_value(uint64_t w) { return __uint_as_float((uint32_t)w); }
+__device__ __forceinline__ void set_error(const LayerArgs& a) {
+  if (lane_id() == 0) st_coh_i(a.w.flags + LF_ERROR, 1);
+}
+// One step of a bounded wait; false once the bound is exhausted (the error word is then set).
+// The pause doubles from 64 to 4096 clocks: waiting waves must leave the memory system to the
+// producers they wait for (hundreds of waves re-reading their inputs back to back starve them).
+__device__ __forceinline__ bool keep_waiting(const LayerArgs& a, int& spins) {
+  if (++spins >= kSpinLimit) {
+    set_error(a);
+    return false;
+  }
+  const int pauses = spins < 6 ? (1 << spins) : 64;
+  for (int k = 0; k < pauses; k++) __builtin_amdgcn_s_sleep(1);
+  return true;
+}
+// the lane's two words p[0], p[1] (a column pair) once both carry `tag`
+__device__ __forceinline__ f32x2 ld_tag_pair(const LayerArgs& a, const uint64_t* p, uint32_t tag) {
+  uint64_t w0 = ld_tag(p), w1 = ld_tag(p + 1);
+  int spins = 0;
+  while (!__all(has_tag(w0, tag) && has_tag(w1, tag)) && keep_waiting(a, spins)) {
+    w0 = ld_tag(p);
+    w1 = ld_tag(p + 1);
+  }
+  return f32x2{tag_value(w0), tag_value(w1)};
+}
+
+// ---------------------------------------------------------------- plan in registers
+// After the plan is published every wave holds it lane-indexed: lane l describes unit l (units
+// 0..63) and unit 64 + l (lanes 0..7): expert id, token count, and the unit's token rows (3 bits
+// each) and slots (7 bits each) packed.
+struct PlanRegs {
+  int units;
+  int ex[2], nt[2];
+  uint32_t tok[2];
+  uint32_t sl[2][2];
+};
+__device__ __forceinline__ PlanRegs load_plan(const Plan* P) {
+  PlanRegs r;
+  r.units = min(max(__builtin_amdgcn_readfirstlane(ld_coh_i(&P->units)), 1), kMaxUnits);
+  const int lane = lane_id();
+  // every word is requested unconditionally (lane indices clamped into the arrays) so the loads
+  // issue back to back; units beyond the count are masked afterwards
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    const int u = min(lane + 64 * h, kMaxUnits - 1);
+    const bool ok = lane + 64 * h < r.units;
+    const int ex = ld_coh_i(&P->expert[u]);
+    const int nt = ld_coh_i(&P->ntok[u]);
+    int tks[kMaxRows], sls[kMaxRows];
+#pragma unroll
+    for (int t = 0; t < kMaxRows; t++) {
+      tks[t] = ld_coh_i(&P->tok[u][t]);
+      sls[t] = ld_coh_i(&P->slot[u][t]);
+    }
+    r.ex[h] = ok ? ex : 0;
+    r.nt[h] = ok ? nt : 0;
+    uint32_t tp = 0, s0 = 0, s1 = 0;
+#pragma unroll
+    for (int t = 0; t < kMaxRows; t++) {
+      const int tk = ok ? tks[t] : 0;
+      const int sl = ok ? sls[t] : 0;
+      tp |= (uint32_t)(tk & 7) << (3 * t);
+      if (t < 4) s0 |= (uint32_t)(sl & 127) << (7 * t);
+      else s1 |= (uint32_t)(sl & 127) << (7 * (t - 4));
+    }
+    r.tok[h] = tp;
+    r.sl[h][0] = s0;
+    r.sl[h][1] = s1;
+  }
+  return r;
+}
+// Every field is clamped into range when read, so a plan that was never published (an exhausted
+// wait) can give wrong results but no out-of-bounds access.
+struct UnitInfo {
+  int e, ntok;
+  uint32_t tok, sl0, sl1;
+  int rows;
+  __device__ __forceinline__ int row(int t) const { return min((int)((tok >> (3 * t)) & 7u), rows - 1); }
+  __device__ __forceinline__ int slot(int t) const {
+    const int s = t < 4 ? (int)((sl0 >> (7 * t)) & 127u) : (int)((sl1 >> (7 * (t - 4))) & 127u);
+    return min(s, kMaxUnits - 1);
+  }
+};
+__device__ __forceinline__ UnitInfo unit_info(const PlanRegs& r, int u, int experts, int rows) {
+  const int h = u >> 6, l = u & 63;
+  UnitInfo i;
+  i.rows = rows;
+  i.e = min(max(__builtin_amdgcn_readlane(h ? r.ex[1] : r.ex[0], l), 0), experts - 1);
+  i.ntok = min(max(__builtin_amdgcn_readlane(h ? r.nt[1] : r.nt[0], l), 0), kMaxRows);
+  i.tok = (uint32_t)__builtin_amdgcn_readlane((int)(h ? r.tok[1] : r.tok[0]), l);
+  i.sl0 = (uint32_t)__builtin_amdgcn_readlane((int)(h ? r.sl[1][0] : r.sl[0][0]), l);
+  i.sl1 = (uint32_t)__builtin_amdgcn_readlane((int)(h ? r.sl[1][1] : r.sl[0][1]), l);
+  return i;
+}
+
+// ---------------------------------------------------------------- the item list
+struct Items {
+  int HB;     // h / 128: parts per gate/up segment, down output blocks
+  int MB;     // m / 128: gate/up column blocks, parts per down segment
+  int G;      // gate/up parts per unit: 2 * MB * HB
+  int D;      // down parts per unit: HB * MB
+  int R;      // router items
+  int S;      // router slices per expert
+  int route;
+};
+enum ItemKind { IT_GU = 0, IT_DOWN = 1, IT_ROUTER = 2, IT_ROUTE = 3, IT_GF = 4, IT_DF = 5, IT_NONE = 6 };
+struct Item {
+  int kind, u, a, b, c;  // GU: a = output block, b = projection, c = part; DOWN: a = output block,
+                         // c = part (input block); GF / DF: a = block; ROUTER: a = item
+};
+// The list: [router R] [route] then phase A, then phase B.
+//   phase A: block b = GU(b), followed for b >= kLagG by GF(b - kLagG); then GF of the last units
+//   phase B: block b = D(b),  followed for b >= kLagD by DF(b - kLagD); then DF of the last units
+// A finisher comes kLag units after the parts it sums, so its inputs are normally complete when it
+// is taken; the last unit's down finishes (the combine) close the list.
+constexpr int kLagG = 2, kLagD = 3;
+// items that need no plan: router, route, and GU(0) = the shared expert's gate/up parts
+__device__ __forceinline__ int pre_items(const Items& L) { return (L.route ? L.R + 1 : 0) + L.G; }
+__device__ __forceinline__ int list_len(const Items& L, int U) {
+  return (L.route ? L.R + 1 : 0) + U * (L.G + L.MB) + U * (L.D + L.HB);
+}
+// position j inside a phase of U blocks of `big` part items, each followed after `lag` blocks by
+// `small` finish items: sets (is_finish, unit, index inside the block)
+__device__ __forceinline__ void phase_at(int j, int U, int big, int small, int lag, bool& fin, int& unit, int& r) {
+  const int lead = min(U, lag);  // blocks without a finish tail
+  if (j < lead * big) {
+    fin = false;
+    unit = j / big;
+    r = j - unit * big;
+    return;
+  }
+  j -= lead * big;
+  const int mid = U - lead;  // blocks with a finish tail
+  if (j < mid * (big + small)) {
+    const int k = j / (big + small), q = j - k * (big + small);
+    if (q < big) {
+      fin = false;
+      unit = lead + k;
+      r = q;
+    } else {
+      fin = true;
+      unit = k;
+      r = q - big;
+    }
+    return;
+  }
+  j -= mid * (big + small);
+  fin = true;
+  unit = mid + j / small;
+  r = j - (unit - mid) * small;
+}
+__device__ __forceinline__ Item item_at(const Items& L, int j, int U) {
+  Item it{IT_NONE, 0, 0, 0, 0};
+  if (L.route) {
+    if (j < L.R) {
+      it.kind = IT_ROUTER;
+      it.a = j;
+      return it;
+    }
+    j -= L.R;
+    if (j == 0) {
+      it.kind = IT_ROUTE;
+      return it;
+    }
+    j -= 1;
+  }
+  bool fin;
+  int unit, r;
+  const int lenA = U * (L.G + L.MB);
+  if (j < lenA) {
+    phase_at(j, U, L.G, L.MB, kLagG, fin, unit, r);
+    it.u = unit;
+    if (fin) {
+      it.kind = IT_GF;
+      it.a = r;
+    } else {
+      it.kind = IT_GU;
+      it.a = r / (2 * L.HB);
+      const int rem = r - it.a * 2 * L.HB;
+      it.b = rem / L.HB;
+      it.c = rem - it.b * L.HB;
+    }
+    return it;
+  }
+  j -= lenA;
+  if (j < U * (L.D + L.HB)) {
+    phase_at(j, U, L.D, L.HB, kLagD, fin, unit, r);
+    it.u = unit;
+    if (fin) {
+      it.kind = IT_DF;
+      it.a = r;
+    } else {
+      it.kind = IT_DOWN;
+      it.c = r / L.HB;
+      it.a = r - it.c * L.HB;
+    }
+  }
+  return it;
+}
+__device__ __forceinline__ bool is_part(const Item& it) { return it.kind == IT_GU || it.kind == IT_DOWN; }
+
+// ---------------------------------------------------------------- tables and LDS
+template <int NT>
+struct LTable {
+  static constexpr bool kF16 = NT == 1;
+  static constexpr int kBytes = kF16 ? 131072 : 65536;
+};
+constexpr int xa_halves(int nt) { return 2 * 2 * (2 * nt) * 4 * 8; }  // [qb][rh][m][g][8] fp16 per wave
+
+__device__ __forceinline__ int part_count(const LayerArgs& a) { return 3 * (a.h / 128) * (a.m / 128); }
+__device__ __forceinline__ uint64_t* part_ptr(const LayerArgs& a, int slot, int index) {
+  return a.w.partial + ((int64_t)slot * part_count(a) + index) * 128;
+}
+
+// ---------------------------------------------------------------- one part: operands
+// The wave's 16 B of quad qb (0, 1) of a part: lane piece of set s4 at +256 s4.
+__device__ __forceinline__ const uint8_t* quad_ptr(const LayerArgs& a, const UnitInfo& ui, const Item& it, int qb) {
+  const int lane = lane_id();
+  const int g = lane >> 4, nn = lane & 15;
+  const bool gu = it.kind == IT_GU;
+  const int side = gu ? 1 : 2;
+  const int in_f = gu ? a.h : a.m;
+  const int it_tiles = in_f / 16, obs = gu ? a.m / 128 : a.h / 128;
+  const uint8_t* base = a.packed[gu ? it.b : 2];
+  return base + chunk_offset(side, (uint64_t)ui.e, it.a, 8 * it.c + 4 * qb + g, it_tiles, obs) +
+         (nn >> 3) * 128 + (nn & 7) * 16;
+}
+__device__ __forceinline__ void load_quad(u32x4 (&pc)[4], const uint8_t* qp) {
+#pragma unroll
+  for (int s4 = 0; s4 < 4; s4++) pc[s4] = load_stream16(qp + 256 * s4);
+}
+// The raw input block of a part, fetched ahead of its staging: gate/up -- the bf16 x pair and the
+// in_scale pair of each token; down -- the tagged down-input pair of each token (DPRE: fetched
+// ahead, else at staging).
+template <int NT, bool DPRE>
+struct InBlock {
+  uint32_t xw[NT];
+  uint32_t sc;
+  uint64_t dw[DPRE ? NT : 1][2];
+};
+template <int NT, bool DPRE>
+__device__ __forceinline__ void fetch_in(const LayerArgs& a, const UnitInfo& ui, const Item& it, InBlock<NT, DPRE>& in) {
+  const int lane = lane_id();
+  if (it.kind == IT_GU) {
+    const int off = 128 * it.c + 2 * lane;
+    in.sc = *reinterpret_cast<const uint32_t*>(a.in_scale[it.b] + (int64_t)ui.e * a.h + off);
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+      in.xw[t] = *reinterpret_cast<const uint32_t*>(a.x + (int64_t)ui.row(min(t, max(ui.ntok - 1, 0))) * a.h + off);
+  } else if (DPRE) {
+#pragma unroll
+    for (int t = 0; t < (DPRE ? NT : 1); t++) {
+      const uint64_t* p = a.w.down_xh + (int64_t)ui.slot(min(t, max(ui.ntok - 1, 0))) * a.m + 128 * it.c + 2 * lane;
+      in.dw[t][0] = ld_tag(p);
+      in.dw[t][1] = ld_tag(p + 1);
+    }
+  }
+}
+// A fragments of the part's 128 input rows (hi and lo fp16 rows per token) into the wave's LDS
+// slice.  Down inputs are polled until they carry the launch's tag.
+template <int NT, bool DPRE>
+__device__ __forceinline__ void stage_in(const LayerArgs& a, const UnitInfo& ui, const Item& it,
+                                         const InBlock<NT, DPRE>& in, uint32_t tag, _Float16* __restrict__ xw) {
+  const int lane = lane_id();
+  float v0[NT], v1[NT];
+  if (it.kind == IT_GU) {
+    const float s0 = f16_to_f32((uint16_t)(in.sc & 0xFFFFu)), s1 = f16_to_f32((uint16_t)(in.sc >> 16));
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      if (t < ui.ntok) {
+        v0[t] = bf16_to_f32((uint16_t)(in.xw[t] & 0xFFFFu)) * s0;
+        v1[t] = bf16_to_f32((uint16_t)(in.xw[t] >> 16)) * s1;
+        hadamard128_wave(v0[t], v1[t]);
+      }
+    }
+  } else {
+    bool ready = true;
+    if (DPRE) {
+#pragma unroll
+      for (int t = 0; t < (DPRE ? NT : 1); t++) {
+        if (t < ui.ntok) {
+          ready = ready && has_tag(in.dw[t][0], tag) && has_tag(in.dw[t][1], tag);
+          v0[t] = tag_value(in.dw[t][0]);
+          v1[t] = tag_value(in.dw[t][1]);
+        }
+      }
+    }
+    if (!DPRE || !__all(ready)) {
+#pragma unroll
+      for (int t = 0; t < NT; t++) {
+        if (t < ui.ntok) {
+          const f32x2 hv = ld_tag_pair(a, a.w.down_xh + (int64_t)ui.slot(t) * a.m + 128 * it.c + 2 * lane, tag);
+          v0[t] = hv.x;
+          v1[t] = hv.y;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int jj = 0; jj < 2; jj++) {
+    const int el = 2 * lane + jj;  // row within the 128-row block
+    const int qb = el >> 6, gg = (el >> 4) & 3, r = el & 15;
+    const int base_off = (qb * 2 + a_rh(r)) * (2 * NT);
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      if (t < ui.ntok) {
+        float xv = jj ? v1[t] : v0[t];
+        // x is materialised in fp32 first so both conversions below see the same value
+        asm volatile("" : "+v"(xv));
+        const _Float16 hi = (_Float16)xv;
+        // the remainder is stored scaled by 2^11 so it stays a normal fp16 (the matrix cores
+        // flush fp16 denormals); the lo row of the product is scaled back by 2^-11 (exact)
+        const _Float16 lo = (_Float16)((xv - (float)hi) * 2048.0f);
+        xw[((base_off + 2 * t) * 4 + gg) * 8 + a_j(r)] = hi;
+        xw[((base_off + 2 * t + 1) * 4 + gg) * 8 + a_j(r)] = lo;
+      }
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+// Decode one quad held in pc (the pieces' predecessor words come from the neighbouring lane) and
+// accumulate it on the matrix cores against the staged A fragments of quad qb.
+template <int NT>
+__device__ __forceinline__ void decode_quad(const u32x4 (&pc)[4], int qb, int ntok, const uint8_t* __restrict__ tab,
+                                            const _Float16* __restrict__ xw, f32x4 (&acc)[4][2]) {
+  const int lane = lane_id();
+  const int g = lane >> 4, nn = lane & 15;
+  const int src_lane = (lane & 7) == 0 ? lane + 7 : lane - 1;
+  const bool live = nn < 2 * ntok;
+  f16x8 A[2];
+#pragma unroll
+  for (int rh = 0; rh < 2; rh++)
+    A[rh] = live ? *reinterpret_cast<const f16x8*>(xw + (((qb * 2 + rh) * (2 * NT) + nn) * 4 + g) * 8)
+                 : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+  uint32_t prior[4];
+#pragma unroll
+  for (int s4 = 0; s4 < 4; s4++) prior[s4] = (uint32_t)__shfl((int)pc[s4].w, src_lane, 64);
+#pragma unroll
+  for (int s4 = 0; s4 < 4; s4++) {
+    const u32x4 v = pc[s4];
+#pragma unroll
+    for (int rh = 0; rh < 2; rh++) {
+      f16x2 q[2][4];
+      const uint32_t w0 = rh ? v.z : v.x, w1 = rh ? v.w : v.y, p0 = rh ? v.y : prior[s4];
+      if (LTable<NT>::kF16)
+        decode_pair_words_f16<MOE_LAYER_ALU_EVEN, MOE_LAYER_ALU_ODD, true>(w0, w1, p0, tab, q);
+      else
+        decode_pair_words_f16<1, 2, false>(w0, w1, p0, tab, q);
+      const f16x8 b0 = frag(q[0][0], q[0][1], q[1][0], q[1][1]);
+      const f16x8 b1 = frag(q[0][2], q[0][3], q[1][2], q[1][3]);
+      acc[s4][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[rh], b0, acc[s4][0], 0, 0, 0);
+      acc[s4][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[rh], b1, acc[s4][1], 0, 0, 0);
+      mfma_acc_guard(acc[s4][0], acc[s4][1]);
+    }
+  }
+}
+// The part's partial sums: token t = D rows 2t, 2t + 1, held by lanes 16 (t / 2) + n, registers
+// 2 (t % 2), +1.  Tagged stores, never waited for.
+template <int NT>
+__device__ __forceinline__ void store_partials(const LayerArgs& a, const UnitInfo& ui, const Item& it,
+                                               const f32x4 (&acc)[4][2], uint32_t tag, const Items& L) {
+  const int lane = lane_id();
+  const int g = lane >> 4, nn = lane & 15;
+  const int index = it.kind == IT_GU ? (it.b * L.MB + it.a) * L.HB + it.c : 2 * L.MB * L.HB + it.a * L.MB + it.c;
+#pragma unroll
+  for (int t = 0; t < NT; t++) {
+    if (t < ui.ntok && g == (t >> 1)) {
+      uint64_t* pw = part_ptr(a, ui.slot(t), index);
+      const int r0 = 2 * (t & 1);
+#pragma unroll
+      for (int s4 = 0; s4 < 4; s4++)
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+          const int col = 16 * (2 * s4 + (nn >> 3)) + (nn & 7) + 8 * hh;
+          st_tag(pw + col, fmaf(acc[s4][hh][r0 + 1], 1.0f / 2048.0f, acc[s4][hh][r0]), tag);
+        }
+    }
+  }
+}
+
+// ---------------------------------------------------------------- finishes
+// Sum of the partials of parts [0, n) at p (stride 128 words) for columns 2 lane, 2 lane + 1, in
+// part order, once every word carries `tag`.
+__device__ __forceinline__ f32x2 sum_parts(const LayerArgs& a, const uint64_t* p, int n, uint32_t tag) {
+  const int lane = lane_id();
+  f32x2 s = {0.0f, 0.0f};
+  for (int i0 = 0; i0 < n; i0 += 16) {
+    // all 32 words of a batch are requested before any is examined (indices clamped, not branched
+    // on, so the loads issue back to back); the batch is reloaded until every word is current
+    uint64_t w[16][2];
+    int spins = 0;
+    // a sample of the batch first (one word per lane: four per part), so a wait costs 1 KB per poll
+    // instead of the batch's 16 KB
+    for (;;) {
+      const uint64_t* q = p + (int64_t)min(i0 + (lane & 15), n - 1) * 128 + ((lane >> 4) * 37 + 11) % 128;
+      if (__all(has_tag(ld_tag(q), tag)) || !keep_waiting(a, spins)) break;
+    }
+    for (;;) {
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        const uint64_t* q = p + (int64_t)min(i0 + i, n - 1) * 128 + 2 * lane;
+        w[i][0] = ld_tag(q);
+        w[i][1] = ld_tag(q + 1);
+      }
+      bool ok = true;
+#pragma unroll
+      for (int i = 0; i < 16; i++) ok = ok & has_tag(w[i][0], tag) & has_tag(w[i][1], tag);
+      if (__all(ok) || !keep_waiting(a, spins)) break;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      if (i0 + i < n) {
+        s.x += tag_value(w[i][0]);
+        s.y += tag_value(w[i][1]);
+      }
+    }
+  }
+  return s;
+}
+
+// gate finish of column block ob of unit ui: the down input of each of its tokens
+__device__ void gate_finish(const LayerArgs& a, const UnitInfo& ui, int ob, uint32_t tag, const Items& L) {
+  const int lane = lane_id();
+  const int col = ob * 128 + 2 * lane;
+  const int64_t si = (int64_t)ui.e * a.m + col;
+  const uint32_t og = *reinterpret_cast<const uint32_t*>(a.out_scale[0] + si);
+  const uint32_t ou = *reinterpret_cast<const uint32_t*>(a.out_scale[1] + si);
+  const uint32_t idn = *reinterpret_cast<const uint32_t*>(a.in_scale[2] + si);
+  auto lo = [](uint32_t v) { return f16_to_f32((uint16_t)(v & 0xFFFFu)); };
+  auto hi = [](uint32_t v) { return f16_to_f32((uint16_t)(v >> 16)); };
+  for (int t = 0; t < ui.ntok; t++) {
+    const int s = ui.slot(t);
+    const f32x2 g = sum_parts(a, part_ptr(a, s, (0 * L.MB + ob) * L.HB), L.HB, tag);
+    const f32x2 uu = sum_parts(a, part_ptr(a, s, (1 * L.MB + ob) * L.HB), L.HB, tag);
+    float g0 = g.x, g1 = g.y, u0 = uu.x, u1 = uu.y;
+    hadamard128_wave(g0, g1);
+    hadamard128_wave(u0, u1);
+    float h0 = swiglu_bf16(g0 * lo(og), u0 * lo(ou));
+    float h1 = swiglu_bf16(g1 * hi(og), u1 * hi(ou));
+    h0 *= lo(idn);
+    h1 *= hi(idn);
+    hadamard128_wave(h0, h1);
+    uint64_t* dst = a.w.down_xh + (int64_t)s * a.m + col;
+    st_tag(dst, h0, tag);
+    st_tag(dst + 1, h1, tag);
+  }
+}
+
+// combine of output block ob over all rows (reference sum order, shared, residual)
+__device__ void combine_block(const LayerArgs& a, int ob, uint32_t tag) {
+  const int lane = lane_id();
+  const int col = ob * 128 + 2 * lane;
+  for (int r = 0; r < a.rows; r++) {
+    f32x2 y[kSlots];
+    {
+      uint64_t w[kSlots][2];
+      int spins = 0;
+      for (;;) {
+        const uint64_t* q = a.w.yslot + (int64_t)(r * kSlots + lane % kSlots) * a.h + col;
+        if (__all(has_tag(ld_tag(q), tag)) || !keep_waiting(a, spins)) break;
+      }
+      for (;;) {
+#pragma unroll
+        for (int j = 0; j < kSlots; j++) {
+          const uint64_t* q = a.w.yslot + (int64_t)(r * kSlots + j) * a.h + col;
+          w[j][0] = ld_tag(q);
+          w[j][1] = ld_tag(q + 1);
+        }
+        bool ok = true;
+#pragma unroll
+        for (int j = 0; j < kSlots; j++) ok = ok & has_tag(w[j][0], tag) & has_tag(w[j][1], tag);
+        if (__all(ok) || !keep_waiting(a, spins)) break;
+      }
+#pragma unroll
+      for (int j = 0; j < kSlots; j++) y[j] = f32x2{tag_value(w[j][0]), tag_value(w[j][1])};
+    }
+    float sc[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) sc[j] = a.route ? ld_coh_f(a.scores + r * 8 + j) : a.scores[r * 8 + j];
+    float tot0 = y[0].x * sc[0] + 0.0f, tot1 = y[0].y * sc[0] + 0.0f;
+#pragma unroll
+    for (int j = 1; j < 8; j++) {
+      tot0 = (y[j].x * sc[j] + 0.0f) + tot0;
+      tot1 = (y[j].y * sc[j] + 0.0f) + tot1;
+    }
+    const float c0f = round_bf16(round_bf16(tot0) + y[8].x);
+    const float c1f = round_bf16(round_bf16(tot1) + y[8].y);
+    const int64_t o = (int64_t)r * a.h + col;
+    const uint32_t res = *reinterpret_cast<const uint32_t*>(a.residual + o);
+    const uint32_t packed2 = (uint32_t)f32_to_bf16(bf16_to_f32((uint16_t)(res & 0xFFFFu)) + c0f) |
+                             ((uint32_t)f32_to_bf16(bf16_to_f32((uint16_t)(res >> 16)) + c1f) << 16);
+    *reinterpret_cast<uint32_t*>(a.out + o) = packed2;
+  }
+}
+
+// down finish of output block ob of unit ui: per-slot values, or the slot outputs for the combine
+// (and, for the last unit, the combine of the block)
+__device__ void down_finish(const LayerArgs& a, const UnitInfo& ui, int ob, bool last, uint32_t tag, const Items& L) {
+  const int lane = lane_id();
+  const int col = ob * 128 + 2 * lane;
+  const uint32_t osc = *reinterpret_cast<const uint32_t*>(a.out_scale[2] + (int64_t)ui.e * a.h + col);
+  const float os0 = f16_to_f32((uint16_t)(osc & 0xFFFFu)), os1 = f16_to_f32((uint16_t)(osc >> 16));
+  for (int t = 0; t < ui.ntok; t++) {
+    const int s = ui.slot(t);
+    const f32x2 v = sum_parts(a, part_ptr(a, s, 2 * L.MB * L.HB + ob * L.MB), L.MB, tag);
+    float v0 = v.x, v1 = v.y;
+    hadamard128_wave(v0, v1);
+    if (a.fin == LFIN_VALUES) {
+      const uint32_t packed2 = (uint32_t)f32_to_bf16(v0 * os0) | ((uint32_t)f32_to_bf16(v1 * os1) << 16);
+      *reinterpret_cast<uint32_t*>(a.values + (int64_t)s * a.h + col) = packed2;
+    } else {
+      uint64_t* dst = a.w.yslot + (int64_t)s * a.h + col;
+      st_tag(dst, round_bf16(v0 * os0), tag);
+      st_tag(dst + 1, round_bf16(v1 * os1), tag);
+    }
+  }
+  if (a.fin == LFIN_COMBINE && last) {
+    release_stores();  // this wave's own slot outputs are read back by the combine
+    combine_block(a, ob, tag);
+  }
+}
+
+// ---------------------------------------------------------------- router
+// item r = e * S + j: partial logit of expert e over inputs [kRouterSlice j, kRouterSlice (j + 1))
+// for every row, stored tagged at logit_part[(row * 256 + e) * S + j].
+__device__ __forceinline__ void router_item(const LayerArgs& a, int r, int S, uint32_t tag) {
+  const int e = r / S, j = r - e * S;
+  const int lane = lane_id();
+  constexpr int kPer = kRouterSlice / 64;  // 16 inputs per lane
+  const int k0 = j * kRouterSlice + kPer * lane;
+  f32x4 w[kPer / 4];
+#pragma unroll
+  for (int i = 0; i < kPer / 4; i++) w[i] = *reinterpret_cast<const f32x4*>(a.router_w + (int64_t)e * a.h + k0 + 4 * i);
+  for (int row = 0; row < a.rows; row++) {
+    u32x4 xv[kPer / 8];
+#pragma unroll
+    for (int i = 0; i < kPer / 8; i++) xv[i] = *reinterpret_cast<const u32x4*>(a.x + (int64_t)row * a.h + k0 + 8 * i);
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kPer / 8; i++) {
+      const f32x4 wa = w[2 * i], wb = w[2 * i + 1];
+      acc = fmaf(bf16_to_f32((uint16_t)(xv[i].x & 0xFFFFu)), wa.x, acc);
+      acc = fmaf(bf16_to_f32((uint16_t)(xv[i].x >> 16)), wa.y, acc);
+      acc = fmaf(bf16_to_f32((uint16_t)(xv[i].y & 0xFFFFu)), wa.z, acc);
+      acc = fmaf(bf16_to_f32((uint16_t)(xv[i].y >> 16)), wa.w, acc);
+      acc = fmaf(bf16_to_f32((uint16_t)(xv[i].z & 0xFFFFu)), wb.x, acc);
+      acc = fmaf(bf16_to_f32((uint16_t)(xv[i].z >> 16)), wb.y, acc);
+      acc = fmaf(bf16_to_f32((uint16_t)(xv[i].w & 0xFFFFu)), wb.z, acc);
+      acc = fmaf(bf16_to_f32((uint16_t)(xv[i].w >> 16)), wb.w, acc);
+    }
+    const float tot = wave_sum(acc);
+    if (lane == 63) st_tag(a.w.logit_part + ((int64_t)row * 256 + e) * S + j, tot, tag);
+  }
+}
+
+// The routing item: logits from their slices (slice order), top-8 per row, then the plan with the
+// shared expert as unit 0 and the routed experts in first-appearance order (routed slot order),
+// published by the plan word = tag.
+__device__ void route_and_plan(const LayerArgs& a, int S, uint32_t tag) {
+  const int lane = lane_id();
+  __shared__ int32_t sid_lds[kMaxUnits];
+  constexpr int kMaxS = kMaxRouteHidden / kRouterSlice;
+  for (int row = 0; row < a.rows; row++) {
+    RouteInput in;
+    const uint64_t* lp = a.w.logit_part + ((int64_t)row * 256 + lane) * S;
+    // every slice word of the lane's four experts in one round trip, reloaded until all are current
+    uint64_t wd[4][kMaxS];
+    int spins = 0;
+    for (;;) {
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < kMaxS; j++) wd[i][j] = ld_tag(lp + (int64_t)64 * i * S + min(j, S - 1));
+      bool ok = true;
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < kMaxS; j++) ok = ok & has_tag(wd[i][j], tag);
+      if (__all(ok) || !keep_waiting(a, spins)) break;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      float v = 0.0f;
+#pragma unroll
+      for (int j = 0; j < kMaxS; j++)
+        if (j < S) v += tag_value(wd[i][j]);
+      in.logit[i] = v;
+      in.bias[i] = a.bias[lane + 64 * i];
+    }
+    route_select<true>(in, row, a.ids, a.scores, sid_lds, true);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  // routed slot s' = 8 row + k (lane s'), global slot 9 row + k
+  Plan* P = a.w.plan;
+  const int n = a.rows * 8;
+  const bool act = lane < n;
+  const int row = lane >> 3, k = lane & 7;
+  const int e = act ? sid_lds[row * 9 + k] : -1;
+  int pos = 0, total = 0, first_lane = lane;
+  for (int q = 0; q < n; q++) {
+    const int eq = __builtin_amdgcn_readlane(e, q);
+    const bool same = eq == e;
+    if (same && q < lane) {
+      if (pos == 0) first_lane = q;
+      pos++;
+    }
+    total += same ? 1 : 0;
+  }
+  const uint64_t firsts = __ballot(act && pos == 0);
+  const int unit = 1 + (int)__popcll(firsts & ((1ull << first_lane) - 1ull));
+  if (act) {
+    const int gs = row * 9 + k;
+    if (pos == 0) {
+      st_coh_i(&P->expert[unit], e);
+      st_coh_i(&P->ntok[unit], total);
+    }
+    st_coh_i(&P->tok[unit][pos], row);
+    st_coh_i(&P->slot[unit][pos], gs);
+    st_coh_i(&P->slot_unit[gs], unit);
+    st_coh_i(&P->slot_pos[gs], pos);
+  }
+  if (lane < a.rows) {
+    st_coh_i(&P->tok[0][lane], lane);
+    st_coh_i(&P->slot[0][lane], lane * 9 + 8);
+    st_coh_i(&P->slot_unit[lane * 9 + 8], 0);
+    st_coh_i(&P->slot_pos[lane * 9 + 8], lane);
+  }
+  if (lane == 0) {
+    st_coh_i(&P->expert[0], 256);
+    st_coh_i(&P->ntok[0], a.rows);
+    st_coh_i(&P->units, 1 + (int)__popcll(firsts));
+    st_coh_i(&P->rows, a.rows);
+  }
+  release_stores();
+  if (lane == 0) st_coh_i(a.w.flags + LF_PLAN, (int)tag);
+}
+
+// ---------------------------------------------------------------- the kernel
+template <int NT>
+__global__ __launch_bounds__(kLW * 64) void k4_layer_kernel(LayerArgs a) {
+  constexpr bool kDPre = NT == 1;  // down inputs fetched ahead (registers allow it for one token)
+  __shared__ __attribute__((aligned(16))) uint8_t tab[LTable<NT>::kBytes];
+  __shared__ __attribute__((aligned(16))) _Float16 xa[kLW * xa_halves(NT)];
+  __shared__ int32_t exit_last;
+
+  const int wv = wave_id_uniform();
+  _Float16* __restrict__ xw = xa + wv * xa_halves(NT);
+  const int xcd = (int)(blockIdx.x % kXcds);
+  int32_t* qc = a.w.queue + xcd * kQueueStride;
+  Items L;
+  L.HB = a.h / 128;
+  L.MB = a.m / 128;
+  L.G = 2 * L.MB * L.HB;
+  L.D = L.HB * L.MB;
+  L.S = a.h / kRouterSlice;
+  L.R = a.route ? 256 * L.S : 0;
+  L.route = a.route;
+  const int pre = pre_items(L);
+  const uint32_t epoch = (uint32_t)__builtin_amdgcn_readfirstlane(ld_coh_i(a.w.flags + LF_EPOCH));
+  const uint32_t tag = epoch + 1u;
+
+  auto claim = [&]() {
+    int v = 0;
+    if (lane_id() == 0) v = __hip_atomic_fetch_add(qc, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    return __builtin_amdgcn_readfirstlane(v);
+  };
+
+  bool have_plan = false;
+  PlanRegs pr{};
+  UnitInfo shared_ui{min(256, a.experts - 1), a.rows, 0, 0, 0, a.rows};
+  if (a.route) {
+    // unit 0 (the shared expert) is known before routing: rows 0.., slots 9 r + 8
+    uint32_t tok = 0, s0 = 0, s1 = 0;
+    for (int t = 0; t < a.rows; t++) {
+      tok |= (uint32_t)t << (3 * t);
+      if (t < 4) s0 |= (uint32_t)(9 * t + 8) << (7 * t);
+      else s1 |= (uint32_t)(9 * t + 8) << (7 * (t - 4));
+    }
+    shared_ui.tok = tok;
+    shared_ui.sl0 = s0;
+    shared_ui.sl1 = s1;
+  } else {
+    pr = load_plan(a.w.plan);
+    have_plan = true;
+  }
+  auto unit_of = [&](int u) { return (u == 0 && a.route) ? shared_ui : unit_info(pr, u, a.experts, a.rows); };
+  // the item at sub-list position `sub`, if it is known without waiting (kind NONE otherwise)
+  auto resolve = [&](int sub, Item& it) {
+    const int j = sub * kXcds + xcd;
+    it = Item{IT_NONE, 0, 0, 0, 0};
+    if (j < pre) it = item_at(L, j, 1);
+    else if (have_plan && j < list_len(L, pr.units)) it = item_at(L, j, pr.units);
+  };
+
+  // A run of part items: pc / in hold the first item's quad 0 and input block on entry; each item
+  // streams its quad 1 while quad 0 is decoded and the next part's quad 0 and input block while
+  // quad 1 is decoded.  Returns with `sub` at the first item that is not a part (or not yet known).
+  u32x4 pc[4];
+  InBlock<NT, kDPre> in;
+  auto run_parts = [&](Item it, int& sub) {
+    for (;;) {
+      const UnitInfo ui = unit_of(it.u);
+      u32x4 pn[4];
+      load_quad(pn, quad_ptr(a, ui, it, 1));
+      __builtin_amdgcn_s_setprio(2);
+      stage_in<NT, kDPre>(a, ui, it, in, tag, xw);
+      __builtin_amdgcn_s_setprio(0);
+      // the next item is claimed once this one can no longer wait (a claimed item is only started
+      // by its claimer); the claim's round trip is hidden by quad 0
+      const int nsub = claim();
+      f32x4 acc[4][2];
+#pragma unroll
+      for (int s4 = 0; s4 < 4; s4++)
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) acc[s4][hh] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      decode_quad<NT>(pc, 0, ui.ntok, tab, xw, acc);
+      Item nit;
+      resolve(nsub, nit);
+      if (is_part(nit)) {
+        const UnitInfo nui = unit_of(nit.u);
+        load_quad(pc, quad_ptr(a, nui, nit, 0));
+        fetch_in<NT, kDPre>(a, nui, nit, in);
+      }
+      decode_quad<NT>(pn, 1, ui.ntok, tab, xw, acc);
+      store_partials<NT>(a, ui, it, acc, tag, L);
+      sub = nsub;
+      if (!is_part(nit)) return;
+      it = nit;
+    }
+  };
+
+  int sub = claim();
+  Item first;
+  resolve(sub, first);
+  // router items need no code table: they run before the copy
+  while (first.kind == IT_ROUTER) {
+    __builtin_amdgcn_s_setprio(3);
+    router_item(a, first.a, L.S, tag);
+    __builtin_amdgcn_s_setprio(0);
+    sub = claim();
+    resolve(sub, first);
+  }
+  // the first part's operands are in flight while the code table is copied
+  if (is_part(first)) {
+    const UnitInfo ui = unit_of(first.u);
+    load_quad(pc, quad_ptr(a, ui, first, 0));
+    fetch_in<NT, kDPre>(a, ui, first, in);
+  }
+  if (LTable<NT>::kF16)
+    copy_table_lds<131072, kLW * 64>(tab, a.tab16);
+  else
+    copy_table_lds<65536, kLW * 64>(tab, a.tab8);
+  __syncthreads();
+  if (is_part(first)) run_parts(first, sub);
+
+  for (;;) {
+    const int j = sub * kXcds + xcd;
+    if (!have_plan && j >= pre) {
+      __builtin_amdgcn_s_setprio(3);
+      int spins = 0;
+      while ((uint32_t)ld_coh_i(a.w.flags + LF_PLAN) != tag && keep_waiting(a, spins)) {
+      }
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+      pr = load_plan(a.w.plan);
+      have_plan = true;
+      __builtin_amdgcn_s_setprio(0);
+    }
+    const int U = have_plan ? pr.units : 1;
+    if (have_plan && j >= list_len(L, U)) break;
+    const Item it = item_at(L, j, U);
+    if (it.kind == IT_NONE) break;
+    if (is_part(it)) {
+      const UnitInfo ui = unit_of(it.u);
+      load_quad(pc, quad_ptr(a, ui, it, 0));
+      fetch_in<NT, kDPre>(a, ui, it, in);
+      run_parts(it, sub);
+      continue;
+    }
+    // items other than parts are short and latency-bound, and others wait for them: they run at
+    // raised wave priority (the SIMD arbiter otherwise favours the older, decoding waves)
+    __builtin_amdgcn_s_setprio(3);
+    if (it.kind == IT_ROUTER) {
+      router_item(a, it.a, L.S, tag);
+    } else if (it.kind == IT_ROUTE) {
+      route_and_plan(a, L.S, tag);
+    } else if (it.kind == IT_GF) {
+      gate_finish(a, unit_of(it.u), it.a, tag, L);
+    } else if (it.kind == IT_DF) {
+      down_finish(a, unit_of(it.u), it.a, it.u == U - 1, tag, L);
+    }
+    __builtin_amdgcn_s_setprio(0);
+    sub = claim();
+  }
+  // the last block to leave resets the sub-list counters and advances the epoch
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    exit_last = __hip_atomic_fetch_add(a.w.flags + LF_EXIT, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) + 1 ==
+                (int)gridDim.x;
+  }
+  __syncthreads();
+  if (exit_last && threadIdx.x < kXcds) st_coh_i(a.w.queue + threadIdx.x * kQueueStride, 0);
+  if (exit_last && threadIdx.x == 0) {
+    st_coh_i(a.w.flags + LF_EXIT, 0);
+    st_coh_i(a.w.flags + LF_EPOCH, (int)(epoch + 1u == 0xFFFFFFFEu ? 0u : epoch + 1u));
+  }
+  // a wave may end with its stores still in flight, and the next launch reads these words at its
+  // start: they are acknowledged before the block ends
+  if (exit_last) release_stores();
+}
+
+// ---------------------------------------------------------------- host side
+size_t layer_align(size_t v) { return (v + 255) & ~(size_t)255; }
+
+LayerWs layer_carve(void* base, int h, int m) {
+  LayerWs w{};
+  size_t off = 0;
+  char* p = static_cast<char*>(base);
+  auto take = [&](size_t bytes) { char* r = p ? p + off : nullptr; off += layer_align(bytes); return r; };
+  const int HB = h / 128, MB = m / 128;
+  w.plan = reinterpret_cast<Plan*>(take(sizeof(Plan)));
+  w.flags = reinterpret_cast<int32_t*>(take(LF_COUNT * 4));
+  w.queue = reinterpret_cast<int32_t*>(take((size_t)kXcds * kQueueStride * 4));
+  w.logit_part = reinterpret_cast<uint64_t*>(take((size_t)kMaxRows * 256 * (h / kRouterSlice + 1) * 8));
+  w.partial = reinterpret_cast<uint64_t*>(take((size_t)kMaxUnits * 3 * HB * MB * 128 * 8));
+  w.down_xh = reinterpret_cast<uint64_t*>(take((size_t)kMaxUnits * m * 8));
+  w.yslot = reinterpret_cast<uint64_t*>(take((size_t)kMaxUnits * h * 8));
+  w.bytes = off;
+  return w;
+}
+
+Plan* k4_layer_plan(void* layer_ws) { return layer_carve(layer_ws, 1024, 128).plan; }
+
+size_t k4_layer_workspace_bytes(int h, int m) {
+  return layer_carve(nullptr, h > 0 ? h : 128, m > 0 ? m : 128).bytes;
+}
+
+bool k4_layer_supported(int h, int m, bool route) {
+  return h > 0 && m > 0 && h % (route ? kRouterSlice : 128) == 0 && m % 128 == 0 && h <= (route ? kMaxRouteHidden : 16384) &&
+         m <= 16384;
+}
+
+// One launch of the fused block.  `workspace` is the layer region (zeroed once; the kernel leaves
+// its counters clean and advances its epoch).
+static int k4_layer_launch(LayerArgs a, void* workspace, hipStream_t s) {
+  a.w = layer_carve(workspace, a.h, a.m);
+  a.tab8 = codebook_device_table();
+  a.tab16 = codebook_f16_device_table();
+  if (!a.tab8 || !a.tab16) return fail(MOE_ENOTSUP, "code tables are not initialised on this device");
+  const int grid = device_cus();
+  if (a.rows <= 1)
+    hipLaunchKernelGGL(k4_layer_kernel<1>, dim3(grid), dim3(kLW * 64), 0, s, a);
+  else
+    hipLaunchKernelGGL(k4_layer_kernel<kMaxRows>, dim3(grid), dim3(kLW * 64), 0, s, a);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail((int)e, "launch of the fused K4 block failed: %s", hipGetErrorString(e));
+  return MOE_OK;
+}
+
+int k4_layer_run(const uint16_t* x, const uint16_t* residual, int rows, int route, const float* router_w,
+                 const float* bias, uint32_t* ids, float* scores, const uint8_t* const packed[3],
+                 const uint16_t* const in_scale[3], const uint16_t* const out_scale[3], int h, int m, int experts,
+                 int combine, uint16_t* out, uint16_t* values, void* layer_ws, hipStream_t s) {
+  if (!k4_layer_supported(h, m, route != 0))
+    return fail(MOE_ENOTSUP, "the fused K4 block needs hidden a multiple of %d and intermediate of 128 (got %d, %d)",
+                route ? kRouterSlice : 128, h, m);
+  if (rows < 1 || rows > kMaxRows) return fail(MOE_EINVAL, "the fused K4 block takes 1..%d rows (got %d)", kMaxRows, rows);
+  LayerArgs a{};
+  a.x = x;
+  a.residual = residual;
+  a.rows = rows;
+  a.route = route;
+  a.router_w = router_w;
+  a.bias = bias;
+  a.ids = ids;
+  a.scores = scores;
+  for (int i = 0; i < 3; i++) {
+    a.packed[i] = packed[i];
+    a.in_scale[i] = in_scale[i];
+    a.out_scale[i] = out_scale[i];
+  }
+  a.h = h;
+  a.m = m;
+  a.experts = experts;
+  a.fin = combine ? LFIN_COMBINE : LFIN_VALUES;
+  a.out = out;
+  a.values = values;
+  return k4_layer_launch(a, layer_ws, s);
+}
+
+}  // namespace moe

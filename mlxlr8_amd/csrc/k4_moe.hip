@@ -659,6 +659,7 @@ __device__ __forceinline__ void k4_mfma_body(const GemvArgs& a, const Plan* __re
           const f16x8 b1 = frag(q[0][2], q[0][3], q[1][2], q[1][3]);
           acc[s4][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[rh], b0, acc[s4][0], 0, 0, 0);
           acc[s4][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[rh], b1, acc[s4][1], 0, 0, 0);
+          mfma_acc_guard(acc[s4][0], acc[s4][1]);
         }
       }
     }
@@ -691,6 +692,7 @@ struct DeviceState {
   bool ready = false;
   int cus = 0;
   const uint8_t* codebook = nullptr;
+  const uint16_t* codebook16 = nullptr;
 };
 std::mutex g_mutex;
 DeviceState g_devices[64];
@@ -726,6 +728,12 @@ int ensure_device_ready() {
   void* table = nullptr;
   MOE_HIP(hipGetSymbolAddress(&table, HIP_SYMBOL(g_codebook_e4m3)));
   st.codebook = static_cast<const uint8_t*>(table);
+  void* table16 = nullptr;
+  MOE_HIP(hipGetSymbolAddress(&table16, HIP_SYMBOL(g_codebook_f16)));
+  st.codebook16 = static_cast<const uint16_t*>(table16);
+  int coop = 0;
+  MOE_HIP(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev));
+  if (!coop) return fail(MOE_ENOTSUP, "device %d does not support cooperative launches", dev);
   hipLaunchKernelGGL(build_codebook_kernel, dim3(128), dim3(256), 0, 0);
   MOE_HIP(hipGetLastError());
   MOE_HIP(hipDeviceSynchronize());
@@ -737,6 +745,12 @@ const uint8_t* codebook_device_table() {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
   return g_devices[dev].codebook;
+}
+
+const uint16_t* codebook_f16_device_table() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  return g_devices[dev].codebook16;
 }
 
 int device_cus() {
@@ -761,6 +775,7 @@ struct Workspace {
   float* scores;        // [kMaxRows][8]
   uint16_t* hrow;       // [kMaxRows][hidden] layer residual T(x + attn) (moe_k4_layer_decode)
   uint16_t* xnrow;      // [kMaxRows][hidden] normalised expert input (moe_k4_layer_decode)
+  void* layer;          // the fused decode block's region (k4_layer.hip)
   size_t bytes;
 };
 
@@ -785,6 +800,7 @@ Workspace carve(void* base, int hidden, int inter) {
   w.scores = reinterpret_cast<float*>(take((size_t)kMaxRows * 8 * 4));
   w.hrow = reinterpret_cast<uint16_t*>(take((size_t)kMaxRows * hidden * 2));
   w.xnrow = reinterpret_cast<uint16_t*>(take((size_t)kMaxRows * hidden * 2));
+  w.layer = take(k4_layer_workspace_bytes(hidden, inter));
   w.bytes = off;
   return w;
 }
@@ -943,70 +959,79 @@ int moe_k4_expert_linear(const uint16_t* x, int x_per_slot, const uint32_t* ids,
   return launch_gemv<IN_PREP, FIN_VALUES>(a, max_users, rows * slots, s);
 }
 
+// The routed decode block in one fused launch: with norm_w, h = T(x + attn) (attn may be NULL) and
+// the block runs on RMSNorm(h) with residual h; otherwise on x with `residual`.  Every argument is
+// checked before the first launch.
+static int k4_block(const uint16_t* x, const uint16_t* attn, const uint16_t* norm_w, float eps,
+                    const uint16_t* residual, int rows, const float* router_w, const float* bias, const void* pg,
+                    const void* pu, const void* pd, int64_t bytes, const uint16_t* in_g, const uint16_t* out_g,
+                    const uint16_t* in_u, const uint16_t* out_u, const uint16_t* in_d, const uint16_t* out_d, int h,
+                    int m, uint16_t* out, uint32_t* indices, float* scores, void* workspace, size_t workspace_bytes,
+                    hipStream_t s) {
+  MOE_ARG(x && router_w && bias && out && pg && pu && pd && in_g && out_g && in_u && out_u && in_d && out_d,
+          "null pointer argument");
+  MOE_ARG(norm_w || residual, "null pointer argument");
+  MOE_ARG(rows >= 1 && rows <= kMaxRows, "rows must be in 1..%d", kMaxRows);
+  int64_t experts = 0;
+  int rc = check_trellis(bytes, h, m, &experts);
+  if (rc) return rc;
+  MOE_ARG(experts == 257, "the routed decode block needs 256 routed experts plus the shared expert (got %lld)",
+          (long long)experts);
+  MOE_ARG(k4_layer_supported(h, m, true), "hidden must be a multiple of 512 and intermediate of 128 (got %d, %d)", h,
+          m);
+  if ((rc = validate_ws(workspace, workspace_bytes, h, m))) return rc;
+  if ((rc = ensure_device_ready())) return rc;
+  Workspace w = carve(workspace, h, m);
+  uint32_t* ids = indices ? indices : w.ids;
+  float* sc = scores ? scores : w.scores;
+  const uint16_t* xin = x;
+  const uint16_t* res = residual;
+  prof_mark(0, s);
+  if (norm_w) {
+    if ((rc = moe_residual_rmsnorm(x, attn, norm_w, rows, h, eps, w.hrow, w.xnrow, (moe_stream_t)s))) return rc;
+    xin = w.xnrow;
+    res = w.hrow;
+  }
+  const uint8_t* packed[3] = {(const uint8_t*)pg, (const uint8_t*)pu, (const uint8_t*)pd};
+  const uint16_t* ins[3] = {in_g, in_u, in_d};
+  const uint16_t* outs[3] = {out_g, out_u, out_d};
+  prof_mark(1, s);
+  rc = k4_layer_run(xin, res, rows, 1, router_w, bias, ids, sc, packed, ins, outs, h, m, 257, 1, out, nullptr,
+                    w.layer, s);
+  prof_mark(3, s);
+  return rc;
+}
+
 static int k4_mlp_common(const uint16_t* x, const uint32_t* ids, const float* scores, const uint16_t* residual,
                          int rows, int slots, const void* pg, const void* pu, const void* pd, int64_t bytes,
                          const uint16_t* in_g, const uint16_t* out_g, const uint16_t* in_u, const uint16_t* out_u,
                          const uint16_t* in_d, const uint16_t* out_d, int h, int m, uint16_t* values, uint16_t* out,
-                         void* workspace, size_t workspace_bytes, hipStream_t s, bool ids_on_plan) {
-  MOE_ARG(x && pg && pu && pd && in_g && out_g && in_u && out_u && in_d && out_d, "null pointer argument");
+                         void* workspace, size_t workspace_bytes, hipStream_t s) {
+  MOE_ARG(x && ids && pg && pu && pd && in_g && out_g && in_u && out_u && in_d && out_d, "null pointer argument");
   MOE_ARG(rows >= 1 && rows <= kMaxRows && slots >= 1 && slots <= kSlots,
           "rows must be in 1..%d and slots in 1..%d", kMaxRows, kSlots);
   int64_t experts = 0;
   int rc = check_trellis(bytes, h, m, &experts);
   if (rc) return rc;
   MOE_ARG(experts >= 1, "no experts");
+  MOE_ARG(k4_layer_supported(h, m, false), "hidden and intermediate must be multiples of 128 (got %d, %d)", h, m);
+  if (out) MOE_ARG(slots == kSlots && scores && residual, "the combined finish needs 9 slots, scores and residual");
   if ((rc = validate_ws(workspace, workspace_bytes, h, m))) return rc;
   if ((rc = ensure_device_ready())) return rc;
   Workspace w = carve(workspace, h, m);
   const int max_users = rows == 1 ? 1 : kMaxRows;
-  if (!ids_on_plan) {
-    MOE_ARG(ids != nullptr, "ids must not be NULL");
-    hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(128), 0, s, ids, rows, slots, (int)(experts > 257 ? 257 : experts),
-                       max_users, w.plan);
-    MOE_HIP(hipGetLastError());
-  }
-  GemvArgs g{};
-  g.packed[0] = (const uint8_t*)pg;
-  g.packed[1] = (const uint8_t*)pu;
-  g.nproj = 2;
-  g.in_f = h; g.out_f = m; g.side = 1;
-  g.x_bf16 = x;
-  g.in_scale[0] = in_g; g.in_scale[1] = in_u;
-  g.plan = w.plan;
-  g.partial = w.partial;
-  g.counter_seg = w.counter_seg;
-  g.counter_grp = w.counter_grp;
-  g.out_scale[0] = out_g; g.out_scale[1] = out_u;
-  g.in_down = in_d;
-  g.down_xh = w.down_xh;
+  const int ecount = (int)(experts > 257 ? 257 : experts);
+  hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(128), 0, s, ids, rows, slots, ecount, max_users,
+                     k4_layer_plan(w.layer));
+  MOE_HIP(hipGetLastError());
+  const uint8_t* packed[3] = {(const uint8_t*)pg, (const uint8_t*)pu, (const uint8_t*)pd};
+  const uint16_t* ins[3] = {in_g, in_u, in_d};
+  const uint16_t* outs[3] = {out_g, out_u, out_d};
   prof_mark(1, s);
-  if ((rc = launch_gemv<IN_PREP, FIN_GATE>(g, max_users, rows * slots, s))) return rc;
-  prof_mark(2, s);
-
-  GemvArgs d{};
-  d.packed[0] = (const uint8_t*)pd;
-  d.nproj = 1;
-  d.in_f = m; d.out_f = h; d.side = 2;
-  d.x_f32 = w.down_xh;
-  d.plan = w.plan;
-  d.partial = w.partial;
-  d.out_scale[0] = out_d;
-  if (out) {
-    MOE_ARG(slots == kSlots && scores && residual, "the combined finish needs 9 slots, scores and residual");
-    d.counter_seg = w.counter_seg;
-    d.counter_grp = w.counter_grp;
-    d.yslot = w.yslot;
-    d.scores = scores;
-    d.residual = residual;
-    d.out = out;
-    rc = launch_gemv<IN_DIRECT, FIN_COMBINE>(d, max_users, rows * slots, s);
-    prof_mark(3, s);
-    return rc;
-  }
-  d.counter_seg = w.counter_seg;
-  d.counter_grp = w.counter_grp;
-  d.values = values;
-  return launch_gemv<IN_DIRECT, FIN_VALUES>(d, max_users, rows * slots, s);
+  rc = k4_layer_run(x, residual, rows, 0, nullptr, nullptr, nullptr, const_cast<float*>(scores), packed, ins, outs, h,
+                    m, ecount, out != nullptr, out, values, w.layer, s);
+  prof_mark(3, s);
+  return rc;
 }
 
 int moe_k4_mlp(const uint16_t* x, const uint32_t* ids, int rows, int slots, const void* packed_gate,
@@ -1017,7 +1042,7 @@ int moe_k4_mlp(const uint16_t* x, const uint32_t* ids, int rows, int slots, cons
   MOE_ARG(values != nullptr, "values must not be NULL");
   return k4_mlp_common(x, ids, nullptr, nullptr, rows, slots, packed_gate, packed_up, packed_down, packed_bytes,
                        in_gate, out_gate, in_up, out_up, in_down, out_down, hidden, intermediate, values, nullptr,
-                       workspace, workspace_bytes, (hipStream_t)stream, false);
+                       workspace, workspace_bytes, (hipStream_t)stream);
 }
 
 int moe_k4_mlp_finish(const uint16_t* x, const uint32_t* ids, const float* scores, const uint16_t* residual, int rows,
@@ -1029,7 +1054,7 @@ int moe_k4_mlp_finish(const uint16_t* x, const uint32_t* ids, const float* score
   MOE_ARG(out != nullptr, "out must not be NULL");
   return k4_mlp_common(x, ids, scores, residual, rows, kSlots, packed_gate, packed_up, packed_down, packed_bytes,
                        in_gate, out_gate, in_up, out_up, in_down, out_down, hidden, intermediate, nullptr, out,
-                       workspace, workspace_bytes, (hipStream_t)stream, false);
+                       workspace, workspace_bytes, (hipStream_t)stream);
 }
 
 int moe_k4_moe_decode(const uint16_t* x, const uint16_t* residual, int rows, const float* router_w, const float* bias,
@@ -1038,25 +1063,9 @@ int moe_k4_moe_decode(const uint16_t* x, const uint16_t* residual, int rows, con
                       const uint16_t* out_up, const uint16_t* in_down, const uint16_t* out_down, int hidden,
                       int intermediate, uint16_t* out, uint32_t* indices, float* scores, void* workspace,
                       size_t workspace_bytes, moe_stream_t stream) {
-  MOE_ARG(x && residual && router_w && bias && out, "null pointer argument");
-  MOE_ARG(rows >= 1 && rows <= kMaxRows, "rows must be in 1..%d", kMaxRows);
-  int rc = validate_ws(workspace, workspace_bytes, hidden, intermediate);
-  if (rc) return rc;
-  if ((rc = ensure_device_ready())) return rc;
-  Workspace w = carve(workspace, hidden, intermediate);
-  hipStream_t s = (hipStream_t)stream;
-  uint32_t* ids = indices ? indices : w.ids;
-  float* sc = scores ? scores : w.scores;
-  int64_t experts = 0;
-  if ((rc = check_trellis(packed_bytes, hidden, intermediate, &experts))) return rc;
-  MOE_ARG(experts == 257, "the routed decode block needs 256 routed experts plus the shared expert (got %lld)",
-          (long long)experts);
-  prof_mark(0, s);
-  rc = moe_router_fused_plan(x, router_w, bias, rows, hidden, 257, w.logits, ids, sc, w.plan, w.router_counter, s);
-  if (rc) return rc;
-  return k4_mlp_common(x, ids, sc, residual, rows, kSlots, packed_gate, packed_up, packed_down, packed_bytes, in_gate,
-                       out_gate, in_up, out_up, in_down, out_down, hidden, intermediate, nullptr, out, workspace,
-                       workspace_bytes, s, true);
+  return k4_block(x, nullptr, nullptr, 0.0f, residual, rows, router_w, bias, packed_gate, packed_up, packed_down,
+                  packed_bytes, in_gate, out_gate, in_up, out_up, in_down, out_down, hidden, intermediate, out, indices,
+                  scores, workspace, workspace_bytes, (hipStream_t)stream);
 }
 
 int moe_k4_layer_decode(const uint16_t* x, const uint16_t* attn, const uint16_t* norm_w, float eps, int rows,
@@ -1066,28 +1075,12 @@ int moe_k4_layer_decode(const uint16_t* x, const uint16_t* attn, const uint16_t*
                         const uint16_t* in_down, const uint16_t* out_down, int hidden, int intermediate,
                         uint16_t* out, uint32_t* indices, float* scores, void* workspace, size_t workspace_bytes,
                         moe_stream_t stream) {
-  MOE_ARG(x && norm_w && router_w && bias && out, "null pointer argument");
-  MOE_ARG(rows >= 1 && rows <= kMaxRows, "rows must be in 1..%d", kMaxRows);
+  MOE_ARG(norm_w != nullptr, "null pointer argument");
   MOE_ARG(eps >= 0.0f, "epsilon must be non-negative");
   MOE_ARG(hidden % 2048 == 0 && hidden <= 8192, "layer width must be a multiple of 2048 up to 8192 (got %d)", hidden);
-  int rc = validate_ws(workspace, workspace_bytes, hidden, intermediate);
-  if (rc) return rc;
-  if ((rc = ensure_device_ready())) return rc;
-  Workspace w = carve(workspace, hidden, intermediate);
-  hipStream_t s = (hipStream_t)stream;
-  uint32_t* ids = indices ? indices : w.ids;
-  float* sc = scores ? scores : w.scores;
-  int64_t experts = 0;
-  if ((rc = check_trellis(packed_bytes, hidden, intermediate, &experts))) return rc;
-  MOE_ARG(experts == 257, "the routed decode block needs 256 routed experts plus the shared expert (got %lld)",
-          (long long)experts);
-  prof_mark(0, s);
-  rc = moe_router_fused_plan(x, router_w, bias, rows, hidden, 257, w.logits, ids, sc, w.plan, w.router_counter, s,
-                             attn, norm_w, eps, w.hrow, w.xnrow);
-  if (rc) return rc;
-  return k4_mlp_common(w.xnrow, ids, sc, w.hrow, rows, kSlots, packed_gate, packed_up, packed_down, packed_bytes,
-                       in_gate, out_gate, in_up, out_up, in_down, out_down, hidden, intermediate, nullptr, out,
-                       workspace, workspace_bytes, s, true);
+  return k4_block(x, attn, norm_w, eps, nullptr, rows, router_w, bias, packed_gate, packed_up, packed_down,
+                  packed_bytes, in_gate, out_gate, in_up, out_up, in_down, out_down, hidden, intermediate, out, indices,
+                  scores, workspace, workspace_bytes, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -238,6 +238,7 @@ __global__ __launch_bounds__(kKpThreads) void kp_gemm_kernel(KpGemm a) {
         acc[mt][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b0, acc[mt][0], 0, 0, 0);
         acc[mt][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b1, acc[mt][1], 0, 0, 0);
       }
+      mfma_acc_guard(acc);
     };
     auto quad = [&](const uint8_t* ab, const Piece& pc) {
       if (!active) return;

@@ -146,10 +146,10 @@ __device__ __forceinline__ void load_codebook16_lds(uint8_t* lds) {
 template <int H>
 __device__ __forceinline__ uint32_t mcg_product_half(uint32_t r, uint32_t k_hi, uint32_t k_lo) {
   uint32_t t, p;
-  asm("v_mul_u32_u24_sdwa %0, %1, %2 dst_sel:WORD_1 dst_unused:UNUSED_PAD src0_sel:WORD_%3 src1_sel:DWORD"
-      : "=v"(t)
-      : "v"(r), "s"(k_hi), "n"(H));
-  asm("v_mad_u32_u16 %0, %1, %2, %3 op_sel:[%4,0,0,0]" : "=v"(p) : "v"(r), "s"(k_lo), "v"(t), "n"(H));
+  asm volatile("v_mul_u32_u24_sdwa %0, %1, %2 dst_sel:WORD_1 dst_unused:UNUSED_PAD src0_sel:WORD_%3 src1_sel:DWORD"
+               : "=v"(t)
+               : "v"(r), "s"(k_hi), "n"(H));
+  asm volatile("v_mad_u32_u16 %0, %1, %2, %3 op_sel:[%4,0,0,0]" : "=v"(p) : "v"(r), "s"(k_lo), "v"(t), "n"(H));
   return p;
 }
 // f16 pair (cw_x, cw_y) for codewords in half HX of rx and half HY of ry, before E4M3 rounding
@@ -159,12 +159,12 @@ __device__ __forceinline__ uint32_t halves_sum_pair(uint32_t rx, uint32_t ry) {
   const uint32_t mx = (mcg_product_half<HX>(rx, k_hi, k_lo) & 0x8FFF8FFFu) ^ 0x3B603B60u;
   const uint32_t my = (mcg_product_half<HY>(ry, k_hi, k_lo) & 0x8FFF8FFFu) ^ 0x3B603B60u;
   uint32_t s;
-  asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1"
-      : "=v"(s)
-      : "v"(mx));
-  asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1"
-      : "+v"(s)
-      : "v"(my));
+  asm volatile("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1"
+               : "=v"(s)
+               : "v"(mx));
+  asm volatile("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1"
+               : "+v"(s)
+               : "v"(my));
   return s;
 }
 // An unconstrained register value: the fp8 conversions below write one half of their destination
@@ -278,9 +278,9 @@ __device__ __forceinline__ void add_halves_hi(uint32_t& s, uint32_t m) {
 template <int H>
 __device__ __forceinline__ uint32_t tab16_off(uint32_t r) {
   uint32_t o;
-  asm("v_lshlrev_b32_sdwa %0, 1, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:WORD_%2"
-      : "=v"(o)
-      : "v"(r), "n"(H));
+  asm volatile("v_lshlrev_b32_sdwa %0, 1, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:WORD_%2"
+               : "=v"(o)
+               : "v"(r), "n"(H));
   return o;
 }
 __device__ __forceinline__ uint16_t tab16_at(const uint8_t* tab, uint32_t off) {
@@ -426,6 +426,75 @@ __device__ __forceinline__ void decode_pair_words_f16(uint32_t w0, uint32_t w1, 
   }
 }
 
+// The same decode as decode_pair_words_f16 with the fp16 table, written without scheduling fences:
+// each table pair is two 16-bit LDS loads into the halves of one register, and the compiler
+// interleaves the table and arithmetic routes of the two words freely.  Measured on MI355X in a
+// register-fed quad loop: 14.0 codewords/clk/CU with NE = 1, NO = 2 (the fenced form: 12.0 at 2/2).
+template <int NE, int NO>
+__device__ __forceinline__ void decode_pair_words_h16(uint32_t w0, uint32_t w1, uint32_t prior0, const uint8_t* tab,
+                                                      f16x2 (&q)[2][4]) {
+  using piece_detail::kOut;
+  const uint32_t w[2] = {w0, w1};
+  const uint32_t pr[2] = {prior0, w0};
+  uint32_t a4[2], a8[2], a12[2];
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    a4[i] = __builtin_amdgcn_alignbit(pr[i], w[i], 4);
+    a8[i] = __builtin_amdgcn_alignbit(pr[i], w[i], 8);
+    a12[i] = __builtin_amdgcn_alignbit(pr[i], w[i], 12);
+  }
+  auto nalu = [](int i) { return (i & 1) ? NO : NE; };
+  auto xr = [&](int i, int k) { return (k & 2) ? a12[i] : a4[i]; };
+  auto yr = [&](int i, int k) { return (k & 2) ? a8[i] : w[i]; };
+#pragma unroll
+  for (int k = 0; k < 4; k++)
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+      if (k >= nalu(i)) {
+        const uint32_t ox = (k & 1) ? tab16_off<1>(xr(i, k)) : tab16_off<0>(xr(i, k));
+        const uint32_t oy = (k & 1) ? tab16_off<1>(yr(i, k)) : tab16_off<0>(yr(i, k));
+        f16x2 v;
+        v.x = *reinterpret_cast<const _Float16*>(tab + ox);
+        v.y = *reinterpret_cast<const _Float16*>(tab + oy);
+        q[i][kOut[k]] = v;
+      }
+  const uint32_t k_hi = 0xCBACu, k_lo = 0x1FEDu;
+  uint32_t sm[2][4];
+#pragma unroll
+  for (int k = 0; k < 4; k++)
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+      if (k < nalu(i)) {
+        uint32_t tx, ty;
+        if (k & 1) {
+          tx = mad_lo16<1>(xr(i, k), k_lo, mul_hi16_shifted<1>(xr(i, k), k_hi));
+          ty = mad_lo16<1>(yr(i, k), k_lo, mul_hi16_shifted<1>(yr(i, k), k_hi));
+        } else {
+          tx = mad_lo16<0>(xr(i, k), k_lo, mul_hi16_shifted<0>(xr(i, k), k_hi));
+          ty = mad_lo16<0>(yr(i, k), k_lo, mul_hi16_shifted<0>(yr(i, k), k_hi));
+        }
+        tx = (tx & 0x8FFF8FFFu) ^ 0x3B603B60u;
+        ty = (ty & 0x8FFF8FFFu) ^ 0x3B603B60u;
+        sm[i][k] = add_halves_lo(tx);
+        add_halves_hi(sm[i][k], ty);
+      }
+  int pend_i = -1, pend_k = -1;
+#pragma unroll
+  for (int k = 0; k < 4; k++)
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+      if (k < nalu(i)) {
+        if (pend_i < 0) {
+          pend_i = i;
+          pend_k = k;
+        } else {
+          round_e4m3_two(sm[pend_i][pend_k], sm[i][k], q[pend_i][kOut[pend_k]], q[i][kOut[k]]);
+          pend_i = -1;
+        }
+      }
+  if (pend_i >= 0) q[pend_i][kOut[pend_k]] = round_e4m3_pair(sm[pend_i][pend_k]);
+}
+
 // ---------------------------------------------------------------- K4 storage and MFMA fragments
 // Chunk of 8 tiles (256 K bytes at K bits: 1 KB at K4) of expert e, output block ob (128 columns),
 // input tile tk of a packed projection with `it` input tiles and `obs` output blocks (side 1:
@@ -447,6 +516,35 @@ __device__ __forceinline__ f16x8 frag(f16x2 a, f16x2 b, f16x2 c, f16x2 d) {
   typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
   const f16x4 ab = __builtin_shufflevector(a, b, 0, 1, 2, 3), cd = __builtin_shufflevector(c, d, 0, 1, 2, 3);
   return __builtin_shufflevector(ab, cd, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// Accumulator guard for MFMAs mixed with the piece decoder's inline asm.  An MFMA keeps reading its
+// accumulator input (SrcC) for several passes after issue; the compiler keeps its own VALU writes
+// out of that window (and places the wait states an MFMA result needs before a VALU reads it), but
+// it cannot see that an inline asm statement is a VALU write, and the register allocator may hand
+// an asm statement a register that an MFMA issued just before still reads as SrcC.  Called with the
+// results of each group of MFMAs right after issue: 16 wait states (longer than the SrcC read and
+// the result latency of every fp16 MFMA used here), ordered after the MFMAs by the data dependence
+// and before every later asm statement (asm volatile statements keep their order).
+__device__ __forceinline__ void mfma_acc_guard(f32x4& a, f32x4& b) { asm volatile("s_nop 15" : "+v"(a), "+v"(b)); }
+template <int N>
+__device__ __forceinline__ void mfma_acc_guard(f32x4 (&acc)[N][2]) {
+  static_assert(N == 1 || N == 2 || N == 4 || N == 8, "guard sizes");
+  if constexpr (N == 1) {
+    asm volatile("s_nop 15" : "+v"(acc[0][0]), "+v"(acc[0][1]));
+  } else if constexpr (N == 2) {
+    asm volatile("s_nop 15" : "+v"(acc[0][0]), "+v"(acc[0][1]), "+v"(acc[1][0]), "+v"(acc[1][1]));
+  } else if constexpr (N == 4) {
+    asm volatile("s_nop 15"
+                 : "+v"(acc[0][0]), "+v"(acc[0][1]), "+v"(acc[1][0]), "+v"(acc[1][1]), "+v"(acc[2][0]),
+                   "+v"(acc[2][1]), "+v"(acc[3][0]), "+v"(acc[3][1]));
+  } else {
+    asm volatile("s_nop 15"
+                 : "+v"(acc[0][0]), "+v"(acc[0][1]), "+v"(acc[1][0]), "+v"(acc[1][1]), "+v"(acc[2][0]),
+                   "+v"(acc[2][1]), "+v"(acc[3][0]), "+v"(acc[3][1]), "+v"(acc[4][0]), "+v"(acc[4][1]),
+                   "+v"(acc[5][0]), "+v"(acc[5][1]), "+v"(acc[6][0]), "+v"(acc[6][1]), "+v"(acc[7][0]),
+                   "+v"(acc[7][1]));
+  }
 }
 
 // A operand of the K4 fp16 MFMAs: row r of a 16-row input tile -> (row half rh, position j inside

@@ -20,12 +20,26 @@ int device_cus();
 // Device address of the current device's 64 KB E4M3 code table (after ensure_device_ready), for
 // kernels of other translation units.
 const uint8_t* codebook_device_table();
+// The same table as fp16 values (128 KB).
+const uint16_t* codebook_f16_device_table();
 
 // Router GEMV + route + dispatch plan for decode batches (router.hip).
 int moe_router_fused_plan(const uint16_t* x, const float* w, const float* bias, int rows, int hidden, int experts,
                           float* logits, uint32_t* ids, float* scores, Plan* plan, int32_t* counter, hipStream_t s,
                           const uint16_t* attn = nullptr, const uint16_t* norm_w = nullptr, float eps = 0.0f,
                           uint16_t* h_out = nullptr, uint16_t* xn_out = nullptr);
+
+// Fused K4 decode block (k4_layer.hip): route = 1 runs the router and plan on the device (slot 8 of
+// every row = the shared expert, id 256), route = 0 uses the plan in the layer workspace, built
+// beforehand from ids.  combine = 1 writes out (scores [rows, 8], residual), else per-slot values.
+size_t k4_layer_workspace_bytes(int h, int m);
+bool k4_layer_supported(int h, int m, bool route);
+int k4_layer_run(const uint16_t* x, const uint16_t* residual, int rows, int route, const float* router_w,
+                 const float* bias, uint32_t* ids, float* scores, const uint8_t* const packed[3],
+                 const uint16_t* const in_scale[3], const uint16_t* const out_scale[3], int h, int m, int experts,
+                 int combine, uint16_t* out, uint16_t* values, void* layer_ws, hipStream_t s);
+// The layer workspace's plan (where a plan kernel writes it for route = 0).
+Plan* k4_layer_plan(void* layer_ws);
 
 }  // namespace moe
 

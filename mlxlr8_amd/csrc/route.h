@@ -49,6 +49,7 @@ __device__ __forceinline__ RouteInput route_load(const float* __restrict__ logit
   return in;
 }
 
+template <bool COH_OUT = false>
 __device__ __forceinline__ void route_select(const RouteInput& in, int row, uint32_t* __restrict__ ids,
                                              float* __restrict__ scores, int32_t* sid, bool store_global);
 
@@ -63,7 +64,9 @@ __device__ __forceinline__ void route_row(const float* __restrict__ logits, cons
 // 255 - id).  Keys are unique, so "top 8 by descending choice, ties to the lower id" is exactly
 // "the 8 largest keys".  Each of the 40 bisection steps counts candidates with wave ballots (no
 // LDS round trip); the 8 winners are then ranked against each other and the scores summed in
-// rank order.
+// rank order.  COH_OUT: ids and scores are stored write-through (read by other CUs in the same
+// launch).
+template <bool COH_OUT>
 __device__ __forceinline__ void route_select(const RouteInput& in, int row, uint32_t* __restrict__ ids,
                                              float* __restrict__ scores, int32_t* sid, bool store_global) {
   const int lane = lane_id();
@@ -127,8 +130,16 @@ __device__ __forceinline__ void route_select(const RouteInput& in, int row, uint
     float total = 1e-20f;
 #pragma unroll
     for (int i = 0; i < 8; i++) total += sel[i];
-    if (lane < 8) scores[(int64_t)row * 8 + lane] = sel[lane] / total * 2.5f;
-    ids[(int64_t)row * 9 + lane] = lane < 8 ? (uint32_t)idl[lane] : 256u;
+    const uint32_t id = lane < 8 ? (uint32_t)idl[lane] : 256u;
+    if (COH_OUT) {
+      if (lane < 8)
+        __hip_atomic_store(scores + (int64_t)row * 8 + lane, sel[lane] / total * 2.5f, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_SYSTEM);
+      __hip_atomic_store(ids + (int64_t)row * 9 + lane, id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    } else {
+      if (lane < 8) scores[(int64_t)row * 8 + lane] = sel[lane] / total * 2.5f;
+      ids[(int64_t)row * 9 + lane] = id;
+    }
   }
   if (sid != nullptr && lane < 9) sid[row * 9 + lane] = lane < 8 ? idl[lane] : 256;
 }
