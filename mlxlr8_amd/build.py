@@ -19,6 +19,12 @@ FLAGS = [
     # packed fp32 vector ops are kept out of generated code
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
+# Per-source additions.  The fused decode block claims work with single-lane atomics whose result
+# it reads late on purpose; the atomic optimizer would rewrite them into wave-wide atomics that
+# read the result at once (and so wait for every memory operation issued before them).
+FILE_FLAGS = {
+    "k4_layer.hip": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"],
+}
 
 
 def sources():
@@ -33,7 +39,7 @@ def build(verbose=False):
 
         def compile_one(src):
             obj = Path(tmp) / (src.stem + ".o")
-            cmd = [hipcc, *FLAGS, "-c", str(src), "-o", str(obj)]
+            cmd = [hipcc, *FLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
             r = subprocess.run(cmd, capture_output=True, text=True)
             if r.returncode != 0:
                 raise RuntimeError(f"hipcc failed for {src.name}:\n{r.stderr}")

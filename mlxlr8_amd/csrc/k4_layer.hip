@@ -17,12 +17,17 @@
 //   * Items.  A part is 2 quads (8 KB of K4 weights): 128 input rows x 128 output columns of one
 //     (unit, projection, output block) -- exactly one H128 block of its input.  The list, in
 //     dependency order (an item only ever waits for items before it):
-//         [GU(0)] [router] [route] [GU(1)] [GF(0)] [GU(2)] [GF(1)] ... [GU(U-1)] [GF(U-2)] [GF(U-1)]
-//         [D(0)] [D(1)] [DF(0)] [D(2)] [DF(1)] ... [D(U-1)] [DF(U-2)] [DF(U-1)]
+//         [router] [GU(0)] [GU(1)] [GU(2)] [GF(0)] [GU(3)] [GF(1)] ... [GF(U-1)]
+//         [D(0)] [D(1)] [D(2)] [D(3)] [DF(0)] [D(4)] [DF(1)] ... [DF(U-1)]
 //     Unit 0 is the shared expert (it needs no routing, so its gate/up parts run beside the
 //     router); GU(u) are unit u's gate/up parts, GF(u) its gate finishes (one per column block:
 //     the down input), D(u) its down parts, DF(u) its down finishes (one per output block; the
-//     last unit's also combine that output block of every row).
+//     last unit's also combine that output block of every row).  A finisher trails the parts it
+//     sums by a few units.
+//   * Routing.  Router items store partial logits over fixed input slices.  Each block's first
+//     wave that reaches an item past GU(0) routes every row itself (top-8 into the block's LDS
+//     plan table, the same in every block) while the block's other waves that need the table
+//     wait on an LDS word: there is no plan hand-over between blocks.
 //   * Queue.  The list is dealt round-robin over 8 sub-lists, one per XCD (block b serves sub-list
 //     b mod 8); a wave claims its next item with one atomic on its sub-list's counter a whole item
 //     ahead of use, so a wave that waited or finished something simply claims fewer items.  Any
@@ -72,13 +77,13 @@ constexpr int kXcds = 8;            // queue sub-lists
 constexpr int kQueueStride = 32;    // ints between sub-list counters (one 128 B line each)
 
 enum LayerFin { LFIN_VALUES = 0, LFIN_COMBINE = 1 };
-enum LayerFlag { LF_PLAN = 0, LF_ERROR = 1, LF_EXIT = 2, LF_EPOCH = 3, LF_COUNT = 8 };
+enum LayerFlag { LF_ERROR = 1, LF_EXIT = 2, LF_EPOCH = 3, LF_COUNT = 8 };
 
 struct LayerWs {
   Plan* plan;
   int32_t* flags;        // LayerFlag words
   int32_t* queue;        // [kXcds][kQueueStride] sub-list counters
-  uint64_t* logit_part;  // [kMaxRows][256][h / kRouterSlice] tagged
+  uint64_t* logit_part;  // [kMaxRows][h / kRouterSlice][256] tagged
   uint64_t* partial;     // [slot][3 (h/128)(m/128) parts][128] tagged
   uint64_t* down_xh;     // [slot][m] tagged
   uint64_t* yslot;       // [slot][h] tagged
@@ -106,6 +111,16 @@ struct LayerArgs {
   uint16_t* values;          // values [slots, h]
   LayerWs w;
 };
+
+// The lane index recomputed where it is used.  Code that runs rarely (router items, routing,
+// finishes) uses it: with the plain index the compiler hoists their lane-derived addresses to the
+// kernel's start, keeps them live across the decode loop and spills its registers to memory, and
+// every reload in a latency-critical item then costs a memory round trip.
+__device__ __forceinline__ int cold_lane() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
 
 // ---------------------------------------------------------------- coherent and tagged words
 __device__ __forceinline__ int ld_coh_i(const int32_t* p) {
@@ -152,26 +167,26 @@ __device__ __forceinline__ f32x2 ld_tag_pair(const LayerArgs& a, const uint64_t*
   return f32x2{tag_value(w0), tag_value(w1)};
 }
 
-// ---------------------------------------------------------------- plan in registers
-// After the plan is published every wave holds it lane-indexed: lane l describes unit l (units
-// 0..63) and unit 64 + l (lanes 0..7): expert id, token count, and the unit's token rows (3 bits
-// each) and slots (7 bits each) packed.
-struct PlanRegs {
-  int units;
-  int ex[2], nt[2];
-  uint32_t tok[2];
-  uint32_t sl[2][2];
+// ---------------------------------------------------------------- plan in LDS
+// Each block holds the plan in LDS: per unit the expert id, the token count, the unit's token rows
+// (3 bits each) and slots (7 bits each) packed, and (when the launch routes) the rows' scores.
+// A routing launch computes it in every block; otherwise it is copied from the prebuilt plan.
+struct PlanLds {
+  int32_t units;
+  int32_t ex[kMaxUnits], nt[kMaxUnits];
+  uint32_t tok[kMaxUnits], sl0[kMaxUnits], sl1[kMaxUnits];
+  float score[kMaxRows * 8];
 };
-__device__ __forceinline__ PlanRegs load_plan(const Plan* P) {
-  PlanRegs r;
-  r.units = min(max(__builtin_amdgcn_readfirstlane(ld_coh_i(&P->units)), 1), kMaxUnits);
+// Returns the unit count.  Every word is requested unconditionally (indices clamped into the
+// arrays) so the loads issue back to back; units beyond the count are stored as empty.
+__device__ __forceinline__ int load_plan(const Plan* P, PlanLds& T) {
+  const int units = min(max(__builtin_amdgcn_readfirstlane(ld_coh_i(&P->units)), 1), kMaxUnits);
   const int lane = lane_id();
-  // every word is requested unconditionally (lane indices clamped into the arrays) so the loads
-  // issue back to back; units beyond the count are masked afterwards
 #pragma unroll
   for (int h = 0; h < 2; h++) {
+    if (h == 1 && units <= 64) break;
     const int u = min(lane + 64 * h, kMaxUnits - 1);
-    const bool ok = lane + 64 * h < r.units;
+    const bool ok = lane + 64 * h < units;
     const int ex = ld_coh_i(&P->expert[u]);
     const int nt = ld_coh_i(&P->ntok[u]);
     int tks[kMaxRows], sls[kMaxRows];
@@ -180,22 +195,25 @@ __device__ __forceinline__ PlanRegs load_plan(const Plan* P) {
       tks[t] = ld_coh_i(&P->tok[u][t]);
       sls[t] = ld_coh_i(&P->slot[u][t]);
     }
-    r.ex[h] = ok ? ex : 0;
-    r.nt[h] = ok ? nt : 0;
     uint32_t tp = 0, s0 = 0, s1 = 0;
 #pragma unroll
     for (int t = 0; t < kMaxRows; t++) {
-      const int tk = ok ? tks[t] : 0;
-      const int sl = ok ? sls[t] : 0;
-      tp |= (uint32_t)(tk & 7) << (3 * t);
-      if (t < 4) s0 |= (uint32_t)(sl & 127) << (7 * t);
-      else s1 |= (uint32_t)(sl & 127) << (7 * (t - 4));
+      tp |= (uint32_t)(tks[t] & 7) << (3 * t);
+      if (t < 4) s0 |= (uint32_t)(sls[t] & 127) << (7 * t);
+      else s1 |= (uint32_t)(sls[t] & 127) << (7 * (t - 4));
     }
-    r.tok[h] = tp;
-    r.sl[h][0] = s0;
-    r.sl[h][1] = s1;
+    if (lane + 64 * h < kMaxUnits) {
+      T.ex[u] = ok ? ex : 0;
+      T.nt[u] = ok ? nt : 0;
+      T.tok[u] = tp;
+      T.sl0[u] = s0;
+      T.sl1[u] = s1;
+    }
   }
-  return r;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  return units;
 }
 // Every field is clamped into range when read, so a plan that was never published (an exhausted
 // wait) can give wrong results but no out-of-bounds access.
@@ -209,15 +227,15 @@ struct UnitInfo {
     return min(s, kMaxUnits - 1);
   }
 };
-__device__ __forceinline__ UnitInfo unit_info(const PlanRegs& r, int u, int experts, int rows) {
-  const int h = u >> 6, l = u & 63;
+__device__ __forceinline__ UnitInfo unit_info(const PlanLds& T, int u, int experts, int rows) {
+  u = min(max(u, 0), kMaxUnits - 1);
   UnitInfo i;
   i.rows = rows;
-  i.e = min(max(__builtin_amdgcn_readlane(h ? r.ex[1] : r.ex[0], l), 0), experts - 1);
-  i.ntok = min(max(__builtin_amdgcn_readlane(h ? r.nt[1] : r.nt[0], l), 0), kMaxRows);
-  i.tok = (uint32_t)__builtin_amdgcn_readlane((int)(h ? r.tok[1] : r.tok[0]), l);
-  i.sl0 = (uint32_t)__builtin_amdgcn_readlane((int)(h ? r.sl[1][0] : r.sl[0][0]), l);
-  i.sl1 = (uint32_t)__builtin_amdgcn_readlane((int)(h ? r.sl[1][1] : r.sl[0][1]), l);
+  i.e = min(max(__builtin_amdgcn_readfirstlane(T.ex[u]), 0), experts - 1);
+  i.ntok = min(max(__builtin_amdgcn_readfirstlane(T.nt[u]), 0), kMaxRows);
+  i.tok = (uint32_t)__builtin_amdgcn_readfirstlane((int)T.tok[u]);
+  i.sl0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)T.sl0[u]);
+  i.sl1 = (uint32_t)__builtin_amdgcn_readfirstlane((int)T.sl1[u]);
   return i;
 }
 
@@ -231,24 +249,27 @@ struct Items {
   int S;      // router slices per expert
   int route;
 };
-enum ItemKind { IT_GU = 0, IT_DOWN = 1, IT_ROUTER = 2, IT_ROUTE = 3, IT_GF = 4, IT_DF = 5, IT_NONE = 6 };
+enum ItemKind { IT_GU = 0, IT_DOWN = 1, IT_ROUTER = 2, IT_GF = 3, IT_DF = 4, IT_NONE = 5 };
 struct Item {
   int kind, u, a, b, c;  // GU: a = output block, b = projection, c = part; DOWN: a = output block,
                          // c = part (input block); GF / DF: a = block; ROUTER: a = item
 };
-// The list: [router R] [route] then phase A, then phase B.
-//   phase A: block b = GU(b), followed for b >= kLagG by GF(b - kLagG); then GF of the last units
-//   phase B: block b = D(b),  followed for b >= kLagD by DF(b - kLagD); then DF of the last units
-// A finisher comes kLag units after the parts it sums, so its inputs are normally complete when it
-// is taken; the last unit's down finishes (the combine) close the list.
+// The list: [router R], then phase A, then phase B.
+//   phase A: for the units 0..U-1, block b = GU(b), followed for b >= kLagG by GF(b - kLagG);
+//            then GF of the last units
+//   phase B: for the units 0..U-1, block b = D(b), followed for b >= kLagD by DF(b - kLagD);
+//            then DF of the last units
+// Unit 0 (the shared expert when routing) needs no plan, so its gate/up parts run beside the
+// router.  A finisher comes kLag units after the parts it sums, so its inputs are normally complete
+// when it is taken; the last unit's down finishes (the combine) close the list.
 constexpr int kLagG = 2, kLagD = 3;
-// items that need no plan: router, route, and GU(0) = the shared expert's gate/up parts
-__device__ __forceinline__ int pre_items(const Items& L) { return (L.route ? L.R + 1 : 0) + L.G; }
+// items that need no plan (the positions of GU(0) do not depend on the unit count)
+__device__ __forceinline__ int pre_items(const Items& L) { return L.route ? L.R + L.G : 0; }
 __device__ __forceinline__ int list_len(const Items& L, int U) {
-  return (L.route ? L.R + 1 : 0) + U * (L.G + L.MB) + U * (L.D + L.HB);
+  return (L.route ? L.R : 0) + U * (L.G + L.MB) + U * (L.D + L.HB);
 }
 // position j inside a phase of U blocks of `big` part items, each followed after `lag` blocks by
-// `small` finish items: sets (is_finish, unit, index inside the block)
+// `small` finish items: sets (is_finish, unit, index inside the block); units count from 0
 __device__ __forceinline__ void phase_at(int j, int U, int big, int small, int lag, bool& fin, int& unit, int& r) {
   const int lead = min(U, lag);  // blocks without a finish tail
   if (j < lead * big) {
@@ -277,50 +298,65 @@ __device__ __forceinline__ void phase_at(int j, int U, int big, int small, int l
   unit = mid + j / small;
   r = j - (unit - mid) * small;
 }
+__device__ __forceinline__ void set_gu(const Items& L, Item& it, int u, int r) {
+  it.kind = IT_GU;
+  it.u = u;
+  it.a = r / (2 * L.HB);
+  const int rem = r - it.a * 2 * L.HB;
+  it.b = rem / L.HB;
+  it.c = rem - it.b * L.HB;
+}
+__device__ __forceinline__ void set_down(const Items& L, Item& it, int u, int r) {
+  it.kind = IT_DOWN;
+  it.u = u;
+  it.c = r / L.HB;
+  it.a = r - it.c * L.HB;
+}
 __device__ __forceinline__ Item item_at(const Items& L, int j, int U) {
   Item it{IT_NONE, 0, 0, 0, 0};
   if (L.route) {
-    if (j < L.R) {
-      it.kind = IT_ROUTER;
-      it.a = j;
+    // The first R + G positions hold the router items and GU(0) mixed in the ratio R : G within
+    // every run of kXcds * kLW positions (one position per wave of eight blocks), so every block
+    // starts with some router items: its waves that finish them route the block early.
+    const int P = L.R + L.G;
+    if (j < P) {
+      constexpr int C = kXcds * kLW;
+      const int c0 = j - j % C, c1 = min(c0 + C, P);
+      const int r0 = c0 * L.R / P, rc = c1 * L.R / P - r0;  // below 2^31: P <= 18432, R <= 2048
+      const int o = j - c0;  // = 8 wave + sub-list for the first waves: wave < rc / 8 routes
+      if (o < rc) {
+        it.kind = IT_ROUTER;
+        it.a = r0 + o;
+        return it;
+      }
+      set_gu(L, it, 0, (c0 - r0) + (o - rc));
       return it;
     }
     j -= L.R;
-    if (j == 0) {
-      it.kind = IT_ROUTE;
-      return it;
-    }
-    j -= 1;
   }
   bool fin;
   int unit, r;
   const int lenA = U * (L.G + L.MB);
   if (j < lenA) {
     phase_at(j, U, L.G, L.MB, kLagG, fin, unit, r);
-    it.u = unit;
     if (fin) {
       it.kind = IT_GF;
+      it.u = unit;
       it.a = r;
     } else {
-      it.kind = IT_GU;
-      it.a = r / (2 * L.HB);
-      const int rem = r - it.a * 2 * L.HB;
-      it.b = rem / L.HB;
-      it.c = rem - it.b * L.HB;
+      set_gu(L, it, unit, r);
     }
     return it;
   }
   j -= lenA;
   if (j < U * (L.D + L.HB)) {
     phase_at(j, U, L.D, L.HB, kLagD, fin, unit, r);
-    it.u = unit;
     if (fin) {
       it.kind = IT_DF;
+      it.u = unit;
       it.a = r;
     } else {
-      it.kind = IT_DOWN;
-      it.c = r / L.HB;
-      it.a = r - it.c * L.HB;
+      set_down(L, it, unit, r);
     }
   }
   return it;
@@ -357,31 +393,46 @@ __device__ __forceinline__ void load_quad(u32x4 (&pc)[4], const uint8_t* qp) {
 #pragma unroll
   for (int s4 = 0; s4 < 4; s4++) pc[s4] = load_stream16(qp + 256 * s4);
 }
-// The raw input block of a part, fetched ahead of its staging: gate/up -- the bf16 x pair and the
-// in_scale pair of each token; down -- the tagged down-input pair of each token (DPRE: fetched
-// ahead, else at staging).
+// The raw input block of a part, fetched ahead of its staging.
+//   DPRE (one token): both kinds issue two 64-bit loads into r[0..1] and r[2..3] -- gate/up the
+//     aligned 8 bytes holding the lane's bf16 x pair and those holding its in_scale pair (the
+//     lane's half is picked at staging), down the two tagged down-input words.  Same loads, same
+//     registers, same order: with kind-dependent register sets the compiler keeps the other
+//     kind's words alive and copies them at the loop's joins, and a copy of a register still
+//     loading waits for every memory operation issued since (the next part's quads included).
+//   otherwise: gate/up the x pair of each token (r[t]) and the in_scale pair (r[NT]); down inputs
+//     are loaded at staging.
 template <int NT, bool DPRE>
 struct InBlock {
-  uint32_t xw[NT];
-  uint32_t sc;
-  uint64_t dw[DPRE ? NT : 1][2];
+  static_assert(!DPRE || NT == 1, "down inputs are fetched ahead for one token only");
+  uint32_t r[DPRE ? 4 : NT + 1];
 };
 template <int NT, bool DPRE>
 __device__ __forceinline__ void fetch_in(const LayerArgs& a, const UnitInfo& ui, const Item& it, InBlock<NT, DPRE>& in) {
   const int lane = lane_id();
-  if (it.kind == IT_GU) {
+  if (DPRE) {
+    uint64_t w0, w1;
+    if (it.kind == IT_GU) {
+      // 8-byte words (x and in_scale rows are 8-byte aligned): lane l's pair is half l & 1 of word
+      // l / 2 of the 128-element block
+      const int blk = 128 * it.c;
+      w0 = reinterpret_cast<const uint64_t*>(a.x + (int64_t)ui.row(0) * a.h + blk)[lane >> 1];
+      w1 = reinterpret_cast<const uint64_t*>(a.in_scale[it.b] + (int64_t)ui.e * a.h + blk)[lane >> 1];
+    } else {
+      const uint64_t* p = a.w.down_xh + (int64_t)ui.slot(0) * a.m + 128 * it.c + 2 * lane;
+      w0 = ld_tag(p);
+      w1 = ld_tag(p + 1);
+    }
+    in.r[0] = (uint32_t)w0;
+    in.r[1] = (uint32_t)(w0 >> 32);
+    in.r[2] = (uint32_t)w1;
+    in.r[3] = (uint32_t)(w1 >> 32);
+  } else if (it.kind == IT_GU) {
     const int off = 128 * it.c + 2 * lane;
-    in.sc = *reinterpret_cast<const uint32_t*>(a.in_scale[it.b] + (int64_t)ui.e * a.h + off);
 #pragma unroll
     for (int t = 0; t < NT; t++)
-      in.xw[t] = *reinterpret_cast<const uint32_t*>(a.x + (int64_t)ui.row(min(t, max(ui.ntok - 1, 0))) * a.h + off);
-  } else if (DPRE) {
-#pragma unroll
-    for (int t = 0; t < (DPRE ? NT : 1); t++) {
-      const uint64_t* p = a.w.down_xh + (int64_t)ui.slot(min(t, max(ui.ntok - 1, 0))) * a.m + 128 * it.c + 2 * lane;
-      in.dw[t][0] = ld_tag(p);
-      in.dw[t][1] = ld_tag(p + 1);
-    }
+      in.r[t] = *reinterpret_cast<const uint32_t*>(a.x + (int64_t)ui.row(min(t, max(ui.ntok - 1, 0))) * a.h + off);
+    in.r[NT] = *reinterpret_cast<const uint32_t*>(a.in_scale[it.b] + (int64_t)ui.e * a.h + off);
   }
 }
 // A fragments of the part's 128 input rows (hi and lo fp16 rows per token) into the wave's LDS
@@ -391,27 +442,30 @@ __device__ __forceinline__ void stage_in(const LayerArgs& a, const UnitInfo& ui,
                                          const InBlock<NT, DPRE>& in, uint32_t tag, _Float16* __restrict__ xw) {
   const int lane = lane_id();
   float v0[NT], v1[NT];
+  uint32_t w[4] = {0u, 0u, 0u, 0u};
+  if (DPRE) {
+#pragma unroll
+    for (int k = 0; k < 4; k++) w[k] = in.r[k];
+  }
   if (it.kind == IT_GU) {
-    const float s0 = f16_to_f32((uint16_t)(in.sc & 0xFFFFu)), s1 = f16_to_f32((uint16_t)(in.sc >> 16));
+    const bool odd = (lane & 1) != 0;
+    const uint32_t scw = DPRE ? (odd ? w[3] : w[2]) : in.r[NT];
+    const float s0 = f16_to_f32((uint16_t)(scw & 0xFFFFu)), s1 = f16_to_f32((uint16_t)(scw >> 16));
 #pragma unroll
     for (int t = 0; t < NT; t++) {
       if (t < ui.ntok) {
-        v0[t] = bf16_to_f32((uint16_t)(in.xw[t] & 0xFFFFu)) * s0;
-        v1[t] = bf16_to_f32((uint16_t)(in.xw[t] >> 16)) * s1;
+        const uint32_t xw2 = DPRE ? (odd ? w[1] : w[0]) : in.r[t];
+        v0[t] = bf16_to_f32((uint16_t)(xw2 & 0xFFFFu)) * s0;
+        v1[t] = bf16_to_f32((uint16_t)(xw2 >> 16)) * s1;
         hadamard128_wave(v0[t], v1[t]);
       }
     }
   } else {
     bool ready = true;
     if (DPRE) {
-#pragma unroll
-      for (int t = 0; t < (DPRE ? NT : 1); t++) {
-        if (t < ui.ntok) {
-          ready = ready && has_tag(in.dw[t][0], tag) && has_tag(in.dw[t][1], tag);
-          v0[t] = tag_value(in.dw[t][0]);
-          v1[t] = tag_value(in.dw[t][1]);
-        }
-      }
+      ready = w[1] == tag && w[3] == tag;
+      v0[0] = __uint_as_float(w[0]);
+      v1[0] = __uint_as_float(w[2]);
     }
     if (!DPRE || !__all(ready)) {
 #pragma unroll
@@ -485,13 +539,34 @@ __device__ __forceinline__ void decode_quad(const u32x4 (&pc)[4], int qb, int nt
   }
 }
 // The part's partial sums: token t = D rows 2t, 2t + 1, held by lanes 16 (t / 2) + n, registers
-// 2 (t % 2), +1.  Tagged stores, never waited for.
+// 2 (t % 2), +1.  Tagged stores, never waited for.  One token: the 128 sums pass through the
+// wave's LDS row `pst` so that every lane stores two columns with no branch around the stores
+// (stores under a branch leave the compiler unsure how many are outstanding, and it then waits
+// for all of them before the next part's staging).
 template <int NT>
 __device__ __forceinline__ void store_partials(const LayerArgs& a, const UnitInfo& ui, const Item& it,
-                                               const f32x4 (&acc)[4][2], uint32_t tag, const Items& L) {
+                                               const f32x4 (&acc)[4][2], uint32_t tag, const Items& L,
+                                               float* __restrict__ pst) {
   const int lane = lane_id();
   const int g = lane >> 4, nn = lane & 15;
   const int index = it.kind == IT_GU ? (it.b * L.MB + it.a) * L.HB + it.c : 2 * L.MB * L.HB + it.a * L.MB + it.c;
+  if (NT == 1) {
+    if (g == 0) {
+#pragma unroll
+      for (int s4 = 0; s4 < 4; s4++)
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++)
+          pst[16 * (2 * s4 + (nn >> 3)) + (nn & 7) + 8 * hh] = fmaf(acc[s4][hh][1], 1.0f / 2048.0f, acc[s4][hh][0]);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const f32x2 v = *reinterpret_cast<const f32x2*>(pst + 2 * lane);
+    uint64_t* pw = part_ptr(a, ui.slot(0), index) + 2 * lane;
+    st_tag(pw, v.x, tag);
+    st_tag(pw + 1, v.y, tag);
+    return;
+  }
 #pragma unroll
   for (int t = 0; t < NT; t++) {
     if (t < ui.ntok && g == (t >> 1)) {
@@ -509,48 +584,63 @@ __device__ __forceinline__ void store_partials(const LayerArgs& a, const UnitInf
 }
 
 // ---------------------------------------------------------------- finishes
-// Sum of the partials of parts [0, n) at p (stride 128 words) for columns 2 lane, 2 lane + 1, in
-// part order, once every word carries `tag`.
-__device__ __forceinline__ f32x2 sum_parts(const LayerArgs& a, const uint64_t* p, int n, uint32_t tag) {
-  const int lane = lane_id();
-  f32x2 s = {0.0f, 0.0f};
-  for (int i0 = 0; i0 < n; i0 += 16) {
-    // all 32 words of a batch are requested before any is examined (indices clamped, not branched
-    // on, so the loads issue back to back); the batch is reloaded until every word is current
-    uint64_t w[16][2];
-    int spins = 0;
-    // a sample of the batch first (one word per lane: four per part), so a wait costs 1 KB per poll
-    // instead of the batch's 16 KB
-    for (;;) {
-      const uint64_t* q = p + (int64_t)min(i0 + (lane & 15), n - 1) * 128 + ((lane >> 4) * 37 + 11) % 128;
-      if (__all(has_tag(ld_tag(q), tag)) || !keep_waiting(a, spins)) break;
-    }
+// Sums, for each of the K part rows p[k], of the partials of parts [0, n) (stride 128 words) for
+// columns 2 lane, 2 lane + 1, in part order, once every word carries `tag`.  Rounds of B parts per
+// row: every word of a round is requested before any is examined (indices clamped, not branched
+// on, so the loads issue back to back).  A round that is not complete is waited for on a sample
+// (one word per lane), so a waiting wave costs 512 B per poll instead of the round's, and loaded
+// again.
+template <int K, int B>
+__device__ __forceinline__ void sum_parts(const LayerArgs& a, const uint64_t* const (&p)[K], int n, uint32_t tag,
+                                          f32x2 (&s)[K]) {
+  const int lane = cold_lane();
+#pragma unroll
+  for (int k = 0; k < K; k++) s[k] = f32x2{0.0f, 0.0f};
+  int spins = 0;
+  for (int i0 = 0; i0 < n; i0 += B) {
+    uint64_t w[K][B][2];
     for (;;) {
 #pragma unroll
-      for (int i = 0; i < 16; i++) {
-        const uint64_t* q = p + (int64_t)min(i0 + i, n - 1) * 128 + 2 * lane;
-        w[i][0] = ld_tag(q);
-        w[i][1] = ld_tag(q + 1);
-      }
+      for (int k = 0; k < K; k++)
+#pragma unroll
+        for (int i = 0; i < B; i++) {
+          const uint64_t* q = p[k] + (int64_t)min(i0 + i, n - 1) * 128 + 2 * lane;
+          w[k][i][0] = ld_tag(q);
+          w[k][i][1] = ld_tag(q + 1);
+        }
       bool ok = true;
 #pragma unroll
-      for (int i = 0; i < 16; i++) ok = ok & has_tag(w[i][0], tag) & has_tag(w[i][1], tag);
-      if (__all(ok) || !keep_waiting(a, spins)) break;
+      for (int k = 0; k < K; k++)
+#pragma unroll
+        for (int i = 0; i < B; i++) ok = ok & (int)has_tag(w[k][i][0], tag) & (int)has_tag(w[k][i][1], tag);
+      if (__all(ok)) break;
+      bool live = true;
+      for (;;) {
+        const int k = K == 1 ? 0 : (lane >> 5) % K;
+        const uint64_t* q = p[k] + (int64_t)min(i0 + (lane & 31) % B, n - 1) * 128 + (lane * 37 + 11) % 128;
+        if (__all(has_tag(ld_tag(q), tag))) break;
+        if (!keep_waiting(a, spins)) {
+          live = false;
+          break;
+        }
+      }
+      if (!live) break;
     }
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-      if (i0 + i < n) {
-        s.x += tag_value(w[i][0]);
-        s.y += tag_value(w[i][1]);
+    for (int k = 0; k < K; k++)
+#pragma unroll
+      for (int i = 0; i < B; i++) {
+        if (i0 + i < n) {
+          s[k].x += tag_value(w[k][i][0]);
+          s[k].y += tag_value(w[k][i][1]);
+        }
       }
-    }
   }
-  return s;
 }
 
 // gate finish of column block ob of unit ui: the down input of each of its tokens
 __device__ void gate_finish(const LayerArgs& a, const UnitInfo& ui, int ob, uint32_t tag, const Items& L) {
-  const int lane = lane_id();
+  const int lane = cold_lane();
   const int col = ob * 128 + 2 * lane;
   const int64_t si = (int64_t)ui.e * a.m + col;
   const uint32_t og = *reinterpret_cast<const uint32_t*>(a.out_scale[0] + si);
@@ -560,9 +650,10 @@ __device__ void gate_finish(const LayerArgs& a, const UnitInfo& ui, int ob, uint
   auto hi = [](uint32_t v) { return f16_to_f32((uint16_t)(v >> 16)); };
   for (int t = 0; t < ui.ntok; t++) {
     const int s = ui.slot(t);
-    const f32x2 g = sum_parts(a, part_ptr(a, s, (0 * L.MB + ob) * L.HB), L.HB, tag);
-    const f32x2 uu = sum_parts(a, part_ptr(a, s, (1 * L.MB + ob) * L.HB), L.HB, tag);
-    float g0 = g.x, g1 = g.y, u0 = uu.x, u1 = uu.y;
+    const uint64_t* rows[2] = {part_ptr(a, s, (0 * L.MB + ob) * L.HB), part_ptr(a, s, (1 * L.MB + ob) * L.HB)};
+    f32x2 gu[2];
+    sum_parts<2, 8>(a, rows, L.HB, tag, gu);
+    float g0 = gu[0].x, g1 = gu[0].y, u0 = gu[1].x, u1 = gu[1].y;
     hadamard128_wave(g0, g1);
     hadamard128_wave(u0, u1);
     float h0 = swiglu_bf16(g0 * lo(og), u0 * lo(ou));
@@ -576,19 +667,16 @@ __device__ void gate_finish(const LayerArgs& a, const UnitInfo& ui, int ob, uint
   }
 }
 
-// combine of output block ob over all rows (reference sum order, shared, residual)
-__device__ void combine_block(const LayerArgs& a, int ob, uint32_t tag) {
-  const int lane = lane_id();
+// combine of output block ob over all rows (reference sum order, shared, residual); `score` is the
+// rows' [rows, 8] scores (the block's plan table when the launch routes, else the caller's)
+__device__ void combine_block(const LayerArgs& a, int ob, uint32_t tag, const float* score) {
+  const int lane = cold_lane();
   const int col = ob * 128 + 2 * lane;
   for (int r = 0; r < a.rows; r++) {
     f32x2 y[kSlots];
     {
       uint64_t w[kSlots][2];
       int spins = 0;
-      for (;;) {
-        const uint64_t* q = a.w.yslot + (int64_t)(r * kSlots + lane % kSlots) * a.h + col;
-        if (__all(has_tag(ld_tag(q), tag)) || !keep_waiting(a, spins)) break;
-      }
       for (;;) {
 #pragma unroll
         for (int j = 0; j < kSlots; j++) {
@@ -598,15 +686,25 @@ __device__ void combine_block(const LayerArgs& a, int ob, uint32_t tag) {
         }
         bool ok = true;
 #pragma unroll
-        for (int j = 0; j < kSlots; j++) ok = ok & has_tag(w[j][0], tag) & has_tag(w[j][1], tag);
-        if (__all(ok) || !keep_waiting(a, spins)) break;
+        for (int j = 0; j < kSlots; j++) ok = ok & (int)has_tag(w[j][0], tag) & (int)has_tag(w[j][1], tag);
+        if (__all(ok)) break;
+        bool live = true;
+        for (;;) {
+          const uint64_t* q = a.w.yslot + (int64_t)(r * kSlots + lane % kSlots) * a.h + col;
+          if (__all(has_tag(ld_tag(q), tag))) break;
+          if (!keep_waiting(a, spins)) {
+            live = false;
+            break;
+          }
+        }
+        if (!live) break;
       }
 #pragma unroll
       for (int j = 0; j < kSlots; j++) y[j] = f32x2{tag_value(w[j][0]), tag_value(w[j][1])};
     }
     float sc[8];
 #pragma unroll
-    for (int j = 0; j < 8; j++) sc[j] = a.route ? ld_coh_f(a.scores + r * 8 + j) : a.scores[r * 8 + j];
+    for (int j = 0; j < 8; j++) sc[j] = score[r * 8 + j];
     float tot0 = y[0].x * sc[0] + 0.0f, tot1 = y[0].y * sc[0] + 0.0f;
 #pragma unroll
     for (int j = 1; j < 8; j++) {
@@ -625,15 +723,18 @@ __device__ void combine_block(const LayerArgs& a, int ob, uint32_t tag) {
 
 // down finish of output block ob of unit ui: per-slot values, or the slot outputs for the combine
 // (and, for the last unit, the combine of the block)
-__device__ void down_finish(const LayerArgs& a, const UnitInfo& ui, int ob, bool last, uint32_t tag, const Items& L) {
-  const int lane = lane_id();
+__device__ void down_finish(const LayerArgs& a, const UnitInfo& ui, int ob, bool last, uint32_t tag, const Items& L,
+                            const float* score) {
+  const int lane = cold_lane();
   const int col = ob * 128 + 2 * lane;
   const uint32_t osc = *reinterpret_cast<const uint32_t*>(a.out_scale[2] + (int64_t)ui.e * a.h + col);
   const float os0 = f16_to_f32((uint16_t)(osc & 0xFFFFu)), os1 = f16_to_f32((uint16_t)(osc >> 16));
   for (int t = 0; t < ui.ntok; t++) {
     const int s = ui.slot(t);
-    const f32x2 v = sum_parts(a, part_ptr(a, s, 2 * L.MB * L.HB + ob * L.MB), L.MB, tag);
-    float v0 = v.x, v1 = v.y;
+    const uint64_t* rows[1] = {part_ptr(a, s, 2 * L.MB * L.HB + ob * L.MB)};
+    f32x2 v[1];
+    sum_parts<1, 16>(a, rows, L.MB, tag, v);
+    float v0 = v[0].x, v1 = v[0].y;
     hadamard128_wave(v0, v1);
     if (a.fin == LFIN_VALUES) {
       const uint32_t packed2 = (uint32_t)f32_to_bf16(v0 * os0) | ((uint32_t)f32_to_bf16(v1 * os1) << 16);
@@ -646,16 +747,16 @@ __device__ void down_finish(const LayerArgs& a, const UnitInfo& ui, int ob, bool
   }
   if (a.fin == LFIN_COMBINE && last) {
     release_stores();  // this wave's own slot outputs are read back by the combine
-    combine_block(a, ob, tag);
+    combine_block(a, ob, tag, score);
   }
 }
 
 // ---------------------------------------------------------------- router
 // item r = e * S + j: partial logit of expert e over inputs [kRouterSlice j, kRouterSlice (j + 1))
-// for every row, stored tagged at logit_part[(row * 256 + e) * S + j].
+// for every row, stored tagged at logit_part[(row * S + j) * 256 + e].
 __device__ __forceinline__ void router_item(const LayerArgs& a, int r, int S, uint32_t tag) {
   const int e = r / S, j = r - e * S;
-  const int lane = lane_id();
+  const int lane = cold_lane();
   constexpr int kPer = kRouterSlice / 64;  // 16 inputs per lane
   const int k0 = j * kRouterSlice + kPer * lane;
   f32x4 w[kPer / 4];
@@ -679,92 +780,154 @@ __device__ __forceinline__ void router_item(const LayerArgs& a, int r, int S, ui
       acc = fmaf(bf16_to_f32((uint16_t)(xv[i].w >> 16)), wb.w, acc);
     }
     const float tot = wave_sum(acc);
-    if (lane == 63) st_tag(a.w.logit_part + ((int64_t)row * 256 + e) * S + j, tot, tag);
+    if (lane == 63) st_tag(a.w.logit_part + ((int64_t)row * S + j) * 256 + e, tot, tag);
   }
 }
 
-// The routing item: logits from their slices (slice order), top-8 per row, then the plan with the
-// shared expert as unit 0 and the routed experts in first-appearance order (routed slot order),
-// published by the plan word = tag.
-__device__ void route_and_plan(const LayerArgs& a, int S, uint32_t tag) {
-  const int lane = lane_id();
-  __shared__ int32_t sid_lds[kMaxUnits];
+// Routing of every row by one wave into its block's plan table: logits summed over their slices in
+// slice order, bias-corrected top-8 per row, then the units -- the shared expert as unit 0 and the
+// routed experts in first-appearance (slot) order.  Every block computes the same table from the
+// same words; block 0 also stores ids and scores for the caller.
+__device__ void route_block(const LayerArgs& a, int S, uint32_t tag, PlanLds& T) {
+  const int lane = cold_lane();
+  __shared__ int32_t sid_lds[kMaxRows * kSlots];
   constexpr int kMaxS = kMaxRouteHidden / kRouterSlice;
+  float bias[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) bias[i] = a.bias[lane + 64 * i];
   for (int row = 0; row < a.rows; row++) {
-    RouteInput in;
-    const uint64_t* lp = a.w.logit_part + ((int64_t)row * 256 + lane) * S;
-    // every slice word of the lane's four experts in one round trip, reloaded until all are current
-    uint64_t wd[4][kMaxS];
+    const uint64_t* lp = a.w.logit_part + (int64_t)row * S * 256;
     int spins = 0;
+    // every word of the lane's four experts in one round trip; while some are not yet current, a
+    // sample (one word per lane spread over the row's slices) is polled before loading them again
+    uint64_t wd[kMaxS][4];
     for (;;) {
 #pragma unroll
-      for (int i = 0; i < 4; i++)
+      for (int j = 0; j < kMaxS; j++)
 #pragma unroll
-        for (int j = 0; j < kMaxS; j++) wd[i][j] = ld_tag(lp + (int64_t)64 * i * S + min(j, S - 1));
+        for (int i = 0; i < 4; i++) wd[j][i] = ld_tag(lp + (int64_t)min(j, S - 1) * 256 + lane + 64 * i);
       bool ok = true;
 #pragma unroll
-      for (int i = 0; i < 4; i++)
+      for (int j = 0; j < kMaxS; j++)
 #pragma unroll
-        for (int j = 0; j < kMaxS; j++) ok = ok & has_tag(wd[i][j], tag);
-      if (__all(ok) || !keep_waiting(a, spins)) break;
+        for (int i = 0; i < 4; i++) ok = ok & has_tag(wd[j][i], tag);
+      if (__all(ok)) break;
+      bool live = true;
+      for (;;) {
+        if (__all(has_tag(ld_tag(lp + (lane * 24 + 7) % (S * 256)), tag))) break;
+        if (!keep_waiting(a, spins)) {
+          live = false;
+          break;
+        }
+      }
+      if (!live) break;
     }
+    RouteInput in;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       float v = 0.0f;
 #pragma unroll
       for (int j = 0; j < kMaxS; j++)
-        if (j < S) v += tag_value(wd[i][j]);
+        if (j < S) v += tag_value(wd[j][i]);
       in.logit[i] = v;
-      in.bias[i] = a.bias[lane + 64 * i];
+      in.bias[i] = bias[i];
     }
-    route_select<true>(in, row, a.ids, a.scores, sid_lds, true);
+    route_select<false>(in, row, a.ids, a.scores, sid_lds, blockIdx.x == 0, T.score);
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  // routed slot s' = 8 row + k (lane s'), global slot 9 row + k
-  Plan* P = a.w.plan;
+  // Units.  Routed slot s' = 8 row + k is lane s' (global slot 9 row + k).  A row holds each expert
+  // at most once, so a slot's position inside its unit is the number of earlier rows that chose the
+  // same expert; the unit's first slot (position 0) leads it, and units are numbered in the order
+  // of their leading slots.  Per-row expert bitmaps in LDS answer both questions in one pass over
+  // the rows; the unit's rows and slots are then merged with LDS or (order-free).
+  __shared__ uint32_t row_bits[kMaxRows][8];  // row r: bit e when expert e is in the row's top-8
+  __shared__ uint8_t row_rank[kMaxRows][256];  // row r, expert e: its rank in the row (where set)
   const int n = a.rows * 8;
   const bool act = lane < n;
   const int row = lane >> 3, k = lane & 7;
-  const int e = act ? sid_lds[row * 9 + k] : -1;
-  int pos = 0, total = 0, first_lane = lane;
-  for (int q = 0; q < n; q++) {
-    const int eq = __builtin_amdgcn_readlane(e, q);
-    const bool same = eq == e;
-    if (same && q < lane) {
-      if (pos == 0) first_lane = q;
-      pos++;
-    }
-    total += same ? 1 : 0;
+  const int e = act ? min(max(sid_lds[row * kSlots + k], 0), 255) : 0;
+  row_bits[lane >> 3][lane & 7] = 0u;
+  for (int u = lane; u < kMaxUnits; u += 64) {
+    T.tok[u] = 0u;
+    T.sl0[u] = 0u;
+    T.sl1[u] = 0u;
   }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if (act) {
+    __hip_atomic_fetch_or(&row_bits[row][e >> 5], 1u << (e & 31), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    row_rank[row][e] = (uint8_t)k;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  int pos = 0, total = 0, first_row = row;
+  for (int r = a.rows - 1; r >= 0; r--) {
+    const int b = (int)((row_bits[r][e >> 5] >> (e & 31)) & 1u);
+    total += b;
+    pos += r < row ? b : 0;
+    first_row = b ? r : first_row;
+  }
+  const int first_lane = first_row * 8 + row_rank[first_row][e];
   const uint64_t firsts = __ballot(act && pos == 0);
   const int unit = 1 + (int)__popcll(firsts & ((1ull << first_lane) - 1ull));
   if (act) {
-    const int gs = row * 9 + k;
     if (pos == 0) {
-      st_coh_i(&P->expert[unit], e);
-      st_coh_i(&P->ntok[unit], total);
+      T.ex[unit] = e;
+      T.nt[unit] = total;
     }
-    st_coh_i(&P->tok[unit][pos], row);
-    st_coh_i(&P->slot[unit][pos], gs);
-    st_coh_i(&P->slot_unit[gs], unit);
-    st_coh_i(&P->slot_pos[gs], pos);
-  }
-  if (lane < a.rows) {
-    st_coh_i(&P->tok[0][lane], lane);
-    st_coh_i(&P->slot[0][lane], lane * 9 + 8);
-    st_coh_i(&P->slot_unit[lane * 9 + 8], 0);
-    st_coh_i(&P->slot_pos[lane * 9 + 8], lane);
+    const uint32_t gs = (uint32_t)(row * kSlots + k);
+    __hip_atomic_fetch_or(&T.tok[unit], (uint32_t)row << (3 * pos), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (pos < 4)
+      __hip_atomic_fetch_or(&T.sl0[unit], gs << (7 * pos), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    else
+      __hip_atomic_fetch_or(&T.sl1[unit], gs << (7 * (pos - 4)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
   if (lane == 0) {
-    st_coh_i(&P->expert[0], 256);
-    st_coh_i(&P->ntok[0], a.rows);
-    st_coh_i(&P->units, 1 + (int)__popcll(firsts));
-    st_coh_i(&P->rows, a.rows);
+    uint32_t t0 = 0, z0 = 0, z1 = 0;
+    for (int r = 0; r < a.rows; r++) {
+      t0 |= (uint32_t)r << (3 * r);
+      if (r < 4) z0 |= (uint32_t)(r * kSlots + 8) << (7 * r);
+      else z1 |= (uint32_t)(r * kSlots + 8) << (7 * (r - 4));
+    }
+    T.ex[0] = 256;
+    T.nt[0] = a.rows;
+    T.tok[0] = t0;
+    T.sl0[0] = z0;
+    T.sl1[0] = z1;
+    T.units = 1 + (int)__popcll(firsts);
   }
-  release_stores();
-  if (lane == 0) st_coh_i(a.w.flags + LF_PLAN, (int)tag);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Share k of SHARES of the code table (a power-of-two size) into LDS by one wave, in one batch:
+// every load is issued (unconditionally, index clamped: a load under a branch is waited for
+// before the next) before the first store.
+template <int BYTES, int SHARES>
+__device__ __forceinline__ void copy_table_share(uint8_t* lds, const void* table, int k) {
+  const u32x4* src = reinterpret_cast<const u32x4*>(table);
+  u32x4* dst = reinterpret_cast<u32x4*>(lds);
+  constexpr int n = BYTES / 16;
+  constexpr int per = ((n + SHARES - 1) / SHARES + 63) & ~63;
+  constexpr int kLoads = per / 64;
+  const int lane = lane_id();
+  const int lo = k * per, hi = min(n, lo + per);
+  // every block walks the table from its own 1 KB offset: all CUs reading the same lines at the
+  // same time would queue on the same L2 channels
+  const int rot = ((int)blockIdx.x * 97 * 64) & (n - 1);
+  u32x4 v[kLoads];
+#pragma unroll
+  for (int j = 0; j < kLoads; j++) v[j] = src[(min(lo + 64 * j + lane, hi - 1) + rot) & (n - 1)];
+#pragma unroll
+  for (int j = 0; j < kLoads; j++) {
+    const int i = lo + 64 * j + lane;
+    if (i < hi) dst[(i + rot) & (n - 1)] = v[j];
+  }
 }
 
 // ---------------------------------------------------------------- the kernel
@@ -773,6 +936,7 @@ __global__ __launch_bounds__(kLW * 64) void k4_layer_kernel(LayerArgs a) {
   constexpr bool kDPre = NT == 1;  // down inputs fetched ahead (registers allow it for one token)
   __shared__ __attribute__((aligned(16))) uint8_t tab[LTable<NT>::kBytes];
   __shared__ __attribute__((aligned(16))) _Float16 xa[kLW * xa_halves(NT)];
+  __shared__ __attribute__((aligned(16))) float pst_all[NT == 1 ? kLW * 128 : 1];  // one token: partial rows
   __shared__ int32_t exit_last;
 
   const int wv = wave_id_uniform();
@@ -788,116 +952,173 @@ __global__ __launch_bounds__(kLW * 64) void k4_layer_kernel(LayerArgs a) {
   L.R = a.route ? 256 * L.S : 0;
   L.route = a.route;
   const int pre = pre_items(L);
-  const uint32_t epoch = (uint32_t)__builtin_amdgcn_readfirstlane(ld_coh_i(a.w.flags + LF_EPOCH));
-  const uint32_t tag = epoch + 1u;
+  // the launch's epoch (read once per block below) and its tag
+  uint32_t epoch = 0, tag = 0;
 
-  auto claim = [&]() {
+  // A wave's first item is its index among the waves serving its sub-list (no atomic: thousands
+  // of simultaneous claims on eight counters would serialise the start); the counter hands out the
+  // items after those.
+  const int xcd_waves = (((int)gridDim.x - xcd + kXcds - 1) / kXcds) * kLW;
+  const int first_sub = ((int)blockIdx.x / kXcds) * kLW + wv;
+  // A claim in two steps: the atomic is issued, its result is read later.  Reading it waits for
+  // every earlier memory operation of the wave (loads and stores share one counter), so a claim
+  // issued during an item is read only once the data it was issued behind is needed anyway.
+  auto claim_issue = [&]() {
     int v = 0;
     if (lane_id() == 0) v = __hip_atomic_fetch_add(qc, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    return __builtin_amdgcn_readfirstlane(v);
+    return v;
   };
+  auto claim_take = [&](int v) { return xcd_waves + __builtin_amdgcn_readfirstlane(v); };
+  auto claim = [&]() { return claim_take(claim_issue()); };
 
+  __shared__ PlanLds plan_t;
+  __shared__ int32_t route_state;  // routing launches: 0 not started, 1 being computed, 2 ready
   bool have_plan = false;
-  PlanRegs pr{};
+  int units = 1;
   UnitInfo shared_ui{min(256, a.experts - 1), a.rows, 0, 0, 0, a.rows};
   if (a.route) {
     // unit 0 (the shared expert) is known before routing: rows 0.., slots 9 r + 8
     uint32_t tok = 0, s0 = 0, s1 = 0;
     for (int t = 0; t < a.rows; t++) {
       tok |= (uint32_t)t << (3 * t);
-      if (t < 4) s0 |= (uint32_t)(9 * t + 8) << (7 * t);
-      else s1 |= (uint32_t)(9 * t + 8) << (7 * (t - 4));
+      if (t < 4) s0 |= (uint32_t)(kSlots * t + 8) << (7 * t);
+      else s1 |= (uint32_t)(kSlots * t + 8) << (7 * (t - 4));
     }
     shared_ui.tok = tok;
     shared_ui.sl0 = s0;
     shared_ui.sl1 = s1;
   } else {
-    pr = load_plan(a.w.plan);
+    units = load_plan(a.w.plan, plan_t);
     have_plan = true;
   }
-  auto unit_of = [&](int u) { return (u == 0 && a.route) ? shared_ui : unit_info(pr, u, a.experts, a.rows); };
+  const float* score = a.route ? plan_t.score : a.scores;
+  auto unit_of = [&](int u) { return (u == 0 && a.route) ? shared_ui : unit_info(plan_t, u, a.experts, a.rows); };
   // the item at sub-list position `sub`, if it is known without waiting (kind NONE otherwise)
   auto resolve = [&](int sub, Item& it) {
     const int j = sub * kXcds + xcd;
     it = Item{IT_NONE, 0, 0, 0, 0};
     if (j < pre) it = item_at(L, j, 1);
-    else if (have_plan && j < list_len(L, pr.units)) it = item_at(L, j, pr.units);
+    else if (have_plan && j < list_len(L, units)) it = item_at(L, j, units);
   };
 
-  // A run of part items: pc / in hold the first item's quad 0 and input block on entry; each item
-  // streams its quad 1 while quad 0 is decoded and the next part's quad 0 and input block while
-  // quad 1 is decoded.  Returns with `sub` at the first item that is not a part (or not yet known).
+  // A run of part items: pc / in hold the first item's quad 0 and input block on entry.  Each item
+  // is staged, streams its quad 1 while quad 0 is decoded and the next part's quad 0 and input
+  // block while quad 1 is decoded, then stores its partials.  A wave never waits while it holds
+  // partials it has not stored (the only wait of the loop, a down part's staging, comes after the
+  // previous part's stores), so the lowest unfinished item always makes progress.
+  // Returns with `sub` at the first item that is not a part (or not yet known).
   u32x4 pc[4];
   InBlock<NT, kDPre> in;
   auto run_parts = [&](Item it, int& sub) {
     for (;;) {
       const UnitInfo ui = unit_of(it.u);
-      u32x4 pn[4];
-      load_quad(pn, quad_ptr(a, ui, it, 1));
       __builtin_amdgcn_s_setprio(2);
       stage_in<NT, kDPre>(a, ui, it, in, tag, xw);
       __builtin_amdgcn_s_setprio(0);
+      u32x4 pn[4];
+      load_quad(pn, quad_ptr(a, ui, it, 1));
       // the next item is claimed once this one can no longer wait (a claimed item is only started
       // by its claimer); the claim's round trip is hidden by quad 0
-      const int nsub = claim();
+      const int claimed = claim_issue();
       f32x4 acc[4][2];
 #pragma unroll
       for (int s4 = 0; s4 < 4; s4++)
 #pragma unroll
         for (int hh = 0; hh < 2; hh++) acc[s4][hh] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
       decode_quad<NT>(pc, 0, ui.ntok, tab, xw, acc);
+      const int nsub = claim_take(claimed);
       Item nit;
       resolve(nsub, nit);
-      if (is_part(nit)) {
-        const UnitInfo nui = unit_of(nit.u);
-        load_quad(pc, quad_ptr(a, nui, nit, 0));
-        fetch_in<NT, kDPre>(a, nui, nit, in);
-      }
+      // the next part's quad 0 and input block -- this part's again when the next item is not a
+      // part (every load of the loop is unconditional: a load under a branch makes the compiler
+      // wait for all outstanding memory operations before the next use)
+      const bool more = is_part(nit);
+      const Item pit = more ? nit : it;
+      const UnitInfo pui = unit_of(pit.u);
+      load_quad(pc, quad_ptr(a, pui, pit, 0));
+      fetch_in<NT, kDPre>(a, pui, pit, in);
       decode_quad<NT>(pn, 1, ui.ntok, tab, xw, acc);
-      store_partials<NT>(a, ui, it, acc, tag, L);
+      store_partials<NT>(a, ui, it, acc, tag, L, pst_all + (NT == 1 ? wv * 128 : 0));
       sub = nsub;
-      if (!is_part(nit)) return;
+      if (!more) return;
       it = nit;
     }
   };
 
-  int sub = claim();
+  // The code table: every wave copies its share into LDS first, before any other memory traffic
+  // of the launch (which would slow the copy several-fold); the block then meets once.
+  __shared__ uint32_t epoch_lds;
+  if (threadIdx.x == 0) {
+    epoch_lds = (uint32_t)ld_coh_i(a.w.flags + LF_EPOCH);
+    route_state = 0;
+  }
+  if (LTable<NT>::kF16)
+    copy_table_share<131072, kLW>(tab, a.tab16, wv);
+  else
+    copy_table_share<65536, kLW>(tab, a.tab8, wv);
+  __syncthreads();
+  epoch = (uint32_t)__builtin_amdgcn_readfirstlane((int)epoch_lds);
+  tag = epoch + 1u;
+  int sub = first_sub;
   Item first;
   resolve(sub, first);
-  // router items need no code table: they run before the copy
+  // Router items first.  The block's first wave done with one routes at once, before it claims
+  // anything: a wave that routes holds no claimed item and the block's other waves keep claiming,
+  // so the router items it waits for are always taken.
+  bool route_now = false;
   while (first.kind == IT_ROUTER) {
     __builtin_amdgcn_s_setprio(3);
     router_item(a, first.a, L.S, tag);
     __builtin_amdgcn_s_setprio(0);
+    if (!have_plan) {
+      int old = 0;
+      if (lane_id() == 0) {
+        int expected = 0;
+        __hip_atomic_compare_exchange_strong(&route_state, &expected, 1, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_WORKGROUP);
+        old = expected;
+      }
+      route_now = __builtin_amdgcn_readfirstlane(old) == 0;
+      if (route_now) break;
+    }
     sub = claim();
     resolve(sub, first);
   }
-  // the first part's operands are in flight while the code table is copied
-  if (is_part(first)) {
-    const UnitInfo ui = unit_of(first.u);
-    load_quad(pc, quad_ptr(a, ui, first, 0));
-    fetch_in<NT, kDPre>(a, ui, first, in);
-  }
-  if (LTable<NT>::kF16)
-    copy_table_lds<131072, kLW * 64>(tab, a.tab16);
-  else
-    copy_table_lds<65536, kLW * 64>(tab, a.tab8);
-  __syncthreads();
-  if (is_part(first)) run_parts(first, sub);
 
   for (;;) {
-    const int j = sub * kXcds + xcd;
-    if (!have_plan && j >= pre) {
+    if (route_now || (!have_plan && sub * kXcds + xcd >= pre)) {
+      // the block's plan table: the first wave to ask routes (route_now: it has already won the
+      // right after its router items), a later one waits for it
       __builtin_amdgcn_s_setprio(3);
-      int spins = 0;
-      while ((uint32_t)ld_coh_i(a.w.flags + LF_PLAN) != tag && keep_waiting(a, spins)) {
+      int old = 0;
+      if (!route_now && lane_id() == 0) {
+        int expected = 0;
+        __hip_atomic_compare_exchange_strong(&route_state, &expected, 1, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_WORKGROUP);
+        old = expected;
       }
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-      pr = load_plan(a.w.plan);
+      old = __builtin_amdgcn_readfirstlane(old);
+      if (old == 0) {
+        route_block(a, L.S, tag, plan_t);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        if (lane_id() == 0) __hip_atomic_store(&route_state, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      } else {
+        while (__hip_atomic_load(&route_state, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 2)
+          __builtin_amdgcn_s_sleep(1);
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+      }
+      units = min(max(__builtin_amdgcn_readfirstlane(plan_t.units), 1), kMaxUnits);
       have_plan = true;
       __builtin_amdgcn_s_setprio(0);
+      if (route_now) {
+        // the router item at `sub` is done: on to the next
+        route_now = false;
+        sub = claim();
+        continue;
+      }
     }
-    const int U = have_plan ? pr.units : 1;
+    const int j = sub * kXcds + xcd;
+    const int U = have_plan ? units : 1;
     if (have_plan && j >= list_len(L, U)) break;
     const Item it = item_at(L, j, U);
     if (it.kind == IT_NONE) break;
@@ -905,6 +1126,10 @@ __global__ __launch_bounds__(kLW * 64) void k4_layer_kernel(LayerArgs a) {
       const UnitInfo ui = unit_of(it.u);
       load_quad(pc, quad_ptr(a, ui, it, 0));
       fetch_in<NT, kDPre>(a, ui, it, in);
+      // the run's first part waits for its operands here, so nothing is pending on entry: without
+      // this the compiler merges the entry (input block just requested) into the loop's state and
+      // waits for every outstanding operation at each part's staging
+      __builtin_amdgcn_s_waitcnt(0);
       run_parts(it, sub);
       continue;
     }
@@ -913,12 +1138,10 @@ __global__ __launch_bounds__(kLW * 64) void k4_layer_kernel(LayerArgs a) {
     __builtin_amdgcn_s_setprio(3);
     if (it.kind == IT_ROUTER) {
       router_item(a, it.a, L.S, tag);
-    } else if (it.kind == IT_ROUTE) {
-      route_and_plan(a, L.S, tag);
     } else if (it.kind == IT_GF) {
       gate_finish(a, unit_of(it.u), it.a, tag, L);
     } else if (it.kind == IT_DF) {
-      down_finish(a, unit_of(it.u), it.a, it.u == U - 1, tag, L);
+      down_finish(a, unit_of(it.u), it.a, it.u == U - 1, tag, L, score);
     }
     __builtin_amdgcn_s_setprio(0);
     sub = claim();

@@ -51,7 +51,8 @@ __device__ __forceinline__ RouteInput route_load(const float* __restrict__ logit
 
 template <bool COH_OUT = false>
 __device__ __forceinline__ void route_select(const RouteInput& in, int row, uint32_t* __restrict__ ids,
-                                             float* __restrict__ scores, int32_t* sid, bool store_global);
+                                             float* __restrict__ scores, int32_t* sid, bool store_global,
+                                             float* score_lds = nullptr);
 
 template <bool COHERENT = false>
 __device__ __forceinline__ void route_row(const float* __restrict__ logits, const float* __restrict__ bias, int row,
@@ -62,30 +63,57 @@ __device__ __forceinline__ void route_row(const float* __restrict__ logits, cons
 
 // Selection of one row from its loaded logits: a radix select on 40-bit keys (choice key << 8 |
 // 255 - id).  Keys are unique, so "top 8 by descending choice, ties to the lower id" is exactly
-// "the 8 largest keys".  Each of the 40 bisection steps counts candidates with wave ballots (no
+// "the 8 largest keys".  Each bisection step counts candidates with wave-wide compare masks (no
 // LDS round trip); the 8 winners are then ranked against each other and the scores summed in
 // rank order.  COH_OUT: ids and scores are stored write-through (read by other CUs in the same
 // launch).
 template <bool COH_OUT>
 __device__ __forceinline__ void route_select(const RouteInput& in, int row, uint32_t* __restrict__ ids,
-                                             float* __restrict__ scores, int32_t* sid, bool store_global) {
+                                             float* __restrict__ scores, int32_t* sid, bool store_global,
+                                             float* score_lds) {
   const int lane = lane_id();
   float orig[4];
+  uint32_t fk[4];
   uint64_t key[4];
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const int e = lane + 64 * i;
     orig[i] = router_sigmoid(in.logit[i]);
     const float choice = orig[i] + in.bias[i];
-    key[i] = ((uint64_t)float_key(choice) << 8) | (uint64_t)(255 - e);
+    fk[i] = float_key(choice);
+    key[i] = ((uint64_t)fk[i] << 8) | (uint64_t)(255 - e);
   }
-  uint64_t thr = 0;
-  for (int b = 39; b >= 0; b--) {
-    const uint64_t cand = thr | (1ull << b);
+  // Bisection on the choice keys alone first (32-bit compares), each compare into its own mask so
+  // the four compares of a step overlap: th = the 8th largest choice key.  Only when more than 8
+  // keys reach th (a tie at the boundary) do the 8 id bits continue the bisection on full keys.
+  uint32_t th = 0;
+  for (int b = 31; b >= 0; b--) {
+    const uint32_t cand = th | (1u << b);
+    uint64_t m[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) m[i] = __builtin_amdgcn_uicmp(fk[i], cand, 35 /* unsigned >= */);
     int cnt = 0;
 #pragma unroll
-    for (int i = 0; i < 4; i++) cnt += __popcll(__ballot(key[i] >= cand));
-    if (cnt >= 8) thr = cand;
+    for (int i = 0; i < 4; i++) cnt += __popcll(m[i]);
+    if (cnt >= 8) th = cand;
+  }
+  uint64_t thr = (uint64_t)th << 8;
+  {
+    int at = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) at += __popcll(__builtin_amdgcn_uicmp(fk[i], th, 35));
+    if (at > 8) {
+      for (int b = 7; b >= 0; b--) {
+        const uint64_t cand = thr | (1ull << b);
+        uint64_t m[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) m[i] = __builtin_amdgcn_uicmpl(key[i], cand, 35);
+        int cnt = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) cnt += __popcll(m[i]);
+        if (cnt >= 8) thr = cand;
+      }
+    }
   }
   // exactly 8 keys are >= thr.  The winners are packed into 8 LDS entries (position = winners in
   // earlier slots and lower lanes); lane l < 8 then ranks entry l against the other seven
@@ -125,20 +153,23 @@ __device__ __forceinline__ void route_select(const RouteInput& in, int row, uint
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  if (store_global && lane < 9) {
+  if ((store_global || score_lds != nullptr) && lane < 9) {
     // every lane forms the same rank-ordered sum; lane i < 8 writes winner i, lane 8 the shared id
     float total = 1e-20f;
 #pragma unroll
     for (int i = 0; i < 8; i++) total += sel[i];
+    const float score = lane < 8 ? sel[lane] / total * 2.5f : 0.0f;
     const uint32_t id = lane < 8 ? (uint32_t)idl[lane] : 256u;
-    if (COH_OUT) {
-      if (lane < 8)
-        __hip_atomic_store(scores + (int64_t)row * 8 + lane, sel[lane] / total * 2.5f, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_SYSTEM);
-      __hip_atomic_store(ids + (int64_t)row * 9 + lane, id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    } else {
-      if (lane < 8) scores[(int64_t)row * 8 + lane] = sel[lane] / total * 2.5f;
-      ids[(int64_t)row * 9 + lane] = id;
+    if (score_lds != nullptr && lane < 8) score_lds[row * 8 + lane] = score;
+    if (store_global) {
+      if (COH_OUT) {
+        if (lane < 8)
+          __hip_atomic_store(scores + (int64_t)row * 8 + lane, score, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(ids + (int64_t)row * 9 + lane, id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      } else {
+        if (lane < 8) scores[(int64_t)row * 8 + lane] = score;
+        ids[(int64_t)row * 9 + lane] = id;
+      }
     }
   }
   if (sid != nullptr && lane < 9) sid[row * 9 + lane] = lane < 8 ? idl[lane] : 256;
