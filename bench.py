@@ -1,17 +1,20 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X MoE expert path: one GLM-5.3-style K4 trellis MoE layer, batch-1 decode.
 
-    python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu] [--config 0..4]
+    python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu] [--no-prefill] [--config 0..4]
 
 Default (--config 0): one step = one token through the whole layer (router GEMV, bias-corrected top-8, eight routed
 experts plus the shared expert as K4-trellis decode GEMVs with SwiGLU, weighted combine and
-residual).  Inputs and weights are resident in HBM before timing starts.  Weights of several
-independently seeded layers are rotated (and tokens vary) so consecutive steps stream
-different expert bytes instead of re-reading the 256 MB last-level cache.
+residual) -- one launch of the fused decode kernel.  Inputs and weights are resident in HBM before
+timing starts.  Several independently seeded layers (expert and router weights) are rotated, and
+tokens vary, so consecutive steps stream different bytes instead of re-reading the 256 MB
+last-level cache.
 
-Prints ONE JSON line.  `value` is tokens/s; `us_per_token`, achieved algorithmic HBM GB/s and
-the roofline of the dominant kernel (the fused gate/up decode GEMV, timed with HIP events on
-its own stream) are reported beside it, with the CPU oracle timed on this host's cores.
+Prints ONE JSON line.  `value` is decode tokens/s; `us_per_token`, achieved algorithmic HBM GB/s
+and the roofline of the fused layer kernel (timed with HIP events on its launch stream) are
+reported beside it.  The same line carries the metric's prefill half (`prefill`: a 512-token
+chunk through the joined-MXFP4 layer, tokens/s) and the CPU baseline (the C restatement with fp32
+accumulation, built with -march=native for this host, timed on all its cores).
 
 The other workloads of the same path are measured with --config N (same JSON shape, whole-step
 timing with HIP events):
@@ -48,6 +51,7 @@ def parse():
     p.add_argument("--tokens", type=int, default=16, help="distinct tokens rotated per step")
     p.add_argument("--seed", type=int, default=2026)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--no-prefill", action="store_true", help="skip the prefill measurement of the default line")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--config", type=int, default=0, choices=range(5),
                    help="workload: 0 K4 b=1 (default), 1 MXFP4 b=1, 2 K4 8-token verify, 3 MXFP4 512-token "
@@ -74,12 +78,20 @@ def traffic_from_profiles():
 
 
 def cpu_baseline(layer, w, bias, xs, rs, seconds):
-    """The CPU oracle (C restatement of the reference operator chain, OpenMP) on this host."""
+    """The CPU restatement of the reference operator chain, timed on this host: the oracle's C source
+    built here with fp32 accumulation and -march=native (OpenMP over all cores); the float64 oracle
+    if that build is not possible."""
+    import tempfile
+
     import numpy as np
     import torch
-    from oracle import lib as oracle_lib
+    from oracle import lib as oracle_lib, native_f32
 
-    orc = oracle_lib()
+    orc = native_f32(Path(tempfile.gettempdir()) / "moe_cpu_baseline")
+    kind = "C restatement built here: -O3 -march=native -fopenmp, fp32 accumulation"
+    if orc is None:
+        orc = oracle_lib()
+        kind = "C oracle (prebuilt -O3 -march=x86-64-v3 -fopenmp), float64 accumulation"
     host = {p: t.cpu().numpy() for p, t in layer["packed"].items()}
     sc = {p: tuple(v.contiguous().view(torch.int16).cpu().numpy().view(np.uint16) for v in pair)
           for p, pair in layer["scales"].items()}
@@ -98,7 +110,7 @@ def cpu_baseline(layer, w, bias, xs, rs, seconds):
             break
     return {"value": done / el, "unit": "tokens/s", "cores": orc.num_threads(), "kind": "port",
             "sample": f"{done} tokens of the same batch-1 K4 layer (router GEMV + route + 9-expert MLP + combine), "
-                      f"{el:.1f} s, C oracle -O3 -fopenmp, float64 accumulation"}
+                      f"{el:.1f} s; {kind}"}
 
 
 def main():
@@ -124,7 +136,8 @@ def main():
         L = synth.k4_layer(dev, args.seed + 17 * i)
         raw.append(L)
         layers.append(ExpertLayer(L["packed"], L["scales"], H, M))
-    w, bias = synth.router(dev, args.seed)
+    # each rotated layer has its own router weights (6.3 MB per step, streamed like the experts)
+    routers = [synth.router(dev, args.seed + 17 * i) for i in range(args.layers)]
     xs, rs = [], []
     for t in range(args.tokens):
         x, r = synth.activations(dev, args.seed + 1000 + t, 1)
@@ -133,7 +146,8 @@ def main():
     torch.cuda.synchronize()
 
     # one prepared C call per (layer, token) pair: no per-step tensor work on the host
-    calls = [[layer.prepare_decode(xs[t], rs[t], w, bias) for t in range(len(xs))] for layer in layers]
+    calls = [[layer.prepare_decode(xs[t], rs[t], *routers[k]) for t in range(len(xs))]
+             for k, layer in enumerate(layers)]
 
     def step(i):
         return calls[i % len(layers)][i % len(xs)].run()
@@ -202,8 +216,8 @@ def main():
         "hbm_frac": round(hbm / HBM_PEAK_GBPS, 4),
         "bytes_per_token": BYTES_TOKEN,
         "kernels_us": {"k4_layer_kernel": round(layer_us, 2)},
-        "roofline": {"kernel": "k4_layer_kernel<1> (router, top-8, 9-unit gate/up and down decode GEMVs and "
-                               "combine in one cooperative launch)",
+        "roofline": {"kernel": "k4_layer_kernel<1> (router, top-8, shared and routed gate/up and down decode "
+                               "GEMVs, finishes and combine in one persistent launch)",
                      "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "algorithmic_bytes": BYTES_TOKEN},
@@ -216,8 +230,15 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         result["calibration_copy_bytes"] = 1 << 30
+    if not args.no_prefill:
+        pf = bench_prefill(args, steps=20, warmup=3)
+        result["prefill"] = {"metric": "prefill tok/s", "value": pf["value"], "unit": "tokens/s",
+                             "ms_per_chunk": pf["ms_per_step"], "workload": pf["config"]["workload"],
+                             "touched_experts": pf["config"]["touched_experts"],
+                             "hbm_GBps": pf["roofline"]["achieved"],
+                             "mfma_util_fp4_peak": pf["mfma_util_fp4_peak"], "steps": pf["steps"]}
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline(raw[0], w, bias, xs, rs, args.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline(raw[0], *routers[0], xs, rs, args.cpu_seconds)
     print(json.dumps(result), flush=True)
 
 
@@ -308,7 +329,7 @@ def bench_k4_verify(args):
                 us_per_step=round(ms * 1e3, 2))
 
 
-def bench_prefill(args):
+def bench_prefill(args, steps=None, warmup=None):
     import torch
     from mlxlr8_amd import synth
     dev = torch.device("cuda:0")
@@ -318,8 +339,9 @@ def bench_prefill(args):
     _, ids, _ = layers[0].prefill(x, res, w, bias)
     torch.cuda.synchronize()
     touched = len(set(ids.cpu().numpy().ravel().tolist()))
-    steps = max(1, min(args.steps, 40))
-    ms = _time_steps(lambda i: layers[i % 2].prefill(x, res, w, bias), steps, min(args.warmup, 5))
+    steps = steps if steps is not None else max(1, min(args.steps, 40))
+    warmup = warmup if warmup is not None else min(args.warmup, 5)
+    ms = _time_steps(lambda i: layers[i % 2].prefill(x, res, w, bias), steps, warmup)
     algo = touched * MX_EXPERT_BYTES + 256 * H * 4 + 3 * 512 * H * 2
     out = _line(args, 512e3 / ms, "tokens/s", ms, "f32",
                 "512-token prefill chunk through the joined-MXFP4 MoE layer (Zipf(1.1)-skewed routing, "

@@ -5,7 +5,9 @@ may import this package, and only as the checker (or the timed CPU baseline).  T
 product package ``mlxlr8_amd`` never imports it.
 
 ``moe_oracle.c`` (built to ``libmoe_oracle.so`` by ``oracle/Makefile``) restates the
-reference operators; ``numpy_ref.py`` holds independent numpy restatements used to
-pin the C code (closed forms, brute force, the reference's own known answers).
+reference operators.  The checks that pin it (closed forms, brute force on small cases, the
+reference's own known answers under ``tests/golden/``) live in ``tests/`` (``tests/refmath.py``
+and the ``tests/test_oracle_*.py`` files).  ``native_f32`` builds the same source with fp32
+accumulation for the host it runs on: the timed CPU baseline of ``bench.py``.
 """
-from .cbind import lib, build  # noqa: F401
+from .cbind import lib, build, native_f32  # noqa: F401

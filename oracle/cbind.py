@@ -189,3 +189,16 @@ def lib():
         build()
         _lib = _Oracle(ctypes.CDLL(str(SO)))
     return _lib
+
+
+def native_f32(out_dir):
+    """The CPU baseline build (fp32 accumulation, -march=native for this host) compiled into
+    `out_dir` and loaded; None when it cannot be built here."""
+    out = Path(out_dir)
+    out.mkdir(parents=True, exist_ok=True)
+    r = subprocess.run(["make", "-s", "-f", str(HERE / "Makefile"), "native", f"OUT={out}"], cwd=HERE,
+                       capture_output=True, text=True)
+    so = out / "libmoe_oracle_f32.so"
+    if r.returncode != 0 or not so.exists():
+        return None
+    return _Oracle(ctypes.CDLL(str(so)))

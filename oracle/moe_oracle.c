@@ -224,15 +224,22 @@ void orc_hadamard128(float* x, int64_t n) {
   }
 }
 
+/* Accumulator of the router and K4 linear dot products: double for the oracle (the parity
+   checker); the timed CPU baseline is the same code built with -DORC_ACC=float (fp32 accumulate,
+   as the reference's own kernels). */
+#ifndef ORC_ACC
+#define ORC_ACC double
+#endif
+
 /* ---------------- router (model.py:111-132, fast_router.metal:1-42) ---------------- */
 void orc_router_logits(const uint16_t* x_bf16, const float* w, int rows, int hidden, int experts, float* logits) {
 #pragma omp parallel for collapse(2) schedule(static)
   for (int r = 0; r < rows; r++)
     for (int e = 0; e < experts; e++) {
-      double acc = 0.0;
+      ORC_ACC acc = 0;
       const uint16_t* xr = x_bf16 + (int64_t)r * hidden;
       const float* we = w + (int64_t)e * hidden;
-      for (int k = 0; k < hidden; k++) acc += (double)bf16_to_f32(xr[k]) * (double)we[k];
+      for (int k = 0; k < hidden; k++) acc += (ORC_ACC)bf16_to_f32(xr[k]) * (ORC_ACC)we[k];
       logits[(int64_t)r * experts + e] = (float)acc;
     }
 }
@@ -272,21 +279,21 @@ float orc_swiglu_bf16(float gate, float up) {
 }
 
 /* ---------------- K4 trellis linear (trellis.py:172-196) ----------------
-   y[out] = out_scale (*) H( H(x (*) in_scale) @ inner_e ), float32 side vectors, float64 dot.
+   y[out] = out_scale (*) H( H(x (*) in_scale) @ inner_e ), float32 side vectors, ORC_ACC dot.
    Returns the pre-cast float value; the caller applies the bf16 cast. */
 static void k4_linear_one(const float* x, const uint8_t* packed, int k, int in_f, int out_f, int side,
                           int64_t e, const uint16_t* in_scale, const uint16_t* out_scale, float* y, float* tmp_in) {
   for (int i = 0; i < in_f; i++) tmp_in[i] = x[i] * f16_to_f32(in_scale[(int64_t)e * in_f + i]);
   orc_hadamard128(tmp_in, in_f);
   uint32_t it = (uint32_t)in_f / 16u, ot = (uint32_t)out_f / 16u;
-  double* acc = (double*)calloc((size_t)out_f, sizeof(double));
+  ORC_ACC* acc = (ORC_ACC*)calloc((size_t)out_f, sizeof(ORC_ACC));
   for (uint32_t tk = 0; tk < it; tk++)
     for (uint32_t tn = 0; tn < ot; tn++) {
       uint64_t t = tile_index((uint64_t)e, tk, tn, it, ot, side);
       const uint32_t* w = (const uint32_t*)(packed + t * 32u * (uint64_t)k);
       for (uint32_t i = 0; i < 256u; i++) {
         uint32_t r, c; tile_position(i, &r, &c);
-        acc[tn * 16u + c] += (double)tmp_in[tk * 16u + r] * (double)g_codebook_f32[tile_codeword(w, k, i)];
+        acc[tn * 16u + c] += (ORC_ACC)tmp_in[tk * 16u + r] * (ORC_ACC)g_codebook_f32[tile_codeword(w, k, i)];
       }
     }
   for (int o = 0; o < out_f; o++) y[o] = (float)acc[o];

@@ -199,6 +199,54 @@ def test_moe_decode_block_verify_batch(cuda, orc, glm_layer):
     _check_decode_block(orc, glm_layer, 8, True, 21)
 
 
+@pytest.mark.parametrize("rows", [3, 8])
+def test_batch_rows_equal_single_rows(cuda, glm_layer, rows):
+    """A token's output does not depend on the batch it is decoded in: every row of a routed
+    rows-token decode block equals, bit for bit, the same token decoded alone (ids, scores and the
+    combined output).  The reference requires this of its multi-row reuse
+    (tests/test_fast_decode.py:218-243); here every output is summed over fixed 128-row parts in
+    part order, whatever the batch's units."""
+    from mlxlr8_amd import synth
+    say(f"case: batch of {rows} rows vs single rows, bit for bit")
+    experts, layer, host, sc, w, bias = glm_layer
+    x, residual = synth.activations(w.device, 31 + rows, rows, correlated=True)
+    out, ids, scores = experts.decode_block_routes(x, residual, w, bias)
+    for r in range(rows):
+        o1, i1, s1 = experts.decode_block_routes(x[r:r + 1].contiguous(), residual[r:r + 1].contiguous(), w, bias)
+        assert torch.equal(ids[r], i1[0]), f"row {r}: ids differ"
+        assert torch.equal(scores[r].view(torch.int32), s1[0].view(torch.int32)), f"row {r}: scores differ"
+        assert torch.equal(out[r].view(torch.int16), o1[0].view(torch.int16)), f"row {r}: output differs"
+
+
+@pytest.mark.parametrize("rows", [2, 3, 4, 8])
+@pytest.mark.parametrize("pattern", ["shared", "all", "changing", "duplicates"])
+def test_values_batch_equals_single_rows(cuda, glm_layer, rows, pattern):
+    """The reference's id patterns for multi-row reuse (tests/test_fast_decode.py:218-243): rows
+    sharing only the shared expert, rows using the same nine experts in rotated order, overlapping
+    windows, and ids repeated inside a row.  Each row's nine slot values from the batch equal the
+    row's values computed alone, bit for bit."""
+    say(f"case: values rows={rows} pattern={pattern} vs single rows")
+    experts, layer, host, sc, w, bias = glm_layer
+    if pattern == "shared":
+        routed = np.arange(rows * 8).reshape(rows, 8)
+        ids = np.concatenate([routed, np.full((rows, 1), 256)], axis=-1)
+    elif pattern == "all":
+        ids = np.stack([np.roll(np.arange(9), r) for r in range(rows)])
+    elif pattern == "changing":
+        routed = np.stack([np.arange(r * 4, r * 4 + 8) for r in range(rows)])
+        ids = np.concatenate([routed, np.full((rows, 1), 256)], axis=-1)
+    else:
+        ids = np.tile([0, 0, 1, 1, 2, 2, 0, 1, 2], (rows, 1))
+    ids = torch.tensor(ids, dtype=torch.int32, device=cuda)
+    g = torch.Generator(device=cuda)
+    g.manual_seed(431 + rows)
+    x = torch.randn((rows, 6144), generator=g, device=cuda).to(torch.bfloat16)
+    values = experts(x, ids)
+    for r in range(rows):
+        v1 = experts(x[r:r + 1].contiguous(), ids[r:r + 1].contiguous())
+        assert torch.equal(values[r].view(torch.int16), v1[0].view(torch.int16)), f"row {r} differs"
+
+
 def test_mlp_values_glm(cuda, orc, glm_layer):
     from mlxlr8_amd.fast_decode import fast_expert_mlp
     say("case: GLM values rows=2")
