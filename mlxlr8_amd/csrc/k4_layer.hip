@@ -561,10 +561,11 @@ __device__ __forceinline__ void store_partials(const LayerArgs& a, const UnitInf
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const f32x2 v = *reinterpret_cast<const f32x2*>(pst + 2 * lane);
-    uint64_t* pw = part_ptr(a, ui.slot(0), index) + 2 * lane;
-    st_tag(pw, v.x, tag);
-    st_tag(pw + 1, v.y, tag);
+    // lane l stores columns l and 64 + l: each store instruction writes 512 contiguous bytes (whole
+    // lines; interleaved pairs would write every line in two halves)
+    uint64_t* pw = part_ptr(a, ui.slot(0), index) + lane;
+    st_tag(pw, pst[lane], tag);
+    st_tag(pw + 64, pst[64 + lane], tag);
     return;
   }
 #pragma unroll
