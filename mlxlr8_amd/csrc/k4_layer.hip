@@ -435,11 +435,26 @@ __device__ __forceinline__ void fetch_in(const LayerArgs& a, const UnitInfo& ui,
     in.r[NT] = *reinterpret_cast<const uint32_t*>(a.in_scale[it.b] + (int64_t)ui.e * a.h + off);
   }
 }
+// Largest value over the wave's lanes (valid in every lane after the read of lane 63).
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp_f32<0xB1>(v));
+  v = fmaxf(v, dpp_f32<0x4E>(v));
+  v = fmaxf(v, dpp_f32<0x124>(v));
+  v = fmaxf(v, dpp_f32<0x128>(v));
+  v = fmaxf(v, dpp_f32<0x142, 0xA>(v));
+  v = fmaxf(v, dpp_f32<0x143, 0xC>(v));
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
 // A fragments of the part's 128 input rows (hi and lo fp16 rows per token) into the wave's LDS
 // slice.  Down inputs are polled until they carry the launch's tag.
+// A block whose values reach 2^15 (beyond what the fp16 hi row holds; the reference computes in
+// fp32) is staged scaled by 2^-k so that its largest value stays below 2^15, and the part's
+// partial sums are multiplied back by scale[t] = 2^k (powers of two: exact).  Other blocks keep
+// scale 1 and bit-identical results.
 template <int NT, bool DPRE>
 __device__ __forceinline__ void stage_in(const LayerArgs& a, const UnitInfo& ui, const Item& it,
-                                         const InBlock<NT, DPRE>& in, uint32_t tag, _Float16* __restrict__ xw) {
+                                         const InBlock<NT, DPRE>& in, uint32_t tag, _Float16* __restrict__ xw,
+                                         float (&scale)[NT]) {
   const int lane = lane_id();
   float v0[NT], v1[NT];
   uint32_t w[4] = {0u, 0u, 0u, 0u};
@@ -475,6 +490,22 @@ __device__ __forceinline__ void stage_in(const LayerArgs& a, const UnitInfo& ui,
           v0[t] = hv.x;
           v1[t] = hv.y;
         }
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < NT; t++) {
+    scale[t] = 1.0f;
+    if (t < ui.ntok) {
+      const float big = fmaxf(fabsf(v0[t]), fabsf(v1[t]));
+      if (__any(big >= 32768.0f)) {
+        const float mx = wave_max(big);
+        // floor(log2(mx)) from the exponent field (>= 15 here; inf and NaN give 128)
+        const int e = (int)((__float_as_uint(mx) >> 23) & 0xFFu) - 127;
+        const int k = min(e - 14, 120);
+        v0[t] = ldexpf(v0[t], -k);
+        v1[t] = ldexpf(v1[t], -k);
+        scale[t] = ldexpf(1.0f, k);
       }
     }
   }
@@ -546,7 +577,7 @@ __device__ __forceinline__ void decode_quad(const u32x4 (&pc)[4], int qb, int nt
 template <int NT>
 __device__ __forceinline__ void store_partials(const LayerArgs& a, const UnitInfo& ui, const Item& it,
                                                const f32x4 (&acc)[4][2], uint32_t tag, const Items& L,
-                                               float* __restrict__ pst) {
+                                               float* __restrict__ pst, const float (&scale)[NT]) {
   const int lane = lane_id();
   const int g = lane >> 4, nn = lane & 15;
   const int index = it.kind == IT_GU ? (it.b * L.MB + it.a) * L.HB + it.c : 2 * L.MB * L.HB + it.a * L.MB + it.c;
@@ -556,7 +587,8 @@ __device__ __forceinline__ void store_partials(const LayerArgs& a, const UnitInf
       for (int s4 = 0; s4 < 4; s4++)
 #pragma unroll
         for (int hh = 0; hh < 2; hh++)
-          pst[16 * (2 * s4 + (nn >> 3)) + (nn & 7) + 8 * hh] = fmaf(acc[s4][hh][1], 1.0f / 2048.0f, acc[s4][hh][0]);
+          pst[16 * (2 * s4 + (nn >> 3)) + (nn & 7) + 8 * hh] =
+              fmaf(acc[s4][hh][1], 1.0f / 2048.0f, acc[s4][hh][0]) * scale[0];
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -578,7 +610,7 @@ __device__ __forceinline__ void store_partials(const LayerArgs& a, const UnitInf
 #pragma unroll
         for (int hh = 0; hh < 2; hh++) {
           const int col = 16 * (2 * s4 + (nn >> 3)) + (nn & 7) + 8 * hh;
-          st_tag(pw + col, fmaf(acc[s4][hh][r0 + 1], 1.0f / 2048.0f, acc[s4][hh][r0]), tag);
+          st_tag(pw + col, fmaf(acc[s4][hh][r0 + 1], 1.0f / 2048.0f, acc[s4][hh][r0]) * scale[t], tag);
         }
     }
   }
@@ -1014,7 +1046,8 @@ __global__ __launch_bounds__(kLW * 64) void k4_layer_kernel(LayerArgs a) {
     for (;;) {
       const UnitInfo ui = unit_of(it.u);
       __builtin_amdgcn_s_setprio(2);
-      stage_in<NT, kDPre>(a, ui, it, in, tag, xw);
+      float scale[NT];
+      stage_in<NT, kDPre>(a, ui, it, in, tag, xw, scale);
       __builtin_amdgcn_s_setprio(0);
       u32x4 pn[4];
       load_quad(pn, quad_ptr(a, ui, it, 1));
@@ -1039,7 +1072,7 @@ __global__ __launch_bounds__(kLW * 64) void k4_layer_kernel(LayerArgs a) {
       load_quad(pc, quad_ptr(a, pui, pit, 0));
       fetch_in<NT, kDPre>(a, pui, pit, in);
       decode_quad<NT>(pn, 1, ui.ntok, tab, xw, acc);
-      store_partials<NT>(a, ui, it, acc, tag, L, pst_all + (NT == 1 ? wv * 128 : 0));
+      store_partials<NT>(a, ui, it, acc, tag, L, pst_all + (NT == 1 ? wv * 128 : 0), scale);
       sub = nsub;
       if (!more) return;
       it = nit;

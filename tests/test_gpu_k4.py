@@ -268,6 +268,31 @@ def test_mlp_values_glm(cuda, orc, glm_layer):
     assert values.shape == (2, 9, 6144)
 
 
+@pytest.mark.parametrize("rows", [1, 3])
+def test_large_activations_stay_exact(cuda, orc, glm_layer, rows):
+    """Activations whose transformed blocks reach 2^15 and beyond (the fp16 hi row of the staged
+    input tops out at 65504; the reference computes in fp32): such a block is staged scaled by a
+    power of two and its partial sums are scaled back, so the slot values still match the oracle to
+    the usual bar.  An unguarded fp16 conversion would give inf."""
+    say(f"case: large activations rows={rows}")
+    experts, layer, host, sc, w, bias = glm_layer
+    ids = torch.tensor([[5, 17, 256, 40, 99, 1, 2, 3, 4], [17, 0, 256, 250, 7, 8, 9, 10, 11],
+                        [200, 201, 256, 5, 17, 30, 31, 32, 33]][:rows], dtype=torch.int32, device=cuda)
+    g = torch.Generator(device=cuda)
+    g.manual_seed(97 + rows)
+    x = (torch.randn((rows, 6144), generator=g, device=cuda) * 3.0e4).to(torch.bfloat16)
+    values = experts(x, ids)
+    assert torch.isfinite(values.float()).all()
+    res = np.zeros((rows, 6144), np.uint16)
+    _, want = orc.k4_moe(bf16_bits(x), ids.cpu().numpy(), np.zeros((rows, 8), np.float32), res, 6144, 2048,
+                         host["gate"], host["up"], host["down"],
+                         sc["gate"][0], sc["gate"][1], sc["up"][0], sc["up"][1], sc["down"][0], sc["down"][1],
+                         want_values=True)
+    err = rel_l2(bits_to_f32(bf16_bits(values)), bits_to_f32(want))
+    say(f"  rel_l2={err:.3e}")
+    assert err <= 1e-3
+
+
 def test_fp32_accumulation_known_answer(cuda):
     """Known answer of the reference (tests/golden, from its tests/test_fast_prefill.py:208-228): an
     all-zero K4 bitstream decodes to codebook[0] = 1.875 everywhere, so with unit scales and one
