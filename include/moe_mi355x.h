@@ -216,6 +216,11 @@ int moe_combine_values(const uint16_t* values, const float* scores, const uint16
  * combine with the shared expert and the residual.  Weights/side vectors as moe_mxfp4_mlp
  * (hidden a multiple of 1024, intermediate of 128); indices/scores optional outputs.
  * Workspace: moe_mxfp4_prefill_workspace_bytes(rows, hidden, intermediate, experts) (no zeroing).
+ * Exact window: the grouped GEMMs widen the e2m1 weights to fp16 with their block scale, which is
+ * exact only for e8m0 scale bytes 114..140 (the same holds for moe_mxfp4_grouped_mlp).  A caller
+ * whose weights hold any scale outside that window must use the decode entries (moe_mxfp4_moe_decode,
+ * moe_mxfp4_mlp: exact for every scale) in chunks of <= 8 rows; the Python layer checks the window
+ * once per layer and does so.
  * Replaces: exlr8/joined_mxfp4.py:90-134,148-163 (JoinedMXFP4._inner with gather_qmm sorted RHS,
  * finish) for prefill rows, with the router of exlr8/model.py:111-132. */
 int moe_mxfp4_prefill(const uint16_t* x, const uint16_t* residual, int rows, const float* router_w,

@@ -73,6 +73,12 @@ class JoinedMXFP4:
             raise ValueError("down must be [experts, h, m/2] codes with [experts, h, m/32] scales")
         self.experts = codes.shape[0]
         require_cuda(codes, sc, dcodes, dsc, unit)
+        # the grouped GEMMs (prefill-sized batches) widen the weights to fp16 with their block
+        # scale, which is exact only for e8m0 scales in GROUPED_SCALES (scaled e2m1 values stay
+        # normal fp16 numbers); a layer with any scale outside takes the decode GEMVs (exact for
+        # every scale) in chunks of decode size instead
+        lo, hi = self.GROUPED_SCALES
+        self.grouped_exact = all(int(t.min()) >= lo and int(t.max()) <= hi for t in (sc, dsc))
 
     def _args(self):
         (gc, gs), (dc, ds) = self.weights["gate_up"], self.weights["down"]
@@ -83,6 +89,7 @@ class JoinedMXFP4:
     # GEMM on the MX matrix cores (the reference switches to its sorted gather_qmm for prefill
     # sizes, exlr8/joined_mxfp4.py:98-113)
     DECODE_ROWS = 8
+    GROUPED_SCALES = (114, 140)
 
     def slots(self, x, ids):
         """values [*ids.shape, h] (exlr8/joined_mxfp4.py:143-147)."""
@@ -98,7 +105,7 @@ class JoinedMXFP4:
         xr = x.reshape(rows, h).contiguous()
         values = torch.empty((rows * slots, h), dtype=BF16, device=x.device)
         st = stream(x.device)
-        if rows > self.DECODE_ROWS:
+        if rows > self.DECODE_ROWS and self.grouped_exact:
             nbytes = lib().moe_mxfp4_grouped_mlp_workspace_bytes(rows, slots, h, self.intermediate, self.experts)
             ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
             check(lib().moe_mxfp4_grouped_mlp(ptr(xr), ptr(idx), rows, slots, *self._args(), h, self.intermediate,
@@ -183,6 +190,11 @@ class JoinedMXFP4:
         res = residual.reshape(rows, h).to(BF16).contiguous()
         w = router_weight.to(torch.float32).contiguous()
         b = bias.to(torch.float32).contiguous()
+        if not self.grouped_exact:
+            # block scales outside the grouped GEMMs' exact window: decode-sized routed blocks
+            parts = [self.decode_block(xr[r0:r0 + 8], res[r0:r0 + 8], w, b) for r0 in range(0, rows, 8)]
+            return (torch.cat([p[0] for p in parts]).reshape(residual.shape), torch.cat([p[1] for p in parts]),
+                    torch.cat([p[2] for p in parts]))
         out = torch.empty((rows, h), dtype=BF16, device=x.device)
         ids = torch.empty((rows, 9), dtype=torch.int32, device=x.device)
         scores = torch.empty((rows, 8), dtype=torch.float32, device=x.device)

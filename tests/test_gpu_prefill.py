@@ -87,6 +87,48 @@ def _check_prefill(orc, joined, host, hidden, inter, x, res, w, bias, sample):
     return out
 
 
+def test_scales_outside_grouped_window(cuda, orc):
+    """Block scales outside 114..140 (the window in which the grouped GEMMs' fp16 widening of the
+    weights is exact): the layer notices at construction and runs prefill-sized batches through the
+    decode GEMVs in chunks of 8 rows, so the result still matches the oracle and equals the 8-row
+    chunks computed separately, bit for bit."""
+    from mlxlr8_amd import synth
+    from mlxlr8_amd.joined_mxfp4 import JoinedMXFP4
+    say("case: mxfp4 scales outside the grouped window, rows=20, GLM shape with 16 experts")
+    hidden, inter = 6144, 2048   # the decode GEMVs' shape
+    L = synth.mxfp4_layer(cuda, 41, hidden=hidden, intermediate=inter, experts=16)
+    (gc, gs), (dc, ds) = L["weights"]["gate_up"], L["weights"]["down"]
+    gs, ds = gs.clone(), ds.clone()
+    gs[3, 5, 0] = 150   # 2^23: e2m1 x scale above the fp16 range
+    ds[7, 1, 2] = 100   # 2^-27: below the smallest normal fp16
+    side = L["side"]
+    joined = JoinedMXFP4({"gate_up": (gc, gs), "down": (dc, ds)}, L["unit"],
+                         {"gate": (None, side["out_gate"]), "up": (None, side["out_up"]),
+                          "down": (side["in_down"], side["out_down"])}, hidden, inter)
+    assert not joined.grouped_exact
+    rows = 20
+    g = torch.Generator(device=cuda)
+    g.manual_seed(5)
+    ids = torch.randint(0, joined.experts, (rows, 9), generator=g, device=cuda, dtype=torch.int32)
+    ids[:4, 0] = 3
+    ids[4:8, 1] = 7
+    x, _ = synth.activations(cuda, 43, rows, hidden)
+    values = joined.slots(x, ids)
+    for r0 in range(0, rows, 8):
+        part = joined.slots(x[r0:r0 + 8].contiguous(), ids[r0:r0 + 8].contiguous())
+        assert torch.equal(values[r0:r0 + 8].view(torch.int16), part.view(torch.int16))
+    host = dict(gc=gc.cpu().numpy(), gs=gs.cpu().numpy(), dc=dc.cpu().numpy(), ds=ds.cpu().numpy())
+    res = np.zeros((rows, hidden), np.uint16)
+    _, want = orc.mxfp4_moe(bf16_bits(x), ids.cpu().numpy().astype(np.uint32), np.zeros((rows, 8), np.float32), res,
+                            hidden, inter, host["gc"], host["gs"], host["dc"], host["ds"], f16_bits(L["unit"]),
+                            f16_bits(side["out_gate"]), f16_bits(side["out_up"]), f16_bits(side["in_down"]),
+                            f16_bits(side["out_down"]), want_values=True)
+    got = bits_to_f32(bf16_bits(values.reshape(rows * 9, hidden)))
+    err = rel_l2(got, bits_to_f32(want).reshape(rows * 9, hidden))
+    say(f"  rel_l2={err:.3e}")
+    assert err <= 1e-3
+
+
 def test_prefill_small_width(cuda, orc):
     from mlxlr8_amd import synth
     say("case: mxfp4 prefill rows=40 h=2048 m=512")
