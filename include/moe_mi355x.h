@@ -13,6 +13,13 @@
  *
  * Data types: bf16 and f16 are passed as uint16_t bit patterns; fp32 as float.
  * Shapes: hidden h, intermediate m, experts E (routed + shared, the shared expert last).
+ * Alignment: activation rows (x) and per-expert side-vector rows are read 8 bytes at a time and
+ * residual / output rows 4 bytes at a time; the K4 decode entries reject misaligned pointers.
+ * Expert ids: the decode entries (moe_k4_mlp, moe_k4_mlp_finish, moe_k4_expert_linear,
+ * moe_mxfp4_mlp, moe_mxfp4_mlp_finish) clamp an id outside [0, E) to the nearest valid expert
+ * instead of failing: checking ids on the host would synchronise the stream.  Callers validate
+ * ids beforehand (the routed entries produce valid ids themselves); the grouped entries skip such
+ * slots instead (see there).
  *
  * Each entry point names the reference interface it replaces (paths relative to the
  * reference repository root).

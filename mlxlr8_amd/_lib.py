@@ -109,8 +109,10 @@ _workspaces = {}
 
 
 def workspace(device, hidden, intermediate, kind="k4"):
-    """A zero-initialised scratch buffer per (device, shape, kind), reused across calls on one stream."""
-    key = (str(device), int(hidden), int(intermediate), kind)
+    """A zero-initialised scratch buffer per (device, current stream, shape, kind): calls on one stream
+    run in order and share it; calls on different streams get different buffers (sharing one would
+    race)."""
+    key = (str(device), torch.cuda.current_stream(device).cuda_stream, int(hidden), int(intermediate), kind)
     ws = _workspaces.get(key)
     if ws is None:
         size_fn = lib().moe_mxfp4_workspace_bytes if kind == "mxfp4" else lib().moe_workspace_bytes

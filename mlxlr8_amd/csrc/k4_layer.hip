@@ -1223,6 +1223,19 @@ size_t k4_layer_workspace_bytes(int h, int m) {
   return layer_carve(nullptr, h > 0 ? h : 128, m > 0 ? m : 128).bytes;
 }
 
+// The fused block reads x and the side-vector rows 8 bytes at a time (one token) and residual,
+// output and value rows 4 bytes at a time.
+int k4_layer_check_alignment(const uint16_t* x, const uint16_t* residual, const uint16_t* const in_scale[3],
+                             const uint16_t* const out_scale[3], const uint16_t* out, const uint16_t* values) {
+  auto misaligned = [](const void* p, uintptr_t a) { return p != nullptr && ((uintptr_t)p & (a - 1)) != 0; };
+  bool bad = misaligned(x, 8) || misaligned(residual, 4) || misaligned(out, 4) || misaligned(values, 4);
+  for (int i = 0; i < 3; i++) bad = bad || misaligned(in_scale[i], 8) || misaligned(out_scale[i], 4);
+  if (bad)
+    return fail(MOE_EINVAL, "the K4 decode block needs x and side-vector rows 8-byte aligned and residual, "
+                            "output and value rows 4-byte aligned");
+  return MOE_OK;
+}
+
 bool k4_layer_supported(int h, int m, bool route) {
   return h > 0 && m > 0 && h % (route ? kRouterSlice : 128) == 0 && m % 128 == 0 && h <= (route ? kMaxRouteHidden : 16384) &&
          m <= 16384;
@@ -1250,9 +1263,10 @@ int k4_layer_run(const uint16_t* x, const uint16_t* residual, int rows, int rout
                  const uint16_t* const in_scale[3], const uint16_t* const out_scale[3], int h, int m, int experts,
                  int combine, uint16_t* out, uint16_t* values, void* layer_ws, hipStream_t s) {
   if (!k4_layer_supported(h, m, route != 0))
-    return fail(MOE_ENOTSUP, "the fused K4 block needs hidden a multiple of %d and intermediate of 128 (got %d, %d)",
-                route ? kRouterSlice : 128, h, m);
+    return fail(MOE_ENOTSUP, "the fused K4 block needs hidden a multiple of %d%s and intermediate a multiple of 128 "
+                "(got %d, %d)", route ? kRouterSlice : 128, route ? " up to 8192 (fused router)" : "", h, m);
   if (rows < 1 || rows > kMaxRows) return fail(MOE_EINVAL, "the fused K4 block takes 1..%d rows (got %d)", kMaxRows, rows);
+  if (int rc = k4_layer_check_alignment(x, residual, in_scale, out_scale, out, values)) return rc;
   LayerArgs a{};
   a.x = x;
   a.residual = residual;

@@ -977,8 +977,14 @@ static int k4_block(const uint16_t* x, const uint16_t* attn, const uint16_t* nor
   if (rc) return rc;
   MOE_ARG(experts == 257, "the routed decode block needs 256 routed experts plus the shared expert (got %lld)",
           (long long)experts);
-  MOE_ARG(k4_layer_supported(h, m, true), "hidden must be a multiple of 512 and intermediate of 128 (got %d, %d)", h,
-          m);
+  MOE_ARG(k4_layer_supported(h, m, true),
+          "hidden must be a multiple of 1024 up to 8192 (fused router) and intermediate a multiple of 128 (got %d, %d)",
+          h, m);
+  {
+    const uint16_t* ins[3] = {in_g, in_u, in_d};
+    const uint16_t* outs[3] = {out_g, out_u, out_d};
+    if ((rc = k4_layer_check_alignment(norm_w ? nullptr : x, residual, ins, outs, out, nullptr))) return rc;
+  }
   if ((rc = validate_ws(workspace, workspace_bytes, h, m))) return rc;
   if ((rc = ensure_device_ready())) return rc;
   Workspace w = carve(workspace, h, m);
@@ -1016,6 +1022,11 @@ static int k4_mlp_common(const uint16_t* x, const uint32_t* ids, const float* sc
   MOE_ARG(experts >= 1, "no experts");
   MOE_ARG(k4_layer_supported(h, m, false), "hidden and intermediate must be multiples of 128 (got %d, %d)", h, m);
   if (out) MOE_ARG(slots == kSlots && scores && residual, "the combined finish needs 9 slots, scores and residual");
+  {
+    const uint16_t* ins[3] = {in_g, in_u, in_d};
+    const uint16_t* outs[3] = {out_g, out_u, out_d};
+    if ((rc = k4_layer_check_alignment(x, residual, ins, outs, out, values))) return rc;
+  }
   if ((rc = validate_ws(workspace, workspace_bytes, h, m))) return rc;
   if ((rc = ensure_device_ready())) return rc;
   Workspace w = carve(workspace, h, m);

@@ -34,6 +34,8 @@ int moe_router_fused_plan(const uint16_t* x, const float* w, const float* bias, 
 // beforehand from ids.  combine = 1 writes out (scores [rows, 8], residual), else per-slot values.
 size_t k4_layer_workspace_bytes(int h, int m);
 bool k4_layer_supported(int h, int m, bool route);
+int k4_layer_check_alignment(const uint16_t* x, const uint16_t* residual, const uint16_t* const in_scale[3],
+                             const uint16_t* const out_scale[3], const uint16_t* out, const uint16_t* values);
 int k4_layer_run(const uint16_t* x, const uint16_t* residual, int rows, int route, const float* router_w,
                  const float* bias, uint32_t* ids, float* scores, const uint8_t* const packed[3],
                  const uint16_t* const in_scale[3], const uint16_t* const out_scale[3], int h, int m, int experts,

@@ -59,7 +59,8 @@ class ExpertLayer:
 
     def prepare_decode(self, x, residual, router_weight, bias):
         """Bind device buffers once and return a zero-argument callable that enqueues the whole
-        decode block (one C call, no per-call tensor work); results land in `.out`, `.ids`, `.scores`."""
+        decode block (one C call, no per-call tensor work); results land in `.out`, `.ids`, `.scores`.
+        The call runs on the stream that is current now (its workspace belongs to that stream)."""
         h = self.hidden
         rows = x.numel() // h
         if rows > 8 or self.experts != 257 or x.dtype != BF16 or self.k != 4:

@@ -142,7 +142,8 @@ class JoinedMXFP4:
     def prepare_decode(self, x, residual, router_weight, bias):
         """Bind device buffers once and return a callable that enqueues router GEMV + route +
         MXFP4 MLP + combine for <= 8 decode rows in one C call (exlr8/fast_router.py:27-37 with the
-        joined experts); results land in `.out`, `.ids`, `.scores`."""
+        joined experts); results land in `.out`, `.ids`, `.scores`.  The call runs on the stream that
+        is current now (its workspace belongs to that stream)."""
         h = self.hidden
         rows = x.numel() // h
         if rows < 1 or rows > 8 or self.experts != 257 or x.dtype != BF16:

@@ -98,6 +98,20 @@ def test_encode_and_grouped_argument_errors_without_device():
     assert L.moe_k4_grouped_mlp_workspace_bytes(512, 9, 6144, 2048, 257) > 0
 
 
+def test_k4_decode_rejects_misaligned_rows_without_device():
+    """The fused K4 decode block reads x and side-vector rows 8 bytes at a time: a misaligned row
+    pointer is refused before anything is launched."""
+    from mlxlr8_amd._lib import lib
+    L = lib()
+    p = ctypes.c_void_p(256)
+    bytes_ = 3 * 128 * 128 // 2   # three K4 experts of 128 x 128
+    args = lambda x, in_g: [x, p, 1, 9, p, p, p, bytes_, in_g, p, p, p, p, p, 128, 128, p, p, 1 << 30, None]
+    assert L.moe_k4_mlp(*args(ctypes.c_void_p(258), p)) == -1
+    assert b"aligned" in L.moe_last_error()
+    assert L.moe_k4_mlp(*args(p, ctypes.c_void_p(260))) == -1
+    assert b"aligned" in L.moe_last_error()
+
+
 def test_trellis_grouped_and_combine_argument_errors_without_device():
     from mlxlr8_amd._lib import lib
     L = lib()

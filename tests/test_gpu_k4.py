@@ -247,6 +247,28 @@ def test_values_batch_equals_single_rows(cuda, glm_layer, rows, pattern):
         assert torch.equal(values[r].view(torch.int16), v1[0].view(torch.int16)), f"row {r} differs"
 
 
+def test_two_streams_keep_separate_scratch(cuda, glm_layer):
+    """Decode calls prepared on two streams use separate workspaces, so interleaved launches on the
+    two streams reproduce the single-stream results bit for bit."""
+    from mlxlr8_amd import synth
+    say("case: decode on two streams")
+    experts, layer, host, sc, w, bias = glm_layer
+    x, r = synth.activations(w.device, 55, 2)
+    want = [experts.decode_block(x[i:i + 1].contiguous(), r[i:i + 1].contiguous(), w, bias)[0] for i in range(2)]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    calls = []
+    for i, st in enumerate(streams):
+        with torch.cuda.stream(st):
+            calls.append(experts.prepare_decode(x[i:i + 1].contiguous(), r[i:i + 1].contiguous(), w, bias))
+    torch.cuda.synchronize()
+    for _ in range(10):
+        for c in calls:
+            c.run()
+    torch.cuda.synchronize()
+    for i in range(2):
+        assert torch.equal(calls[i].out.reshape(-1).view(torch.int16), want[i].reshape(-1).view(torch.int16))
+
+
 def test_mlp_values_glm(cuda, orc, glm_layer):
     from mlxlr8_amd.fast_decode import fast_expert_mlp
     say("case: GLM values rows=2")
