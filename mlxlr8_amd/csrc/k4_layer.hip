@@ -1048,7 +1048,12 @@ __global__ __launch_bounds__(kLW * 64) void k4_layer_kernel(LayerArgs a) {
       __builtin_amdgcn_s_setprio(2);
       float scale[NT];
       stage_in<NT, kDPre>(a, ui, it, in, tag, xw, scale);
-      __builtin_amdgcn_s_setprio(0);
+      // the last unit's parts head the launch's final dependency chain (its gate finishes, its
+      // down parts, the combine): they get issue priority over the other decoding waves
+      if (have_plan && it.u == units - 1)
+        __builtin_amdgcn_s_setprio(1);
+      else
+        __builtin_amdgcn_s_setprio(0);
       u32x4 pn[4];
       load_quad(pn, quad_ptr(a, ui, it, 1));
       // the next item is claimed once this one can no longer wait (a claimed item is only started

@@ -26,6 +26,10 @@ __global__ __launch_bounds__(256) void residual_rmsnorm_kernel(const uint16_t* _
                                                                uint16_t* __restrict__ out) {
   __shared__ float red[4];
   const int64_t row = blockIdx.x;
+  // the weight row depends on nothing: its loads go out with the activations' (one round trip)
+  u32x4v wv[K];
+#pragma unroll
+  for (int k = 0; k < K; k++) wv[k] = *reinterpret_cast<const u32x4v*>(w + k * 2048 + threadIdx.x * 8);
   u32x4v hv[K];
   float ss = 0.0f;
 #pragma unroll
@@ -52,12 +56,11 @@ __global__ __launch_bounds__(256) void residual_rmsnorm_kernel(const uint16_t* _
 #pragma unroll
   for (int k = 0; k < K; k++) {
     const int64_t off = row * n + k * 2048 + threadIdx.x * 8;
-    const u32x4v wv = *reinterpret_cast<const u32x4v*>(w + k * 2048 + threadIdx.x * 8);
     u32x4v o;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-      o[j] = pack_bf16(round_bf16(lo_bf16(wv[j]) * round_bf16(lo_bf16(hv[k][j]) * inv)),
-                       round_bf16(hi_bf16(wv[j]) * round_bf16(hi_bf16(hv[k][j]) * inv)));
+      o[j] = pack_bf16(round_bf16(lo_bf16(wv[k][j]) * round_bf16(lo_bf16(hv[k][j]) * inv)),
+                       round_bf16(hi_bf16(wv[k][j]) * round_bf16(hi_bf16(hv[k][j]) * inv)));
     }
     *reinterpret_cast<u32x4v*>(out + off) = o;
   }
