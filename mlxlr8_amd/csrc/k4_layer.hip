@@ -54,7 +54,7 @@
 #include "moe_device.h"
 #include "moe_host.h"
 #include "moe_plan.h"
-#include "route.h"
+#include "layer_sync.h"
 
 namespace moe {
 
@@ -70,14 +70,10 @@ namespace moe {
 #endif
 
 constexpr int kLW = MOE_LAYER_WAVES;
-constexpr int kRouterSlice = 1024;  // router inputs per work item
-constexpr int kMaxRouteHidden = 8192;  // hidden size limit of the fused router
-constexpr int kSpinLimit = 1 << 14;  // polls of a bounded wait (with the backoff below: ~50 ms)
 constexpr int kXcds = 8;            // queue sub-lists
 constexpr int kQueueStride = 32;    // ints between sub-list counters (one 128 B line each)
 
 enum LayerFin { LFIN_VALUES = 0, LFIN_COMBINE = 1 };
-enum LayerFlag { LF_ERROR = 1, LF_EXIT = 2, LF_EPOCH = 3, LF_COUNT = 8 };
 
 struct LayerWs {
   Plan* plan;
@@ -112,71 +108,6 @@ struct LayerArgs {
   LayerWs w;
 };
 
-// The lane index recomputed where it is used.  Code that runs rarely (router items, routing,
-// finishes) uses it: with the plain index the compiler hoists their lane-derived addresses to the
-// kernel's start, keeps them live across the decode loop and spills its registers to memory, and
-// every reload in a latency-critical item then costs a memory round trip.
-__device__ __forceinline__ int cold_lane() {
-  int l;
-  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
-  return l;
-}
-
-// ---------------------------------------------------------------- coherent and tagged words
-__device__ __forceinline__ int ld_coh_i(const int32_t* p) {
-  return __hip_atomic_load(const_cast<int32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-}
-__device__ __forceinline__ void st_coh_i(int32_t* p, int v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-}
-__device__ __forceinline__ float ld_coh_f(const float* p) {
-  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-}
-__device__ __forceinline__ uint64_t ld_tag(const uint64_t* p) {
-  return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-}
-__device__ __forceinline__ void st_tag(uint64_t* p, float v, uint32_t tag) {
-  __hip_atomic_store(p, (uint64_t)__float_as_uint(v) | ((uint64_t)tag << 32), __ATOMIC_RELAXED,
-                     __HIP_MEMORY_SCOPE_SYSTEM);
-}
-__device__ __forceinline__ bool has_tag(uint64_t w, uint32_t tag) { return (uint32_t)(w >> 32) == tag; }
-__device__ __forceinline__ float tag_value(uint64_t w) { return __uint_as_float((uint32_t)w); }
-__device__ __forceinline__ void set_error(const LayerArgs& a) {
-  if (lane_id() == 0) st_coh_i(a.w.flags + LF_ERROR, 1);
-}
-// One step of a bounded wait; false once the bound is exhausted (the error word is then set).
-// The pause doubles from 64 to 4096 clocks: waiting waves must leave the memory system to the
-// producers they wait for (hundreds of waves re-reading their inputs back to back starve them).
-__device__ __forceinline__ bool keep_waiting(const LayerArgs& a, int& spins) {
-  if (++spins >= kSpinLimit) {
-    set_error(a);
-    return false;
-  }
-  const int pauses = spins < 6 ? (1 << spins) : 64;
-  for (int k = 0; k < pauses; k++) __builtin_amdgcn_s_sleep(1);
-  return true;
-}
-// the lane's two words p[0], p[1] (a column pair) once both carry `tag`
-__device__ __forceinline__ f32x2 ld_tag_pair(const LayerArgs& a, const uint64_t* p, uint32_t tag) {
-  uint64_t w0 = ld_tag(p), w1 = ld_tag(p + 1);
-  int spins = 0;
-  while (!__all(has_tag(w0, tag) && has_tag(w1, tag)) && keep_waiting(a, spins)) {
-    w0 = ld_tag(p);
-    w1 = ld_tag(p + 1);
-  }
-  return f32x2{tag_value(w0), tag_value(w1)};
-}
-
-// ---------------------------------------------------------------- plan in LDS
-// Each block holds the plan in LDS: per unit the expert id, the token count, the unit's token rows
-// (3 bits each) and slots (7 bits each) packed, and (when the launch routes) the rows' scores.
-// A routing launch computes it in every block; otherwise it is copied from the prebuilt plan.
-struct PlanLds {
-  int32_t units;
-  int32_t ex[kMaxUnits], nt[kMaxUnits];
-  uint32_t tok[kMaxUnits], sl0[kMaxUnits], sl1[kMaxUnits];
-  float score[kMaxRows * 8];
-};
 // Returns the unit count.  Every word is requested unconditionally (indices clamped into the
 // arrays) so the loads issue back to back; units beyond the count are stored as empty.
 __device__ __forceinline__ int load_plan(const Plan* P, PlanLds& T) {
@@ -782,160 +713,6 @@ __device__ void down_finish(const LayerArgs& a, const UnitInfo& ui, int ob, bool
     release_stores();  // this wave's own slot outputs are read back by the combine
     combine_block(a, ob, tag, score);
   }
-}
-
-// ---------------------------------------------------------------- router
-// item r = e * S + j: partial logit of expert e over inputs [kRouterSlice j, kRouterSlice (j + 1))
-// for every row, stored tagged at logit_part[(row * S + j) * 256 + e].
-__device__ __forceinline__ void router_item(const LayerArgs& a, int r, int S, uint32_t tag) {
-  const int e = r / S, j = r - e * S;
-  const int lane = cold_lane();
-  constexpr int kPer = kRouterSlice / 64;  // 16 inputs per lane
-  const int k0 = j * kRouterSlice + kPer * lane;
-  f32x4 w[kPer / 4];
-#pragma unroll
-  for (int i = 0; i < kPer / 4; i++) w[i] = *reinterpret_cast<const f32x4*>(a.router_w + (int64_t)e * a.h + k0 + 4 * i);
-  for (int row = 0; row < a.rows; row++) {
-    u32x4 xv[kPer / 8];
-#pragma unroll
-    for (int i = 0; i < kPer / 8; i++) xv[i] = *reinterpret_cast<const u32x4*>(a.x + (int64_t)row * a.h + k0 + 8 * i);
-    float acc = 0.0f;
-#pragma unroll
-    for (int i = 0; i < kPer / 8; i++) {
-      const f32x4 wa = w[2 * i], wb = w[2 * i + 1];
-      acc = fmaf(bf16_to_f32((uint16_t)(xv[i].x & 0xFFFFu)), wa.x, acc);
-      acc = fmaf(bf16_to_f32((uint16_t)(xv[i].x >> 16)), wa.y, acc);
-      acc = fmaf(bf16_to_f32((uint16_t)(xv[i].y & 0xFFFFu)), wa.z, acc);
-      acc = fmaf(bf16_to_f32((uint16_t)(xv[i].y >> 16)), wa.w, acc);
-      acc = fmaf(bf16_to_f32((uint16_t)(xv[i].z & 0xFFFFu)), wb.x, acc);
-      acc = fmaf(bf16_to_f32((uint16_t)(xv[i].z >> 16)), wb.y, acc);
-      acc = fmaf(bf16_to_f32((uint16_t)(xv[i].w & 0xFFFFu)), wb.z, acc);
-      acc = fmaf(bf16_to_f32((uint16_t)(xv[i].w >> 16)), wb.w, acc);
-    }
-    const float tot = wave_sum(acc);
-    if (lane == 63) st_tag(a.w.logit_part + ((int64_t)row * S + j) * 256 + e, tot, tag);
-  }
-}
-
-// Routing of every row by one wave into its block's plan table: logits summed over their slices in
-// slice order, bias-corrected top-8 per row, then the units -- the shared expert as unit 0 and the
-// routed experts in first-appearance (slot) order.  Every block computes the same table from the
-// same words; block 0 also stores ids and scores for the caller.
-__device__ void route_block(const LayerArgs& a, int S, uint32_t tag, PlanLds& T) {
-  const int lane = cold_lane();
-  __shared__ int32_t sid_lds[kMaxRows * kSlots];
-  constexpr int kMaxS = kMaxRouteHidden / kRouterSlice;
-  float bias[4];
-#pragma unroll
-  for (int i = 0; i < 4; i++) bias[i] = a.bias[lane + 64 * i];
-  for (int row = 0; row < a.rows; row++) {
-    const uint64_t* lp = a.w.logit_part + (int64_t)row * S * 256;
-    int spins = 0;
-    // every word of the lane's four experts in one round trip; while some are not yet current, a
-    // sample (one word per lane spread over the row's slices) is polled before loading them again
-    uint64_t wd[kMaxS][4];
-    for (;;) {
-#pragma unroll
-      for (int j = 0; j < kMaxS; j++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) wd[j][i] = ld_tag(lp + (int64_t)min(j, S - 1) * 256 + lane + 64 * i);
-      bool ok = true;
-#pragma unroll
-      for (int j = 0; j < kMaxS; j++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) ok = ok & has_tag(wd[j][i], tag);
-      if (__all(ok)) break;
-      bool live = true;
-      for (;;) {
-        if (__all(has_tag(ld_tag(lp + (lane * 24 + 7) % (S * 256)), tag))) break;
-        if (!keep_waiting(a, spins)) {
-          live = false;
-          break;
-        }
-      }
-      if (!live) break;
-    }
-    RouteInput in;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      float v = 0.0f;
-#pragma unroll
-      for (int j = 0; j < kMaxS; j++)
-        if (j < S) v += tag_value(wd[j][i]);
-      in.logit[i] = v;
-      in.bias[i] = bias[i];
-    }
-    route_select<false>(in, row, a.ids, a.scores, sid_lds, blockIdx.x == 0, T.score);
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  // Units.  Routed slot s' = 8 row + k is lane s' (global slot 9 row + k).  A row holds each expert
-  // at most once, so a slot's position inside its unit is the number of earlier rows that chose the
-  // same expert; the unit's first slot (position 0) leads it, and units are numbered in the order
-  // of their leading slots.  Per-row expert bitmaps in LDS answer both questions in one pass over
-  // the rows; the unit's rows and slots are then merged with LDS or (order-free).
-  __shared__ uint32_t row_bits[kMaxRows][8];  // row r: bit e when expert e is in the row's top-8
-  __shared__ uint8_t row_rank[kMaxRows][256];  // row r, expert e: its rank in the row (where set)
-  const int n = a.rows * 8;
-  const bool act = lane < n;
-  const int row = lane >> 3, k = lane & 7;
-  const int e = act ? min(max(sid_lds[row * kSlots + k], 0), 255) : 0;
-  row_bits[lane >> 3][lane & 7] = 0u;
-  for (int u = lane; u < kMaxUnits; u += 64) {
-    T.tok[u] = 0u;
-    T.sl0[u] = 0u;
-    T.sl1[u] = 0u;
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  if (act) {
-    __hip_atomic_fetch_or(&row_bits[row][e >> 5], 1u << (e & 31), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    row_rank[row][e] = (uint8_t)k;
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  int pos = 0, total = 0, first_row = row;
-  for (int r = a.rows - 1; r >= 0; r--) {
-    const int b = (int)((row_bits[r][e >> 5] >> (e & 31)) & 1u);
-    total += b;
-    pos += r < row ? b : 0;
-    first_row = b ? r : first_row;
-  }
-  const int first_lane = first_row * 8 + row_rank[first_row][e];
-  const uint64_t firsts = __ballot(act && pos == 0);
-  const int unit = 1 + (int)__popcll(firsts & ((1ull << first_lane) - 1ull));
-  if (act) {
-    if (pos == 0) {
-      T.ex[unit] = e;
-      T.nt[unit] = total;
-    }
-    const uint32_t gs = (uint32_t)(row * kSlots + k);
-    __hip_atomic_fetch_or(&T.tok[unit], (uint32_t)row << (3 * pos), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    if (pos < 4)
-      __hip_atomic_fetch_or(&T.sl0[unit], gs << (7 * pos), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    else
-      __hip_atomic_fetch_or(&T.sl1[unit], gs << (7 * (pos - 4)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-  }
-  if (lane == 0) {
-    uint32_t t0 = 0, z0 = 0, z1 = 0;
-    for (int r = 0; r < a.rows; r++) {
-      t0 |= (uint32_t)r << (3 * r);
-      if (r < 4) z0 |= (uint32_t)(r * kSlots + 8) << (7 * r);
-      else z1 |= (uint32_t)(r * kSlots + 8) << (7 * (r - 4));
-    }
-    T.ex[0] = 256;
-    T.nt[0] = a.rows;
-    T.tok[0] = t0;
-    T.sl0[0] = z0;
-    T.sl1[0] = z1;
-    T.units = 1 + (int)__popcll(firsts);
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 // Share k of SHARES of the code table (a power-of-two size) into LDS by one wave, in one batch:
