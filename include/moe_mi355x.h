@@ -163,7 +163,10 @@ int moe_mxfp4_mlp_finish(const uint16_t* x, const uint32_t* ids, const float* sc
                          uint16_t* out, void* workspace, size_t workspace_bytes, moe_stream_t stream);
 
 /* Router GEMV + route (as moe_k4_moe_decode) + joined-MXFP4 MLP + combine for 1..8 decode rows in
- * one call; indices [rows, 9] and scores [rows, 8] may be NULL (kept in the workspace).
+ * one call; indices [rows, 9] and scores [rows, 8] may be NULL (kept in the workspace).  One row
+ * runs as a single persistent launch (router, both projections of the nine slots and the combine;
+ * one block per compute unit, all resident together); 2..8 rows as the router kernel and two GEMV
+ * launches.  Given the same ids and scores both produce the same output bits.
  * Replaces: exlr8/fast_router.py:27-37 compiled_finish with the joined-MXFP4 experts
  *           (exlr8/joined_mxfp4.py:148-163 JoinedMXFP4.finish; exlr8/model.py:406-418). */
 int moe_mxfp4_moe_decode(const uint16_t* x, const uint16_t* residual, int rows, const float* router_w,
@@ -180,8 +183,9 @@ size_t moe_mxfp4_workspace_bytes(int hidden, int intermediate);
 /* moe_mxfp4_moe_decode with no workspace argument and no allocation of any kind: the workspace is
  * the library's fixed per-GPU scratch array (4 MiB, held by each GPU the library runs on until the
  * process ends; its address is resolved on the first call on a device, so call moe_init() and this
- * entry once before capturing it in a graph).  Its counters are cleared by a fill kernel at the start
- * of every call.  Shapes whose workspace exceeds the scratch are rejected with MOE_ENOTSUP.  Every
+ * entry once before capturing it in a graph).  For 2..8 rows its counters are cleared by a fill
+ * kernel at the start of every call; one row needs no clearing (the single-launch block tags its
+ * words per launch and leaves its counters at zero).  Shapes whose workspace exceeds the scratch are rejected with MOE_ENOTSUP.  Every
  * call on one GPU shares that GPU's scratch: calls that overlap on one GPU (several streams or
  * threads) race.
  * No counterpart in the reference: for callers that cannot allocate device memory (code under HIP

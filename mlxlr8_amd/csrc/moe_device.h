@@ -596,6 +596,27 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// ---------------------------------------------------------------- MXFP4 (e2m1 codes, e8m0 scales)
+// 8 scaled fp4 codes of a 32-bit word -> 8 floats, accumulated against x[0..7]
+__device__ __forceinline__ float dot8_fp4(uint32_t w, float scale, const float* x, float acc) {
+  const f32x2 v0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, scale, 0);
+  const f32x2 v1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, scale, 1);
+  const f32x2 v2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, scale, 2);
+  const f32x2 v3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, scale, 3);
+  acc = fmaf(x[0], v0.x, acc);
+  acc = fmaf(x[1], v0.y, acc);
+  acc = fmaf(x[2], v1.x, acc);
+  acc = fmaf(x[3], v1.y, acc);
+  acc = fmaf(x[4], v2.x, acc);
+  acc = fmaf(x[5], v2.y, acc);
+  acc = fmaf(x[6], v3.x, acc);
+  acc = fmaf(x[7], v3.y, acc);
+  return acc;
+}
+
+// e8m0 block scale 2^(s-127) as a float (s = 0: 2^-127, a denormal)
+__device__ __forceinline__ float e8m0_to_f32(uint32_t s) { return __uint_as_float(s == 0 ? 0x00400000u : s << 23); }
+
 // ---------------------------------------------------------------- small wave helpers
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 __device__ __forceinline__ int wave_id_in_block() { return threadIdx.x >> 6; }

@@ -43,6 +43,15 @@ int k4_layer_run(const uint16_t* x, const uint16_t* residual, int rows, int rout
 // The layer workspace's plan (where a plan kernel writes it for route = 0).
 Plan* k4_layer_plan(void* layer_ws);
 
+// Fused joined-MXFP4 decode block for one token row (mx_layer.hip; hidden 6144, intermediate 2048,
+// 256 routed experts + the shared expert 256): router, both projections of the nine slots and the
+// combine in one launch.  `layer_ws`: mx_layer_workspace_bytes() bytes, zeroed once.
+size_t mx_layer_workspace_bytes();
+int mx_layer_run(const uint16_t* x, const uint16_t* residual, const float* router_w, const float* bias, uint32_t* ids,
+                 float* scores, const uint8_t* gu_codes, const uint8_t* gu_scales, const uint8_t* d_codes,
+                 const uint8_t* d_scales, const uint16_t* unit, const uint16_t* out_gate, const uint16_t* out_up,
+                 const uint16_t* in_down, const uint16_t* out_down, uint16_t* out, void* layer_ws, hipStream_t s);
+
 }  // namespace moe
 
 #define MOE_HIP(expr)                                                              \

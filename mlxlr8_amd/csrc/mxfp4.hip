@@ -76,25 +76,6 @@ __device__ __forceinline__ int slot_expert(const MxArgs& a, int s) {
   return e;
 }
 
-// 8 scaled fp4 codes of a 32-bit word -> 8 floats, accumulated against x[0..7]
-__device__ __forceinline__ float dot8_fp4(uint32_t w, float scale, const float* x, float acc) {
-  const f32x2 v0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, scale, 0);
-  const f32x2 v1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, scale, 1);
-  const f32x2 v2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, scale, 2);
-  const f32x2 v3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, scale, 3);
-  acc = fmaf(x[0], v0.x, acc);
-  acc = fmaf(x[1], v0.y, acc);
-  acc = fmaf(x[2], v1.x, acc);
-  acc = fmaf(x[3], v1.y, acc);
-  acc = fmaf(x[4], v2.x, acc);
-  acc = fmaf(x[5], v2.y, acc);
-  acc = fmaf(x[6], v3.x, acc);
-  acc = fmaf(x[7], v3.y, acc);
-  return acc;
-}
-
-__device__ __forceinline__ float e8m0_to_f32(uint32_t s) { return __uint_as_float(s == 0 ? 0x00400000u : s << 23); }
-
 // KC = K / 2048 (16-byte chunks per lane per row): 3 for K = 6144 (gate/up), 1 for K = 2048 (down).
 // down launches (K = 2048): kept within 128 VGPRs so two 8-wave blocks share a CU, and launched
 // with that many blocks per CU (more rows in flight per CU)
@@ -326,6 +307,7 @@ struct MxWorkspace {
   float* logits;         // [8][256]
   uint32_t* ids;         // [8][9]
   float* scores;         // [8][8]
+  void* layer;           // the fused one-row decode block's region (mx_layer.hip)
   size_t bytes;
 };
 
@@ -344,6 +326,7 @@ MxWorkspace mx_carve(void* base, int h, int m) {
   w.logits = reinterpret_cast<float*>(take((size_t)kMaxRows * 256 * 4));
   w.ids = reinterpret_cast<uint32_t*>(take((size_t)kMaxRows * kSlots * 4));
   w.scores = reinterpret_cast<float*>(take((size_t)kMaxRows * 8 * 4));
+  w.layer = take(mx_layer_workspace_bytes());
   w.bytes = off;
   return w;
 }
@@ -499,7 +482,8 @@ int moe_mxfp4_mlp_finish(const uint16_t* x, const uint32_t* ids, const float* sc
 }
 
 // Router GEMV + route + joined-MXFP4 MLP + combine for decode rows in one call on a checked
-// workspace (every argument is validated before the first launch).
+// workspace (every argument is validated before the first launch).  One token row runs the fused
+// single-launch block (mx_layer.hip); more rows run the router kernel and the two GEMV launches.
 static int mx_decode_block(const uint16_t* x, const uint16_t* residual, int rows, const float* router_w,
                            const float* bias, const uint8_t* gate_up_codes, const uint8_t* gate_up_scales,
                            const uint8_t* down_codes, const uint8_t* down_scales, int64_t experts, const uint16_t* unit,
@@ -518,6 +502,9 @@ static int mx_decode_block(const uint16_t* x, const uint16_t* residual, int rows
                     out_gate, out_up, in_down, out_down, hidden, intermediate, workspace, workspace_bytes);
   if (rc) return rc;
   if ((rc = ensure_device_ready())) return rc;
+  if (rows == 1)
+    return mx_layer_run(x, residual, router_w, bias, ids, sc, gate_up_codes, gate_up_scales, down_codes, down_scales,
+                        unit, out_gate, out_up, in_down, out_down, out, w.layer, s);
   if (clear_counters) {
     // counters that must start at zero: the router's arrival counter and the MLP's block and group
     // counters (a fill kernel, not a memset node, so the call can be captured in a graph)

@@ -121,3 +121,21 @@ def test_mxfp4_decode_block_one_call(cuda, orc):
         assert err <= 1e-3 and err_moe <= 1e-3
         again, _, _ = joined.decode_block(x, res, w, bias)
         assert torch.equal(out.view(torch.int16), again.view(torch.int16))
+
+
+def test_mxfp4_fused_block_equals_three_launch_path(cuda):
+    """One-row decode runs the single-launch block (router, both projections, combine); given the
+    ids and scores it routed, the three-launch finish produces the same output bits, call after
+    call (the block's words are tagged per launch, so replays never read stale values)."""
+    from mlxlr8_amd import synth
+    say("case: mxfp4 fused one-row block vs three-launch finish")
+    joined, _ = _layer(cuda, 257, 6161)
+    w, bias = synth.router(cuda, 6161)
+    for seed in range(4):
+        x, res = synth.activations(cuda, 6200 + seed, 1)
+        out, ids, scores = joined.decode_block(x, res, w, bias)
+        ref = joined.finish(x, ids, scores, res)
+        torch.cuda.synchronize()
+        same = torch.equal(out.view(torch.int16), ref.view(torch.int16))
+        say(f"  seed={seed} ids={ids.cpu().numpy().tolist()} identical={same}")
+        assert same
