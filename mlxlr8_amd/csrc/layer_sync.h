@@ -61,15 +61,17 @@ __device__ __forceinline__ void set_error(const A& a) {
   if (lane_id() == 0) st_coh_i(a.w.flags + LF_ERROR, 1);
 }
 // One step of a bounded wait; false once the bound is exhausted (the error word is then set).
-// The pause doubles from 64 to 4096 clocks: waiting waves must leave the memory system to the
-// producers they wait for (hundreds of waves re-reading their inputs back to back starve them).
-template <class A>
+// The pause doubles from 64 clocks up to 64 * kMaxPauses: waiting waves must leave the memory
+// system to the producers they wait for (hundreds of waves re-reading their inputs back to back
+// starve them).  A wait on the critical path that only one wave per block makes (routing) uses a
+// short pause; the bound on the total wait stays the same (~50 ms).
+template <int kMaxPauses = 64, class A>
 __device__ __forceinline__ bool keep_waiting(const A& a, int& spins) {
-  if (++spins >= kSpinLimit) {
+  if (++spins >= kSpinLimit * (64 / kMaxPauses)) {
     set_error(a);
     return false;
   }
-  const int pauses = spins < 6 ? (1 << spins) : 64;
+  const int pauses = spins < 6 ? min(1 << spins, kMaxPauses) : kMaxPauses;
   for (int k = 0; k < pauses; k++) __builtin_amdgcn_s_sleep(1);
   return true;
 }
@@ -161,7 +163,7 @@ __device__ void route_block(const A& a, int S, uint32_t tag, PlanLds& T) {
       bool live = true;
       for (;;) {
         if (__all(has_tag(ld_tag(lp + (lane * 24 + 7) % (S * 256)), tag))) break;
-        if (!keep_waiting(a, spins)) {
+        if (!keep_waiting<4>(a, spins)) {
           live = false;
           break;
         }
@@ -183,6 +185,22 @@ __device__ void route_block(const A& a, int S, uint32_t tag, PlanLds& T) {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if (a.rows == 1) {
+    // one row: unit 0 = the shared expert (slot 8), unit 1 + k = the row's expert of rank k (slot k)
+    if (lane < kSlots) {
+      const int u = lane < 8 ? lane + 1 : 0;
+      T.ex[u] = lane < 8 ? min(max(sid_lds[lane], 0), 255) : 256;
+      T.nt[u] = 1;
+      T.tok[u] = 0u;
+      T.sl0[u] = (uint32_t)lane;
+      T.sl1[u] = 0u;
+    }
+    if (lane == 0) T.units = kSlots;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    return;
+  }
   // Units.  Routed slot s' = 8 row + k is lane s' (global slot 9 row + k).  A row holds each expert
   // at most once, so a slot's position inside its unit is the number of earlier rows that chose the
   // same expert; the unit's first slot (position 0) leads it, and units are numbered in the order

@@ -119,7 +119,7 @@ __device__ void mx_gate_finish(const MxLayerArgs& a, int q, uint32_t tag, const 
     w[2] = ld_tag(gp + kM);
     w[3] = ld_tag(gp + kM + 1);
     if (__all(has_tag(w[0], tag) && has_tag(w[1], tag) && has_tag(w[2], tag) && has_tag(w[3], tag)) ||
-        !keep_waiting(a, spins))
+        !keep_waiting<8>(a, spins))
       break;
   }
   float g0 = tag_value(w[0]), g1 = tag_value(w[1]), u0 = tag_value(w[2]), u1 = tag_value(w[3]);
@@ -156,10 +156,10 @@ __device__ void mx_combine(const MxLayerArgs& a, int nb, uint32_t tag, const Pla
     bool ok = true;
 #pragma unroll
     for (int u = 0; u < kUnits; u++) ok = ok & has_tag(wd[u][0], tag) & has_tag(wd[u][1], tag);
-    if (__all(ok) || !keep_waiting(a, spins)) break;
+    if (__all(ok) || !keep_waiting<8>(a, spins)) break;
     // one word per lane (lane l: unit l mod 9) until current, then the full reload
     const uint64_t* sp = a.w.dn + (int64_t)(lane % kUnits) * kH + 128 * nb + 2 * (lane / kUnits);
-    while (!__all(has_tag(ld_tag(sp), tag)) && keep_waiting(a, spins)) {
+    while (!__all(has_tag(ld_tag(sp), tag)) && keep_waiting<8>(a, spins)) {
     }
   }
   // slot j < 8: routed unit j + 1; slot 8: the shared expert (unit 0)
@@ -195,7 +195,7 @@ __device__ void mx_combine(const MxLayerArgs& a, int nb, uint32_t tag, const Pla
 // read by every block that has down slots of its unit).
 __device__ __forceinline__ void mx_stage_down_input(const MxLayerArgs& a, int u, float* dst) {
   int spins = 0;
-  while (__builtin_amdgcn_readfirstlane(ld_coh_i(a.w.hid_cnt + u)) < kGfPerUnit && keep_waiting(a, spins)) {
+  while (__builtin_amdgcn_readfirstlane(ld_coh_i(a.w.hid_cnt + u)) < kGfPerUnit && keep_waiting<8>(a, spins)) {
   }
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
   const int lane = cold_lane();

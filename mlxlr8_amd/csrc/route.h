@@ -61,10 +61,28 @@ __device__ __forceinline__ void route_row(const float* __restrict__ logits, cons
   route_select(route_load<COHERENT>(logits, bias, row), row, ids, scores, sid, store_global);
 }
 
-// Selection of one row from its loaded logits: a radix select on 40-bit keys (choice key << 8 |
-// 255 - id).  Keys are unique, so "top 8 by descending choice, ties to the lower id" is exactly
-// "the 8 largest keys".  Each bisection step counts candidates with wave-wide compare masks (no
-// LDS round trip); the 8 winners are then ranked against each other and the scores summed in
+// Largest value over the wave's lanes (valid in lane 63): the DPP steps of wave_sum with max.
+// Lanes a broadcast step does not reach keep their value (max with 0, the unsigned identity).
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, 0xF, false);
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, dpp_u32<0xB1>(v));        // quad_perm [1,0,3,2]
+  v = max(v, dpp_u32<0x4E>(v));        // quad_perm [2,3,0,1]
+  v = max(v, dpp_u32<0x124>(v));       // row_ror:4
+  v = max(v, dpp_u32<0x128>(v));       // row_ror:8
+  v = max(v, dpp_u32<0x142, 0xA>(v));  // row_bcast:15 into rows 1 and 3
+  v = max(v, dpp_u32<0x143, 0xC>(v));  // row_bcast:31 into rows 2 and 3
+  return v;
+}
+
+// Selection of one row from its loaded logits.  The order is "descending choice, ties to the lower
+// id" (a total order on (choice key, id)).  Each lane sorts its four candidates; then eight rounds
+// each take the wave's largest head: a DPP max over the heads' choice keys, the owner lane found by
+// ballot (a tie between lanes' heads -- equal choice keys -- goes to the lower id through a second
+// max over the tied lanes' inverted ids), and the owner pops its head.  The winners come out in
+// rank order, their sigmoid values and ids handed over by lane reads; the scores are summed in
 // rank order.  COH_OUT: ids and scores are stored write-through (read by other CUs in the same
 // launch).
 template <bool COH_OUT>
@@ -73,106 +91,93 @@ __device__ __forceinline__ void route_select(const RouteInput& in, int row, uint
                                              float* score_lds) {
   const int lane = lane_id();
   float orig[4];
-  uint32_t fk[4];
-  uint64_t key[4];
+  uint32_t fk[4], id[4];
 #pragma unroll
   for (int i = 0; i < 4; i++) {
-    const int e = lane + 64 * i;
+    id[i] = (uint32_t)(lane + 64 * i);
     orig[i] = router_sigmoid(in.logit[i]);
-    const float choice = orig[i] + in.bias[i];
-    fk[i] = float_key(choice);
-    key[i] = ((uint64_t)fk[i] << 8) | (uint64_t)(255 - e);
+    fk[i] = float_key(orig[i] + in.bias[i]);
   }
-  // Bisection on the choice keys alone first (32-bit compares), each compare into its own mask so
-  // the four compares of a step overlap: th = the 8th largest choice key.  Only when more than 8
-  // keys reach th (a tie at the boundary) do the 8 id bits continue the bisection on full keys.
-  uint32_t th = 0;
-  for (int b = 31; b >= 0; b--) {
-    const uint32_t cand = th | (1u << b);
-    uint64_t m[4];
+  // the lane's candidates in descending order (a five-exchange network; ids are already ascending
+  // within a lane, so "a before b" is fk[a] > fk[b] or equal keys with the lower id first)
+  auto order = [&](int a, int b) {
+    const bool swap = fk[b] > fk[a] || (fk[b] == fk[a] && id[b] < id[a]);
+    const uint32_t tk = fk[a], ti = id[a];
+    const float to = orig[a];
+    fk[a] = swap ? fk[b] : fk[a];
+    id[a] = swap ? id[b] : id[a];
+    orig[a] = swap ? orig[b] : orig[a];
+    fk[b] = swap ? tk : fk[b];
+    id[b] = swap ? ti : id[b];
+    orig[b] = swap ? to : orig[b];
+  };
+  order(0, 1);
+  order(2, 3);
+  order(0, 2);
+  order(1, 3);
+  order(1, 2);
+  float sel[8];
+  uint32_t win[8];
+  uint32_t live = 4;  // candidates left in this lane (popped heads are replaced from the back)
 #pragma unroll
-    for (int i = 0; i < 4; i++) m[i] = __builtin_amdgcn_uicmp(fk[i], cand, 35 /* unsigned >= */);
-    int cnt = 0;
-#pragma unroll
-    for (int i = 0; i < 4; i++) cnt += __popcll(m[i]);
-    if (cnt >= 8) th = cand;
-  }
-  uint64_t thr = (uint64_t)th << 8;
-  {
-    int at = 0;
-#pragma unroll
-    for (int i = 0; i < 4; i++) at += __popcll(__builtin_amdgcn_uicmp(fk[i], th, 35));
-    if (at > 8) {
-      for (int b = 7; b >= 0; b--) {
-        const uint64_t cand = thr | (1ull << b);
-        uint64_t m[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) m[i] = __builtin_amdgcn_uicmpl(key[i], cand, 35);
-        int cnt = 0;
-#pragma unroll
-        for (int i = 0; i < 4; i++) cnt += __popcll(m[i]);
-        if (cnt >= 8) thr = cand;
-      }
+  for (int r = 0; r < 8; r++) {
+    const uint32_t head = live > 0 ? fk[0] : 0u;
+    const uint32_t top = (uint32_t)__builtin_amdgcn_readlane((int)wave_max_u32(head), 63);
+    const bool mine = live > 0 && head == top;
+    uint64_t owners = __ballot(mine);
+    if (__popcll(owners) > 1) {
+      // equal choice keys in several lanes: the lowest id among them
+      const uint32_t low = ~(uint32_t)__builtin_amdgcn_readlane((int)wave_max_u32(mine ? ~id[0] : 0u), 63);
+      owners = __ballot(mine && id[0] == low);
+    }
+    const int owner = (int)__builtin_ctzll(owners);
+    sel[r] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, orig[0]), owner));
+    win[r] = (uint32_t)__builtin_amdgcn_readlane((int)id[0], owner);
+    if (lane == owner) {
+      fk[0] = fk[1];
+      id[0] = id[1];
+      orig[0] = orig[1];
+      fk[1] = fk[2];
+      id[1] = id[2];
+      orig[1] = orig[2];
+      fk[2] = fk[3];
+      id[2] = id[3];
+      orig[2] = orig[3];
+      live--;
     }
   }
-  // exactly 8 keys are >= thr.  The winners are packed into 8 LDS entries (position = winners in
-  // earlier slots and lower lanes); lane l < 8 then ranks entry l against the other seven
-  // (descending, keys are unique) and places its sigmoid score and id at that rank.
-  __shared__ uint64_t wkey_lds[kMaxRows][8];
-  __shared__ float worig_lds[kMaxRows][8];
-  __shared__ float sel_lds[kMaxRows][8];
-  __shared__ int id_lds[kMaxRows][8];
-  const int rs = row & (kMaxRows - 1);
-  uint64_t* wk = wkey_lds[rs];
-  float* wo = worig_lds[rs];
-  float* sel = sel_lds[rs];
-  int* idl = id_lds[rs];
-  int before = 0;
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const uint64_t m = __ballot(key[i] >= thr);
-    const int pos = before + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
-                                                            __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-    if (key[i] >= thr) {
-      wk[pos] = key[i];
-      wo[pos] = orig[i];
-    }
-    before += __popcll(m);
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  if (lane < 8) {
-    const uint64_t mine = wk[lane];
-    int rank = 0;
-#pragma unroll
-    for (int j = 0; j < 8; j++) rank += wk[j] > mine ? 1 : 0;
-    sel[rank] = wo[lane];
-    idl[rank] = 255 - (int)(mine & 0xFFu);
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   if ((store_global || score_lds != nullptr) && lane < 9) {
     // every lane forms the same rank-ordered sum; lane i < 8 writes winner i, lane 8 the shared id
     float total = 1e-20f;
 #pragma unroll
     for (int i = 0; i < 8; i++) total += sel[i];
-    const float score = lane < 8 ? sel[lane] / total * 2.5f : 0.0f;
-    const uint32_t id = lane < 8 ? (uint32_t)idl[lane] : 256u;
+    float mine = sel[0];
+    uint32_t mid = win[0];
+#pragma unroll
+    for (int i = 1; i < 8; i++) {
+      mine = lane == i ? sel[i] : mine;
+      mid = lane == i ? win[i] : mid;
+    }
+    const float score = lane < 8 ? mine / total * 2.5f : 0.0f;
+    const uint32_t idv = lane < 8 ? mid : 256u;
     if (score_lds != nullptr && lane < 8) score_lds[row * 8 + lane] = score;
     if (store_global) {
       if (COH_OUT) {
         if (lane < 8)
           __hip_atomic_store(scores + (int64_t)row * 8 + lane, score, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        __hip_atomic_store(ids + (int64_t)row * 9 + lane, id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(ids + (int64_t)row * 9 + lane, idv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
       } else {
         if (lane < 8) scores[(int64_t)row * 8 + lane] = score;
-        ids[(int64_t)row * 9 + lane] = id;
+        ids[(int64_t)row * 9 + lane] = idv;
       }
     }
   }
-  if (sid != nullptr && lane < 9) sid[row * 9 + lane] = lane < 8 ? idl[lane] : 256;
+  if (sid != nullptr && lane < 9) {
+    uint32_t mid = win[0];
+#pragma unroll
+    for (int i = 1; i < 8; i++) mid = lane == i ? win[i] : mid;
+    sid[row * 9 + lane] = lane < 8 ? (int)mid : 256;
+  }
 }
 
 }  // namespace moe
