@@ -63,9 +63,9 @@ def parse():
     return p.parse_args()
 
 
-def traffic_from_profiles():
-    """HBM bytes per layer launch from the committed rocprofv3 PMC summary, if present."""
-    path = ROOT / "profiles" / "k4_layer_b1_pmc.txt"
+def traffic_from_profiles(name="k4_layer_b1_pmc.txt"):
+    """HBM bytes per layer launch from a committed rocprofv3 PMC summary, if present."""
+    path = ROOT / "profiles" / name
     if not path.exists():
         return None
     for line in path.read_text().splitlines():
@@ -296,12 +296,13 @@ def bench_mxfp4_decode(args):
     calls = [[l.prepare_decode(x, r, w, bias) for (x, r) in toks] for l in layers]
     ms = _time_steps(lambda i: calls[i % len(calls)][i % len(toks)].run(), args.steps, args.warmup)
     algo = 9 * MX_EXPERT_BYTES + 256 * H * 4 + 9 * (3 * M + H) * 2 + H * 2 + 256 * 4 + 3 * H * 2
-    return dict(_line(args, 1e3 / ms, "tokens/s", ms, "f32",
-                      "GLM-5.3-style joined-MXFP4 MoE layer, batch-1 decode: hidden 6144, 256 routed + 1 shared, "
-                      "top-8, intermediate 2048 (e2m1 + e8m0 per 32), bf16 activations, fp32 accumulate",
-                      {"global_batch": 1, "seq_len": 1, "layers_rotated": len(layers)}, algo,
-                      "whole step: router + mx_gemv gate_up + mx_gemv down/combine"),
-                us_per_token=round(ms * 1e3, 2))
+    line = _line(args, 1e3 / ms, "tokens/s", ms, "f32",
+                 "GLM-5.3-style joined-MXFP4 MoE layer, batch-1 decode: hidden 6144, 256 routed + 1 shared, "
+                 "top-8, intermediate 2048 (e2m1 + e8m0 per 32), bf16 activations, fp32 accumulate",
+                 {"global_batch": 1, "seq_len": 1, "layers_rotated": len(layers)}, algo,
+                 "mx_layer_kernel: router, both projections of the nine slots and the combine in one launch")
+    line["roofline"]["traffic"] = traffic_from_profiles("mxfp4_layer_b1_pmc.txt")
+    return dict(line, us_per_token=round(ms * 1e3, 2))
 
 
 def bench_k4_verify(args):
@@ -325,7 +326,7 @@ def bench_k4_verify(args):
                       "8-token speculative-verify batch through the K4-trellis MoE layer (correlated rows, "
                       "distinct experts streamed once)",
                       {"global_batch": 8, "seq_len": 1, "distinct_experts": U, "layers_rotated": len(layers)},
-                      algo, "whole step: router + k4_mfma_kernel gate/up + down/combine"),
+                      algo, "k4_layer_kernel<8>: router, the distinct experts' projections and the combine in one launch"),
                 us_per_step=round(ms * 1e3, 2))
 
 
@@ -400,7 +401,7 @@ def bench_stack(args):
     out = _line(args, 1e3 / ms, "tokens/s", ms, "f32",
                 "20 consecutive GLM-5.3-style K4-trellis MoE layers (independent seeded weights, Zipf-skewed "
                 "router biases, RMSNorm'd residual per layer), batch-1 decode",
-                {"global_batch": 1, "seq_len": 1, "layers": n}, algo, "whole step: 20 x (router+norm, gate/up, down)")
+                {"global_batch": 1, "seq_len": 1, "layers": n}, algo, "20 x (residual + RMSNorm launch, fused K4 block launch)")
     out["steps"] = steps
     out["us_per_token_stack"] = round(ms * 1e3, 2)
     return out
