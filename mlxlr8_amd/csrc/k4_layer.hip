@@ -69,9 +69,18 @@ namespace moe {
 #define MOE_LAYER_ALU_ODD 2
 #endif
 
+// longest pause (in 64-clock sleeps) of the finishes' and staging waits: they sit on the launch's
+// final dependency chain, so a wait must not oversleep the value it waits for by long
+#ifndef MOE_LAYER_WAIT
+#define MOE_LAYER_WAIT 16
+#endif
+#ifndef MOE_LAYER_GS
+#define MOE_LAYER_GS 1
+#endif
 constexpr int kLW = MOE_LAYER_WAVES;
 constexpr int kXcds = 8;            // queue sub-lists
 constexpr int kQueueStride = 32;    // ints between sub-list counters (one 128 B line each)
+constexpr int kSumRound = 8;        // partial rows summed per round by the gate finishes
 
 enum LayerFin { LFIN_VALUES = 0, LFIN_COMBINE = 1 };
 
@@ -83,6 +92,7 @@ struct LayerWs {
   uint64_t* partial;     // [slot][3 (h/128)(m/128) parts][128] tagged
   uint64_t* down_xh;     // [slot][m] tagged
   uint64_t* yslot;       // [slot][h] tagged
+  uint64_t* gsum;        // [unit][token][m / 128][2][group][128] tagged: the last units' group sums
   size_t bytes;
 };
 
@@ -178,16 +188,21 @@ struct Items {
   int D;      // down parts per unit: HB * MB
   int R;      // router items
   int S;      // router slices per expert
+  int NG;     // group sums per gate/up column block of the last unit (0: none)
   int route;
 };
-enum ItemKind { IT_GU = 0, IT_DOWN = 1, IT_ROUTER = 2, IT_GF = 3, IT_DF = 4, IT_NONE = 5 };
+enum ItemKind { IT_GU = 0, IT_DOWN = 1, IT_ROUTER = 2, IT_GF = 3, IT_DF = 4, IT_NONE = 5, IT_GS = 6 };
 struct Item {
   int kind, u, a, b, c;  // GU: a = output block, b = projection, c = part; DOWN: a = output block,
-                         // c = part (input block); GF / DF: a = block; ROUTER: a = item
+                         // c = part (input block); GF / DF: a = block; GS: a = block, b = group;
+                         // ROUTER: a = item
 };
 // The list: [router R], then phase A, then phase B.
 //   phase A: for the units 0..U-1, block b = GU(b), followed for b >= kLagG by GF(b - kLagG);
-//            then GF of the last units
+//            then GF of the last kLagG units, each unit's GF preceded by its group sums GS (their
+//            parts are the list's last gate/up items, so their finishes head the launch's final
+//            dependency chain: GS items sum the parts' rounds in parallel, and the GF then sums the
+//            group sums in one round instead of HB / 8 rounds in sequence)
 //   phase B: for the units 0..U-1, block b = D(b), followed for b >= kLagD by DF(b - kLagD);
 //            then DF of the last units
 // Unit 0 (the shared expert when routing) needs no plan, so its gate/up parts run beside the
@@ -197,7 +212,7 @@ constexpr int kLagG = 2, kLagD = 3;
 // items that need no plan (the positions of GU(0) do not depend on the unit count)
 __device__ __forceinline__ int pre_items(const Items& L) { return L.route ? L.R + L.G : 0; }
 __device__ __forceinline__ int list_len(const Items& L, int U) {
-  return (L.route ? L.R : 0) + U * (L.G + L.MB) + U * (L.D + L.HB);
+  return (L.route ? L.R : 0) + U * (L.G + L.MB) + min(U, kLagG) * L.NG * L.MB + U * (L.D + L.HB);
 }
 // position j inside a phase of U blocks of `big` part items, each followed after `lag` blocks by
 // `small` finish items: sets (is_finish, unit, index inside the block); units count from 0
@@ -267,7 +282,21 @@ __device__ __forceinline__ Item item_at(const Items& L, int j, int U) {
   }
   bool fin;
   int unit, r;
-  const int lenA = U * (L.G + L.MB);
+  const int lenA = U * (L.G + L.MB), NU = min(U, kLagG), NGS = L.NG * L.MB, tailA = lenA - NU * L.MB;
+  if (j >= tailA && j < lenA + NU * NGS) {
+    // per unit of the last NU: its group sums (block-major), then its gate finishes
+    const int t = j - tailA, k = t / (NGS + L.MB), q = t - k * (NGS + L.MB);
+    it.u = U - NU + k;
+    if (q < NGS) {
+      it.kind = IT_GS;
+      it.a = q / L.NG;
+      it.b = q - it.a * L.NG;
+    } else {
+      it.kind = IT_GF;
+      it.a = q - NGS;
+    }
+    return it;
+  }
   if (j < lenA) {
     phase_at(j, U, L.G, L.MB, kLagG, fin, unit, r);
     if (fin) {
@@ -279,7 +308,7 @@ __device__ __forceinline__ Item item_at(const Items& L, int j, int U) {
     }
     return it;
   }
-  j -= lenA;
+  j -= lenA + NU * NGS;
   if (j < U * (L.D + L.HB)) {
     phase_at(j, U, L.D, L.HB, kLagD, fin, unit, r);
     if (fin) {
@@ -417,7 +446,7 @@ __device__ __forceinline__ void stage_in(const LayerArgs& a, const UnitInfo& ui,
 #pragma unroll
       for (int t = 0; t < NT; t++) {
         if (t < ui.ntok) {
-          const f32x2 hv = ld_tag_pair(a, a.w.down_xh + (int64_t)ui.slot(t) * a.m + 128 * it.c + 2 * lane, tag);
+          const f32x2 hv = ld_tag_pair<MOE_LAYER_WAIT>(a, a.w.down_xh + (int64_t)ui.slot(t) * a.m + 128 * it.c + 2 * lane, tag);
           v0[t] = hv.x;
           v1[t] = hv.y;
         }
@@ -583,27 +612,61 @@ __device__ __forceinline__ void sum_parts(const LayerArgs& a, const uint64_t* co
         const int k = K == 1 ? 0 : (lane >> 5) % K;
         const uint64_t* q = p[k] + (int64_t)min(i0 + (lane & 31) % B, n - 1) * 128 + (lane * 37 + 11) % 128;
         if (__all(has_tag(ld_tag(q), tag))) break;
-        if (!keep_waiting(a, spins)) {
+        if (!keep_waiting<MOE_LAYER_WAIT>(a, spins)) {
           live = false;
           break;
         }
       }
       if (!live) break;
     }
+    // a round's parts are summed on their own, then added: the sum of a round of kSumRound parts
+    // is the same float whether this wave forms it or a group-sum item does
 #pragma unroll
-    for (int k = 0; k < K; k++)
+    for (int k = 0; k < K; k++) {
+      float rx = 0.0f, ry = 0.0f;
 #pragma unroll
       for (int i = 0; i < B; i++) {
         if (i0 + i < n) {
-          s[k].x += tag_value(w[k][i][0]);
-          s[k].y += tag_value(w[k][i][1]);
+          rx += tag_value(w[k][i][0]);
+          ry += tag_value(w[k][i][1]);
         }
       }
+      s[k].x += rx;
+      s[k].y += ry;
+    }
   }
 }
 
-// gate finish of column block ob of unit ui: the down input of each of its tokens
-__device__ void gate_finish(const LayerArgs& a, const UnitInfo& ui, int ob, uint32_t tag, const Items& L) {
+// Group sum g of projection k, column block ob, token t of grouped unit gi (0: the first of the
+// last kLagG units): 128 tagged words; the groups of one (gi, t, ob, k) are consecutive.
+__device__ __forceinline__ uint64_t* group_ptr(const LayerArgs& a, const Items& L, int gi, int t, int ob, int k,
+                                               int g) {
+  return a.w.gsum + (((((int64_t)gi * kMaxRows + t) * L.MB + ob) * 2 + k) * L.NG + g) * 128;
+}
+
+// Group sum g of column block ob of grouped unit gi (unit ui): its gate and up parts of round g,
+// summed as a gate finish sums one round, for each token.
+__device__ void group_sum(const LayerArgs& a, const UnitInfo& ui, int gi, int ob, int g, uint32_t tag,
+                          const Items& L) {
+  const int lane = cold_lane();
+  const int i0 = g * kSumRound, n = min(kSumRound, L.HB - i0);
+  for (int t = 0; t < ui.ntok; t++) {
+    const int s = ui.slot(t);
+    const uint64_t* rows[2] = {part_ptr(a, s, (0 * L.MB + ob) * L.HB + i0), part_ptr(a, s, (1 * L.MB + ob) * L.HB + i0)};
+    f32x2 gu[2];
+    sum_parts<2, kSumRound>(a, rows, n, tag, gu);
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+      uint64_t* dst = group_ptr(a, L, gi, t, ob, k, g) + 2 * lane;
+      st_tag(dst, gu[k].x, tag);
+      st_tag(dst + 1, gu[k].y, tag);
+    }
+  }
+}
+
+// gate finish of column block ob of unit ui: the down input of each of its tokens (gi >= 0: grouped
+// unit gi, whose rounds were summed by its group-sum items)
+__device__ void gate_finish(const LayerArgs& a, const UnitInfo& ui, int ob, uint32_t tag, const Items& L, int gi) {
   const int lane = cold_lane();
   const int col = ob * 128 + 2 * lane;
   const int64_t si = (int64_t)ui.e * a.m + col;
@@ -616,7 +679,13 @@ __device__ void gate_finish(const LayerArgs& a, const UnitInfo& ui, int ob, uint
     const int s = ui.slot(t);
     const uint64_t* rows[2] = {part_ptr(a, s, (0 * L.MB + ob) * L.HB), part_ptr(a, s, (1 * L.MB + ob) * L.HB)};
     f32x2 gu[2];
-    sum_parts<2, 8>(a, rows, L.HB, tag, gu);
+    if (gi >= 0) {
+      // the group sums of the unit's HB / kSumRound rounds, in one round
+      const uint64_t* gs[2] = {group_ptr(a, L, gi, t, ob, 0, 0), group_ptr(a, L, gi, t, ob, 1, 0)};
+      sum_parts<2, kSumRound>(a, gs, L.NG, tag, gu);
+    } else {
+      sum_parts<2, kSumRound>(a, rows, L.HB, tag, gu);
+    }
     float g0 = gu[0].x, g1 = gu[0].y, u0 = gu[1].x, u1 = gu[1].y;
     hadamard128_wave(g0, g1);
     hadamard128_wave(u0, u1);
@@ -656,7 +725,7 @@ __device__ void combine_block(const LayerArgs& a, int ob, uint32_t tag, const fl
         for (;;) {
           const uint64_t* q = a.w.yslot + (int64_t)(r * kSlots + lane % kSlots) * a.h + col;
           if (__all(has_tag(ld_tag(q), tag))) break;
-          if (!keep_waiting(a, spins)) {
+          if (!keep_waiting<MOE_LAYER_WAIT>(a, spins)) {
             live = false;
             break;
           }
@@ -759,6 +828,8 @@ __global__ __launch_bounds__(kLW * 64) void k4_layer_kernel(LayerArgs a) {
   L.G = 2 * L.MB * L.HB;
   L.D = L.HB * L.MB;
   L.S = a.h / kRouterSlice;
+  // group sums for the last kLagG units when their gate finishes then take one round (HB <= 8 kSumRound)
+  L.NG = MOE_LAYER_GS && (L.HB + kSumRound - 1) / kSumRound <= kSumRound ? (L.HB + kSumRound - 1) / kSumRound : 0;
   L.R = a.route ? 256 * L.S : 0;
   L.route = a.route;
   const int pre = pre_items(L);
@@ -955,7 +1026,10 @@ __global__ __launch_bounds__(kLW * 64) void k4_layer_kernel(LayerArgs a) {
     if (it.kind == IT_ROUTER) {
       router_item(a, it.a, L.S, tag);
     } else if (it.kind == IT_GF) {
-      gate_finish(a, unit_of(it.u), it.a, tag, L);
+      const int gi = it.u - (U - min(U, kLagG));
+      gate_finish(a, unit_of(it.u), it.a, tag, L, L.NG > 0 ? gi : -1);
+    } else if (it.kind == IT_GS) {
+      group_sum(a, unit_of(it.u), it.u - (U - min(U, kLagG)), it.a, it.b, tag, L);
     } else if (it.kind == IT_DF) {
       down_finish(a, unit_of(it.u), it.a, it.u == U - 1, tag, L, score);
     }
@@ -995,6 +1069,7 @@ LayerWs layer_carve(void* base, int h, int m) {
   w.partial = reinterpret_cast<uint64_t*>(take((size_t)kMaxUnits * 3 * HB * MB * 128 * 8));
   w.down_xh = reinterpret_cast<uint64_t*>(take((size_t)kMaxUnits * m * 8));
   w.yslot = reinterpret_cast<uint64_t*>(take((size_t)kMaxUnits * h * 8));
+  w.gsum = reinterpret_cast<uint64_t*>(take((size_t)kLagG * kMaxRows * MB * 2 * kSumRound * 128 * 8));
   w.bytes = off;
   return w;
 }

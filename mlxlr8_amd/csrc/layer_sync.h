@@ -76,11 +76,11 @@ __device__ __forceinline__ bool keep_waiting(const A& a, int& spins) {
   return true;
 }
 // the lane's two words p[0], p[1] (a column pair) once both carry `tag`
-template <class A>
+template <int kMaxPauses = 64, class A>
 __device__ __forceinline__ f32x2 ld_tag_pair(const A& a, const uint64_t* p, uint32_t tag) {
   uint64_t w0 = ld_tag(p), w1 = ld_tag(p + 1);
   int spins = 0;
-  while (!__all(has_tag(w0, tag) && has_tag(w1, tag)) && keep_waiting(a, spins)) {
+  while (!__all(has_tag(w0, tag) && has_tag(w1, tag)) && keep_waiting<kMaxPauses>(a, spins)) {
     w0 = ld_tag(p);
     w1 = ld_tag(p + 1);
   }
