@@ -874,12 +874,23 @@ __global__ __launch_bounds__(kLW * 64) void k4_layer_kernel(LayerArgs a) {
   }
   const float* score = a.route ? plan_t.score : a.scores;
   auto unit_of = [&](int u) { return (u == 0 && a.route) ? shared_ui : unit_info(plan_t, u, a.experts, a.rows); };
-  // the item at sub-list position `sub`, if it is known without waiting (kind NONE otherwise)
+  // the item at sub-list position `sub`, if it is known without waiting (kind NONE otherwise); a
+  // wave without the plan takes the block's table once it is complete in LDS, so a run of parts
+  // goes on from the shared expert's parts into the routed ones without leaving its load pipeline
   auto resolve = [&](int sub, Item& it) {
     const int j = sub * kXcds + xcd;
     it = Item{IT_NONE, 0, 0, 0, 0};
-    if (j < pre) it = item_at(L, j, 1);
-    else if (have_plan && j < list_len(L, units)) it = item_at(L, j, units);
+    if (j < pre) {
+      it = item_at(L, j, 1);
+      return;
+    }
+    if (!have_plan &&
+        __builtin_amdgcn_readfirstlane(__hip_atomic_load(&route_state, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) == 2) {
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+      units = min(max(__builtin_amdgcn_readfirstlane(plan_t.units), 1), kMaxUnits);
+      have_plan = true;
+    }
+    if (have_plan && j < list_len(L, units)) it = item_at(L, j, units);
   };
 
   // A run of part items: pc / in hold the first item's quad 0 and input block on entry.  Each item
