@@ -74,6 +74,9 @@ namespace moe {
 #ifndef MOE_LAYER_WAIT
 #define MOE_LAYER_WAIT 16
 #endif
+#ifndef MOE_LAYER_PRIO_UNITS
+#define MOE_LAYER_PRIO_UNITS 2
+#endif
 #ifndef MOE_LAYER_GS
 #define MOE_LAYER_GS 1
 #endif
@@ -907,9 +910,9 @@ __global__ __launch_bounds__(kLW * 64) void k4_layer_kernel(LayerArgs a) {
       __builtin_amdgcn_s_setprio(2);
       float scale[NT];
       stage_in<NT, kDPre>(a, ui, it, in, tag, xw, scale);
-      // the last unit's parts head the launch's final dependency chain (its gate finishes, its
+      // the last units' parts head the launch's final dependency chain (their gate finishes, their
       // down parts, the combine): they get issue priority over the other decoding waves
-      if (have_plan && it.u == units - 1)
+      if (have_plan && it.u >= units - MOE_LAYER_PRIO_UNITS)
         __builtin_amdgcn_s_setprio(1);
       else
         __builtin_amdgcn_s_setprio(0);
