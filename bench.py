@@ -216,7 +216,7 @@ def main():
         "hbm_frac": round(hbm / HBM_PEAK_GBPS, 4),
         "bytes_per_token": BYTES_TOKEN,
         "kernels_us": {"k4_layer_kernel": round(layer_us, 2)},
-        "roofline": {"kernel": "k4_layer_kernel<1> (router, top-8, shared and routed gate/up and down decode "
+        "roofline": {"kernel": "k4_layer_kernel<1, false> (router, top-8, shared and routed gate/up and down decode "
                                "GEMVs, finishes and combine in one persistent launch)",
                      "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
@@ -326,7 +326,7 @@ def bench_k4_verify(args):
                       "8-token speculative-verify batch through the K4-trellis MoE layer (correlated rows, "
                       "distinct experts streamed once)",
                       {"global_batch": 8, "seq_len": 1, "distinct_experts": U, "layers_rotated": len(layers)},
-                      algo, "k4_layer_kernel<8>: router, the distinct experts' projections and the combine in one launch"),
+                      algo, "k4_layer_kernel<8, false>: router, the distinct experts' projections and the combine in one launch"),
                 us_per_step=round(ms * 1e3, 2))
 
 

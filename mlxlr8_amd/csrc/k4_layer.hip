@@ -118,6 +118,14 @@ struct LayerArgs {
   int fin;
   uint16_t* out;             // combine [rows, h]
   uint16_t* values;          // values [slots, h]
+  // one row, norm_x set: the launch first forms the layer's residual add + RMSNorm itself,
+  // h = T(norm_x + norm_res) into h_row (= residual) and the normalised row into x_row (= x)
+  const uint16_t* norm_x;
+  const uint16_t* norm_res;
+  const uint16_t* norm_w;
+  float eps;
+  uint16_t* h_row;
+  uint16_t* x_row;
   LayerWs w;
 };
 
@@ -791,29 +799,43 @@ __device__ void down_finish(const LayerArgs& a, const UnitInfo& ui, int ob, bool
 // every load is issued (unconditionally, index clamped: a load under a branch is waited for
 // before the next) before the first store.
 template <int BYTES, int SHARES>
-__device__ __forceinline__ void copy_table_share(uint8_t* lds, const void* table, int k) {
-  const u32x4* src = reinterpret_cast<const u32x4*>(table);
-  u32x4* dst = reinterpret_cast<u32x4*>(lds);
-  constexpr int n = BYTES / 16;
-  constexpr int per = ((n + SHARES - 1) / SHARES + 63) & ~63;
-  constexpr int kLoads = per / 64;
-  const int lane = lane_id();
-  const int lo = k * per, hi = min(n, lo + per);
-  // every block walks the table from its own 1 KB offset: all CUs reading the same lines at the
-  // same time would queue on the same L2 channels
-  const int rot = ((int)blockIdx.x * 97 * 64) & (n - 1);
+struct TableShare {
+  static constexpr int n = BYTES / 16;
+  static constexpr int per = ((n + SHARES - 1) / SHARES + 63) & ~63;
+  static constexpr int kLoads = per / 64;
   u32x4 v[kLoads];
+};
+// The share's loads (issue) and its LDS stores (commit): every block walks the table from its own
+// 1 KB offset, since all CUs reading the same lines at the same time would queue on the same L2
+// channels
+template <int BYTES, int SHARES>
+__device__ __forceinline__ void copy_table_issue(TableShare<BYTES, SHARES>& t, const void* table, int k) {
+  using T = TableShare<BYTES, SHARES>;
+  const u32x4* src = reinterpret_cast<const u32x4*>(table);
+  const int lane = lane_id();
+  const int lo = k * T::per, hi = min(T::n, lo + T::per);
+  const int rot = ((int)blockIdx.x * 97 * 64) & (T::n - 1);
 #pragma unroll
-  for (int j = 0; j < kLoads; j++) v[j] = src[(min(lo + 64 * j + lane, hi - 1) + rot) & (n - 1)];
+  for (int j = 0; j < T::kLoads; j++) t.v[j] = src[(min(lo + 64 * j + lane, hi - 1) + rot) & (T::n - 1)];
+}
+template <int BYTES, int SHARES>
+__device__ __forceinline__ void copy_table_commit(const TableShare<BYTES, SHARES>& t, uint8_t* lds, int k) {
+  using T = TableShare<BYTES, SHARES>;
+  u32x4* dst = reinterpret_cast<u32x4*>(lds);
+  const int lane = lane_id();
+  const int lo = k * T::per, hi = min(T::n, lo + T::per);
+  const int rot = ((int)blockIdx.x * 97 * 64) & (T::n - 1);
 #pragma unroll
-  for (int j = 0; j < kLoads; j++) {
+  for (int j = 0; j < T::kLoads; j++) {
     const int i = lo + 64 * j + lane;
-    if (i < hi) dst[(i + rot) & (n - 1)] = v[j];
+    if (i < hi) dst[(i + rot) & (T::n - 1)] = t.v[j];
   }
 }
 
 // ---------------------------------------------------------------- the kernel
-template <int NT>
+// NORM (one row): the launch first forms the layer's residual add + RMSNorm (a separate
+// instantiation, so that the plain one keeps its start unchanged)
+template <int NT, bool NORM>
 __global__ __launch_bounds__(kLW * 64) void k4_layer_kernel(LayerArgs a) {
   constexpr bool kDPre = NT == 1;  // down inputs fetched ahead (registers allow it for one token)
   __shared__ __attribute__((aligned(16))) uint8_t tab[LTable<NT>::kBytes];
@@ -953,10 +975,40 @@ __global__ __launch_bounds__(kLW * 64) void k4_layer_kernel(LayerArgs a) {
     epoch_lds = (uint32_t)ld_coh_i(a.w.flags + LF_EPOCH);
     route_state = 0;
   }
-  if (LTable<NT>::kF16)
-    copy_table_share<131072, kLW>(tab, a.tab16, wv);
-  else
-    copy_table_share<65536, kLW>(tab, a.tab8, wv);
+  // The layer's residual add + RMSNorm (one row): waves 0..3 form the row's square sums exactly as
+  // the norm kernel's four waves do, and after the block meets write h and the normalised row;
+  // every block writes the same bits, so each block reads values its own stores put in its L2.
+  // The norm's loads go out first, the table's next; the block meets once the row's sums are in,
+  // then waves 0..3 store the rows while every wave writes its table share into LDS.
+  if constexpr (NORM) {
+    __shared__ float norm_red[4];
+    rms_u32x4 nh[4], nw[4];
+    float nss = 0.0f;
+    if (wv < 4) nss = rms_row_sum<4>(a.norm_x, a.norm_res, a.norm_w, a.h / 2048, (int)threadIdx.x, nh, nw, nullptr);
+    TableShare<LTable<NT>::kBytes, kLW> share;
+    copy_table_issue(share, LTable<NT>::kF16 ? (const void*)a.tab16 : (const void*)a.tab8, wv);
+    if (wv < 4) {
+      nss = wave_sum(nss);
+      if (lane_id() == 63) norm_red[wv] = nss;
+    }
+    __syncthreads();
+    if (wv < 4) {
+      const int K = a.h / 2048, t = (int)threadIdx.x;
+#pragma unroll
+      for (int k = 0; k < 4; k++)
+        if (k < K) *reinterpret_cast<rms_u32x4*>(a.h_row + k * 2048 + t * 8) = nh[k];
+      rms_row_store<4>(nh, nw, K, t, rms_inv(norm_red, a.h, a.eps), a.x_row);
+    }
+    copy_table_commit(share, tab, wv);
+  } else if (LTable<NT>::kF16) {
+    TableShare<131072, kLW> share;
+    copy_table_issue(share, a.tab16, wv);
+    copy_table_commit(share, tab, wv);
+  } else {
+    TableShare<65536, kLW> share;
+    copy_table_issue(share, a.tab8, wv);
+    copy_table_commit(share, tab, wv);
+  }
   __syncthreads();
   epoch = (uint32_t)__builtin_amdgcn_readfirstlane((int)epoch_lds);
   tag = epoch + 1u;
@@ -1120,10 +1172,12 @@ static int k4_layer_launch(LayerArgs a, void* workspace, hipStream_t s) {
   a.tab16 = codebook_f16_device_table();
   if (!a.tab8 || !a.tab16) return fail(MOE_ENOTSUP, "code tables are not initialised on this device");
   const int grid = device_cus();
-  if (a.rows <= 1)
-    hipLaunchKernelGGL(k4_layer_kernel<1>, dim3(grid), dim3(kLW * 64), 0, s, a);
+  if (a.rows <= 1 && a.norm_x)
+    hipLaunchKernelGGL((k4_layer_kernel<1, true>), dim3(grid), dim3(kLW * 64), 0, s, a);
+  else if (a.rows <= 1)
+    hipLaunchKernelGGL((k4_layer_kernel<1, false>), dim3(grid), dim3(kLW * 64), 0, s, a);
   else
-    hipLaunchKernelGGL(k4_layer_kernel<kMaxRows>, dim3(grid), dim3(kLW * 64), 0, s, a);
+    hipLaunchKernelGGL((k4_layer_kernel<kMaxRows, false>), dim3(grid), dim3(kLW * 64), 0, s, a);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail((int)e, "launch of the fused K4 block failed: %s", hipGetErrorString(e));
   return MOE_OK;
@@ -1132,7 +1186,7 @@ static int k4_layer_launch(LayerArgs a, void* workspace, hipStream_t s) {
 int k4_layer_run(const uint16_t* x, const uint16_t* residual, int rows, int route, const float* router_w,
                  const float* bias, uint32_t* ids, float* scores, const uint8_t* const packed[3],
                  const uint16_t* const in_scale[3], const uint16_t* const out_scale[3], int h, int m, int experts,
-                 int combine, uint16_t* out, uint16_t* values, void* layer_ws, hipStream_t s) {
+                 int combine, uint16_t* out, uint16_t* values, void* layer_ws, hipStream_t s, const LayerNorm* norm) {
   if (!k4_layer_supported(h, m, route != 0))
     return fail(MOE_ENOTSUP, "the fused K4 block needs hidden a multiple of %d%s and intermediate a multiple of 128 "
                 "(got %d, %d)", route ? kRouterSlice : 128, route ? " up to 8192 (fused router)" : "", h, m);
@@ -1158,6 +1212,17 @@ int k4_layer_run(const uint16_t* x, const uint16_t* residual, int rows, int rout
   a.fin = combine ? LFIN_COMBINE : LFIN_VALUES;
   a.out = out;
   a.values = values;
+  if (norm) {
+    // x and residual are then the launch's outputs: the normalised row and h
+    if (rows != 1 || !route || !norm->x || !norm->w || h % 2048 || h > 8192)
+      return fail(MOE_EINVAL, "the fused residual + RMSNorm takes one routed row of width a multiple of 2048 up to 8192");
+    a.norm_x = norm->x;
+    a.norm_res = norm->residual;
+    a.norm_w = norm->w;
+    a.eps = norm->eps;
+    a.h_row = const_cast<uint16_t*>(residual);
+    a.x_row = const_cast<uint16_t*>(x);
+  }
   return k4_layer_launch(a, layer_ws, s);
 }
 

@@ -31,6 +31,10 @@
 #include "moe_plan.h"
 #include "route.h"
 
+#ifndef MOE_FOLD_NORM
+#define MOE_FOLD_NORM 1
+#endif
+
 namespace moe {
 
 __device__ uint8_t g_codebook_e4m3[65536];
@@ -993,8 +997,12 @@ static int k4_block(const uint16_t* x, const uint16_t* attn, const uint16_t* nor
   const uint16_t* xin = x;
   const uint16_t* res = residual;
   prof_mark(0, s);
+  // one row: the residual add + RMSNorm runs at the start of the fused block (same bits as the
+  // norm kernel); more rows: the norm kernel first
+  LayerNorm ln{x, attn, norm_w, eps};
+  const bool fold = MOE_FOLD_NORM && norm_w && rows == 1 && h % 2048 == 0;
   if (norm_w) {
-    if ((rc = moe_residual_rmsnorm(x, attn, norm_w, rows, h, eps, w.hrow, w.xnrow, (moe_stream_t)s))) return rc;
+    if (!fold && (rc = moe_residual_rmsnorm(x, attn, norm_w, rows, h, eps, w.hrow, w.xnrow, (moe_stream_t)s))) return rc;
     xin = w.xnrow;
     res = w.hrow;
   }
@@ -1003,7 +1011,7 @@ static int k4_block(const uint16_t* x, const uint16_t* attn, const uint16_t* nor
   const uint16_t* outs[3] = {out_g, out_u, out_d};
   prof_mark(1, s);
   rc = k4_layer_run(xin, res, rows, 1, router_w, bias, ids, sc, packed, ins, outs, h, m, 257, 1, out, nullptr,
-                    w.layer, s);
+                    w.layer, s, fold ? &ln : nullptr);
   prof_mark(3, s);
   return rc;
 }

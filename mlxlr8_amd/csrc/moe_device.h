@@ -30,6 +30,69 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
   return (uint16_t)(u >> 16);
 }
 __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+// ---------------------------------------------------------------- residual add + RMSNorm, one row
+// (exlr8/fast_norm.py:20-28, exlr8/metal/residual_rms.metal:18-90)
+//   h = T(x + residual), out = T(w * T(h * rsqrt(mean(h^2) + eps))), T = bf16, mean in fp32.
+// Thread t of 256 owns elements 2048 k + 8 t .. + 7 for k < K; its square sum runs over them in
+// that order.  The norm kernel and the fused K4 block both use these two steps, so their rows
+// are the same bits.
+typedef uint32_t rms_u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint32_t pack_bf16_pair(float a, float b) {
+  return (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
+}
+template <int KMAX>
+__device__ __forceinline__ float rms_row_sum(const uint16_t* __restrict__ x, const uint16_t* __restrict__ residual,
+                                             const uint16_t* __restrict__ w, int K, int t,
+                                             rms_u32x4 (&hv)[KMAX], rms_u32x4 (&wv)[KMAX],
+                                             uint16_t* __restrict__ h_out) {
+  // the weight row depends on nothing: its loads go out with the activations' (one round trip)
+#pragma unroll
+  for (int k = 0; k < KMAX; k++)
+    if (k < K) wv[k] = *reinterpret_cast<const rms_u32x4*>(w + k * 2048 + t * 8);
+  float ss = 0.0f;
+#pragma unroll
+  for (int k = 0; k < KMAX; k++) {
+    if (k < K) {
+      const int off = k * 2048 + t * 8;
+      const rms_u32x4 xv = *reinterpret_cast<const rms_u32x4*>(x + off);
+      rms_u32x4 rv = rms_u32x4{0, 0, 0, 0};
+      if (residual) rv = *reinterpret_cast<const rms_u32x4*>(residual + off);
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const float a = round_bf16(bf16_to_f32((uint16_t)(xv[j] & 0xFFFFu)) + bf16_to_f32((uint16_t)(rv[j] & 0xFFFFu)));
+        const float b = round_bf16(bf16_to_f32((uint16_t)(xv[j] >> 16)) + bf16_to_f32((uint16_t)(rv[j] >> 16)));
+        ss = fmaf(a, a, ss);
+        ss = fmaf(b, b, ss);
+        hv[k][j] = pack_bf16_pair(a, b);
+      }
+      if (h_out) *reinterpret_cast<rms_u32x4*>(h_out + off) = hv[k];
+    }
+  }
+  return ss;
+}
+// the four waves' sums red[0..3] -> 1 / rms
+__device__ __forceinline__ float rms_inv(const float* red, int n, float eps) {
+  const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+  return 1.0f / sqrtf(tot / (float)n + eps);
+}
+template <int KMAX>
+__device__ __forceinline__ void rms_row_store(const rms_u32x4 (&hv)[KMAX], const rms_u32x4 (&wv)[KMAX], int K, int t,
+                                              float inv, uint16_t* __restrict__ out) {
+#pragma unroll
+  for (int k = 0; k < KMAX; k++) {
+    if (k < K) {
+      rms_u32x4 o;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const float hl = bf16_to_f32((uint16_t)(hv[k][j] & 0xFFFFu)), hh = bf16_to_f32((uint16_t)(hv[k][j] >> 16));
+        const float wl = bf16_to_f32((uint16_t)(wv[k][j] & 0xFFFFu)), wh = bf16_to_f32((uint16_t)(wv[k][j] >> 16));
+        o[j] = pack_bf16_pair(round_bf16(wl * round_bf16(hl * inv)), round_bf16(wh * round_bf16(hh * inv)));
+      }
+      *reinterpret_cast<rms_u32x4*>(out + k * 2048 + t * 8) = o;
+    }
+  }
+}
 __device__ __forceinline__ float f16_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 
 // ---------------------------------------------------------------- weight stream loads

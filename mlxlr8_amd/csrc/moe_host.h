@@ -36,10 +36,20 @@ size_t k4_layer_workspace_bytes(int h, int m);
 bool k4_layer_supported(int h, int m, bool route);
 int k4_layer_check_alignment(const uint16_t* x, const uint16_t* residual, const uint16_t* const in_scale[3],
                              const uint16_t* const out_scale[3], const uint16_t* out, const uint16_t* values);
+// The layer's residual add + RMSNorm folded into a one-row fused K4 launch (exlr8/fast_norm.py:20-28):
+// h = T(x + residual) is written to the launch's residual argument and the normalised row to its
+// x argument before either is read.
+struct LayerNorm {
+  const uint16_t* x;
+  const uint16_t* residual;  // may be null (h = x)
+  const uint16_t* w;
+  float eps;
+};
 int k4_layer_run(const uint16_t* x, const uint16_t* residual, int rows, int route, const float* router_w,
                  const float* bias, uint32_t* ids, float* scores, const uint8_t* const packed[3],
                  const uint16_t* const in_scale[3], const uint16_t* const out_scale[3], int h, int m, int experts,
-                 int combine, uint16_t* out, uint16_t* values, void* layer_ws, hipStream_t s);
+                 int combine, uint16_t* out, uint16_t* values, void* layer_ws, hipStream_t s,
+                 const LayerNorm* norm = nullptr);
 // The layer workspace's plan (where a plan kernel writes it for route = 0).
 Plan* k4_layer_plan(void* layer_ws);
 

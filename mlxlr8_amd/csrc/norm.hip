@@ -9,14 +9,6 @@
 namespace moe {
 namespace {
 
-typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ float lo_bf16(uint32_t v) { return bf16_to_f32((uint16_t)(v & 0xFFFFu)); }
-__device__ __forceinline__ float hi_bf16(uint32_t v) { return bf16_to_f32((uint16_t)(v >> 16)); }
-__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
-  return (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
-}
-
 // block of 256 threads; n = 2048 * k for k <= 4 (8 elements per thread per 2048)
 template <int K>
 __global__ __launch_bounds__(256) void residual_rmsnorm_kernel(const uint16_t* __restrict__ x,
@@ -26,44 +18,13 @@ __global__ __launch_bounds__(256) void residual_rmsnorm_kernel(const uint16_t* _
                                                                uint16_t* __restrict__ out) {
   __shared__ float red[4];
   const int64_t row = blockIdx.x;
-  // the weight row depends on nothing: its loads go out with the activations' (one round trip)
-  u32x4v wv[K];
-#pragma unroll
-  for (int k = 0; k < K; k++) wv[k] = *reinterpret_cast<const u32x4v*>(w + k * 2048 + threadIdx.x * 8);
-  u32x4v hv[K];
-  float ss = 0.0f;
-#pragma unroll
-  for (int k = 0; k < K; k++) {
-    const int64_t off = row * n + k * 2048 + threadIdx.x * 8;
-    const u32x4v xv = *reinterpret_cast<const u32x4v*>(x + off);
-    u32x4v rv = u32x4v{0, 0, 0, 0};
-    if (residual) rv = *reinterpret_cast<const u32x4v*>(residual + off);
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const float a = round_bf16(lo_bf16(xv[j]) + lo_bf16(rv[j]));
-      const float b = round_bf16(hi_bf16(xv[j]) + hi_bf16(rv[j]));
-      ss = fmaf(a, a, ss);
-      ss = fmaf(b, b, ss);
-      hv[k][j] = pack_bf16(a, b);
-    }
-    if (h_out) *reinterpret_cast<u32x4v*>(h_out + off) = hv[k];
-  }
+  rms_u32x4 hv[K], wv[K];
+  float ss = rms_row_sum<K>(x + row * n, residual ? residual + row * n : nullptr, w, K, (int)threadIdx.x, hv, wv,
+                            h_out ? h_out + row * n : nullptr);
   ss = wave_sum(ss);
   if (lane_id() == 63) red[wave_id_in_block()] = ss;
   __syncthreads();
-  const float tot = (red[0] + red[1]) + (red[2] + red[3]);
-  const float inv = 1.0f / sqrtf(tot / (float)n + eps);
-#pragma unroll
-  for (int k = 0; k < K; k++) {
-    const int64_t off = row * n + k * 2048 + threadIdx.x * 8;
-    u32x4v o;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      o[j] = pack_bf16(round_bf16(lo_bf16(wv[k][j]) * round_bf16(lo_bf16(hv[k][j]) * inv)),
-                       round_bf16(hi_bf16(wv[k][j]) * round_bf16(hi_bf16(hv[k][j]) * inv)));
-    }
-    *reinterpret_cast<u32x4v*>(out + off) = o;
-  }
+  rms_row_store<K>(hv, wv, K, (int)threadIdx.x, rms_inv(red, n, eps), out + row * n);
 }
 
 }  // namespace
