@@ -136,3 +136,27 @@ def test_layer_stack_glm(cuda, orc):
         h = out
     stacked = DecoderMoEStack(mods)(x)
     assert torch.equal(stacked.view(torch.int16), h.view(torch.int16))
+
+
+@pytest.mark.parametrize("with_attn", [True, False])
+def test_one_row_layer_folds_norm_bit_exact(cuda, with_attn):
+    """One GLM row: the layer call forms the residual add + RMSNorm inside the fused block; its
+    outputs equal the norm kernel followed by the plain fused block bit for bit (same per-thread
+    sums and reduction order), over three consecutive calls."""
+    from mlxlr8_amd.norm import residual_rms_pair
+    say(f"case: folded norm vs norm kernel + block, attn={with_attn}")
+    hidden, inter = 6144, 2048
+    experts, w, bias, norm, _, _ = _layer(cuda, 410, hidden, inter)
+    g = torch.Generator(device=cuda)
+    g.manual_seed(411)
+    for step in range(3):
+        x = torch.randn((1, hidden), generator=g, device=cuda).to(torch.bfloat16)
+        attn = torch.randn((1, hidden), generator=g, device=cuda).to(torch.bfloat16) if with_attn else None
+        out, ids, scores = experts.layer_decode(x, norm, w, bias, attn=attn)
+        h, xn = residual_rms_pair(x, attn, norm)
+        call = experts.prepare_decode(xn, h, w, bias)
+        ref = call.run()
+        torch.cuda.synchronize()
+        assert torch.equal(ids, call.ids), f"step {step}: routing differs"
+        assert torch.equal(scores, call.scores), f"step {step}: scores differ"
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), f"step {step}: outputs differ"
