@@ -129,6 +129,8 @@ int moe_residual_rmsnorm(const uint16_t* x, const uint16_t* residual, const uint
 /* One decode layer's MoE half with its input norm: h = T(x + attn) (attn may be NULL: h = x),
  * xn = RMSNorm(h) (norm_w [h] bf16, eps), then the routed MoE block on xn with residual h:
  * out = T(h + r).  Shapes and side vectors as moe_k4_moe_decode; hidden a multiple of 2048 <= 8192.
+ * One row: a single launch (the norm runs at the start of the fused block, same bits as
+ * moe_residual_rmsnorm followed by moe_k4_moe_decode); more rows: the norm kernel, then the block.
  * Replaces: exlr8/model.py:382-418 (h = x + r; x = rms_norm(h, post_norm); MoE branch), the
  * layer body of a stack with no attention output. */
 int moe_k4_layer_decode(const uint16_t* x, const uint16_t* attn, const uint16_t* norm_w, float eps, int rows,
