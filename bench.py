@@ -36,7 +36,7 @@ sys.path.insert(0, str(ROOT))
 H, M, E = 6144, 2048, 257
 TRELLIS = H * M // 2                      # bytes per expert projection (K4 = 4 bits/weight)
 # Algorithmic bytes per token (batch 1): 9 experts x 3 projections of trellis + router weight +
-# side vectors + bias + activations in/out ("Measurement").
+# side vectors + bias + activations in/out.
 BYTES_TOKEN = 9 * 3 * TRELLIS + 256 * H * 4 + 9 * 3 * (H + M) * 2 + 256 * 4 + 3 * H * 2
 HBM_PEAK_GBPS = 8000.0
 METRIC = "MoE-layer decode µs/token + HBM GB/s (K4 trellis, b=1); prefill tok/s"
@@ -117,7 +117,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported (this path has no "
-              "multi-GPU collectives; see DESIGN.md for how it would shard)", file=sys.stderr)
+              "multi-GPU collectives: experts would be sharded across GPUs by expert id, one GPU's share per rank)", file=sys.stderr)
         sys.exit(2)
     if args.k4_prefill:
         print(json.dumps(bench_k4_prefill(args)), flush=True)
