@@ -9,7 +9,8 @@ import refmath
 
 def test_codebook_known_answers(orc):
     cb = orc.codebook()
-    # tests/test_trellis.py:63 (reference known answer) and the values listed in the survey crib
+    # tests/test_trellis.py:63 (reference known answer) and further entries of the codebook as
+    # exlr8/trellis.py:22-50 defines it
     assert cb[0] == np.float16(1.875)
     assert cb[1] == np.float16(0.140625) and cb[2] == np.float16(-0.75)
     assert cb[3] == np.float16(0.8125) and cb[65535] == np.float16(0.875)
