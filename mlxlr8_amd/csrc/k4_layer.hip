@@ -219,7 +219,13 @@ struct Item {
 // Unit 0 (the shared expert when routing) needs no plan, so its gate/up parts run beside the
 // router.  A finisher comes kLag units after the parts it sums, so its inputs are normally complete
 // when it is taken; the last unit's down finishes (the combine) close the list.
-constexpr int kLagG = 2, kLagD = 3;
+#ifndef MOE_LAYER_LAG_G
+#define MOE_LAYER_LAG_G 2
+#endif
+#ifndef MOE_LAYER_LAG_D
+#define MOE_LAYER_LAG_D 4
+#endif
+constexpr int kLagG = MOE_LAYER_LAG_G, kLagD = MOE_LAYER_LAG_D;
 // items that need no plan (the positions of GU(0) do not depend on the unit count)
 __device__ __forceinline__ int pre_items(const Items& L) { return L.route ? L.R + L.G : 0; }
 __device__ __forceinline__ int list_len(const Items& L, int U) {
