@@ -34,6 +34,14 @@
 #include "moe_device.h"
 #include "moe_host.h"
 
+// arithmetic pairs per even / odd word of the piece decoder (the rest read the code table)
+#ifndef MOE_KP_ALU_EVEN
+#define MOE_KP_ALU_EVEN 2
+#endif
+#ifndef MOE_KP_ALU_ODD
+#define MOE_KP_ALU_ODD 3
+#endif
+
 namespace moe {
 namespace {
 
@@ -248,9 +256,9 @@ __global__ __launch_bounds__(kKpThreads) void kp_gemm_kernel(KpGemm a) {
         for (int rh = 0; rh < 2; rh++) {
           f16x2 qv[2][4];
           if (rh == 0)
-            decode_pair_words_f16<2, 2>(pc.x, pc.y, prior, tab, qv);
+            decode_pair_words_f16<MOE_KP_ALU_EVEN, MOE_KP_ALU_ODD>(pc.x, pc.y, prior, tab, qv);
           else
-            decode_pair_words_f16<2, 2>(pc.z, pc.w, pc.y, tab, qv);
+            decode_pair_words_f16<MOE_KP_ALU_EVEN, MOE_KP_ALU_ODD>(pc.z, pc.w, pc.y, tab, qv);
           mfmas(ab, rh, frag(qv[0][0], qv[0][1], qv[1][0], qv[1][1]), frag(qv[0][2], qv[0][3], qv[1][2], qv[1][3]));
         }
       } else {
