@@ -77,6 +77,13 @@ namespace moe {
 #ifndef MOE_LAYER_PRIO_UNITS
 #define MOE_LAYER_PRIO_UNITS 2
 #endif
+// arithmetic pairs per even / odd word for batches (E4M3 byte table)
+#ifndef MOE_LAYER8_ALU_EVEN
+#define MOE_LAYER8_ALU_EVEN 1
+#endif
+#ifndef MOE_LAYER8_ALU_ODD
+#define MOE_LAYER8_ALU_ODD 2
+#endif
 #ifndef MOE_LAYER_GS
 #define MOE_LAYER_GS 1
 #endif
@@ -537,7 +544,7 @@ __device__ __forceinline__ void decode_quad(const u32x4 (&pc)[4], int qb, int nt
       if (LTable<NT>::kF16)
         decode_pair_words_f16<MOE_LAYER_ALU_EVEN, MOE_LAYER_ALU_ODD, true>(w0, w1, p0, tab, q);
       else
-        decode_pair_words_f16<1, 2, false>(w0, w1, p0, tab, q);
+        decode_pair_words_f16<MOE_LAYER8_ALU_EVEN, MOE_LAYER8_ALU_ODD, false>(w0, w1, p0, tab, q);
       const f16x8 b0 = frag(q[0][0], q[0][1], q[1][0], q[1][1]);
       const f16x8 b1 = frag(q[0][2], q[0][3], q[1][2], q[1][3]);
       acc[s4][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[rh], b0, acc[s4][0], 0, 0, 0);
