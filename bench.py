@@ -77,10 +77,12 @@ def traffic_from_profiles(name="k4_layer_b1_pmc.txt"):
     return None
 
 
-def cpu_baseline(layer, w, bias, xs, rs, seconds):
+def cpu_baseline(layer, w, bias, xs, rs, seconds, runs=5):
     """The CPU restatement of the reference operator chain, timed on this host: the oracle's C source
     built here with fp32 accumulation and -march=native (OpenMP over all cores); the float64 oracle
-    if that build is not possible."""
+    if that build is not possible.  One warm-up token, then `runs` runs of the same token count
+    (sized so the runs take about `seconds` together); the value is the median run's tokens/s."""
+    import statistics
     import tempfile
 
     import numpy as np
@@ -97,20 +99,33 @@ def cpu_baseline(layer, w, bias, xs, rs, seconds):
           for p, pair in layer["scales"].items()}
     wh, bh = w.cpu().numpy(), bias.cpu().numpy()
     bits = lambda t: t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
-    done, t0 = 0, time.perf_counter()
-    while True:
-        i = done % len(xs)
-        logits = orc.router_logits(bits(xs[i]), wh)
+    xb = [bits(x) for x in xs]
+    rb = [bits(r) for r in rs]
+
+    def token(i):
+        i %= len(xb)
+        logits = orc.router_logits(xb[i], wh)
         ids, scores = orc.route(logits, bh)
-        orc.k4_moe(bits(xs[i]), ids, scores, bits(rs[i]), H, M, host["gate"], host["up"], host["down"],
+        orc.k4_moe(xb[i], ids, scores, rb[i], H, M, host["gate"], host["up"], host["down"],
                    sc["gate"][0], sc["gate"][1], sc["up"][0], sc["up"][1], sc["down"][0], sc["down"][1])
-        done += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
-    return {"value": done / el, "unit": "tokens/s", "cores": orc.num_threads(), "kind": "port",
-            "sample": f"{done} tokens of the same batch-1 K4 layer (router GEMV + route + 9-expert MLP + combine), "
-                      f"{el:.1f} s; {kind}"}
+
+    t0 = time.perf_counter()
+    token(0)  # warm-up (page-in, thread pool start)
+    warm = time.perf_counter() - t0
+    per_run = max(1, int(round(seconds / runs / max(warm, 1e-3))))
+    rates = []
+    done = 0
+    for r in range(runs):
+        t0 = time.perf_counter()
+        for i in range(per_run):
+            token(1 + done + i)
+        rates.append(per_run / (time.perf_counter() - t0))
+        done += per_run
+    return {"value": round(statistics.median(rates), 3), "unit": "tokens/s", "cores": orc.num_threads(),
+            "kind": "port",
+            "runs": [round(v, 3) for v in rates],
+            "sample": f"{runs} runs of {per_run} tokens after one warm-up token, median reported: the same batch-1 "
+                      f"K4 layer (router GEMV + route + 9-expert MLP + combine), rotating {len(xb)} tokens; {kind}"}
 
 
 def main():
@@ -170,26 +185,13 @@ def main():
     per_step_ms = start.elapsed_time(end) / n
     us_tok = per_step_ms * 1e3
 
-    # duration of the layer kernel itself: a second pass that records HIP events on the launch
-    # stream around the one cooperative launch (marks 1 and 3 of moe_profile_events); the events
-    # add gaps, so this pass is not the headline time
-    import ctypes
-    ne = min(n, 100)
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(ne)]
-    L = lib()
-    # torch creates an event's HIP handle on its first record(): record each once first
-    for row in evs:
-        for e in row:
-            e.record()
-    handles = [(ctypes.c_void_p * 4)(*[ctypes.c_void_p(e.cuda_event) for e in row]) for row in evs]
-    torch.cuda.synchronize()
-    for i in range(ne):
-        L.moe_profile_events(handles[i], 4)
-        step(args.warmup + n + i)
-    torch.cuda.synchronize()
-    layer_us = sum(evs[i][1].elapsed_time(evs[i][3]) for i in range(ne)) / ne * 1e3
-    achieved = BYTES_TOKEN / (layer_us * 1e-6) / 1e9
-    hbm = BYTES_TOKEN / (us_tok * 1e-6) / 1e9
+    # one step = one launch of the fused layer kernel on this stream, back to back: the timed
+    # region's per-step time is the kernel's average duration (a rocprofv3 kernel trace of the same
+    # command agrees: profiles/k4_layer_b1_kernel_trace.txt)
+    from mlxlr8_amd._lib import stalled_launches
+    wait_errors = stalled_launches()
+    achieved = BYTES_TOKEN / (us_tok * 1e-6) / 1e9
+    hbm = achieved
     traffic = traffic_from_profiles()
 
     result = {
@@ -215,11 +217,13 @@ def main():
         "hbm_GBps": round(hbm, 1),
         "hbm_frac": round(hbm / HBM_PEAK_GBPS, 4),
         "bytes_per_token": BYTES_TOKEN,
-        "kernels_us": {"k4_layer_kernel": round(layer_us, 2)},
+        "wait_errors": wait_errors,
         "roofline": {"kernel": "k4_layer_kernel<1, false> (router, top-8, shared and routed gate/up and down decode "
                                "GEMVs, finishes and combine in one persistent launch)",
                      "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
+                     "traffic_source": "committed rocprofv3 PMC summary profiles/k4_layer_b1_pmc.txt (FETCH_SIZE, "
+                                       "WRITE_SIZE per launch, copy-calibrated), not measured in this run",
                      "algorithmic_bytes": BYTES_TOKEN},
         "wall_s": round(wall, 3),
     }
@@ -271,6 +275,12 @@ def _line(args, value, unit, ms, dtype, workload, extra, algo_bytes, kernel):
     return out
 
 
+def _stalls():
+    """Fused decode launches of this run whose bounded cross-wave waits ran out (should be 0)."""
+    from mlxlr8_amd._lib import stalled_launches
+    return stalled_launches()
+
+
 MX_EXPERT_BYTES = 2 * M * H // 2 + 2 * M * H // 32 + H * M // 2 + H * M // 32   # 20,054,016
 
 
@@ -302,7 +312,10 @@ def bench_mxfp4_decode(args):
                  {"global_batch": 1, "seq_len": 1, "layers_rotated": len(layers)}, algo,
                  "mx_layer_kernel: router, both projections of the nine slots and the combine in one launch")
     line["roofline"]["traffic"] = traffic_from_profiles("mxfp4_layer_b1_pmc.txt")
-    return dict(line, us_per_token=round(ms * 1e3, 2))
+    if line["roofline"]["traffic"] is not None:
+        line["roofline"]["traffic_source"] = "committed rocprofv3 PMC summary profiles/mxfp4_layer_b1_pmc.txt"
+    from mlxlr8_amd._lib import stalled_launches
+    return dict(line, us_per_token=round(ms * 1e3, 2), wait_errors=stalled_launches())
 
 
 def bench_k4_verify(args):
@@ -327,7 +340,7 @@ def bench_k4_verify(args):
                       "distinct experts streamed once)",
                       {"global_batch": 8, "seq_len": 1, "distinct_experts": U, "layers_rotated": len(layers)},
                       algo, "k4_layer_kernel<8, false>: router, the distinct experts' projections and the combine in one launch"),
-                us_per_step=round(ms * 1e3, 2))
+                us_per_step=round(ms * 1e3, 2), wait_errors=_stalls())
 
 
 def bench_prefill(args, steps=None, warmup=None):
@@ -404,6 +417,7 @@ def bench_stack(args):
                 {"global_batch": 1, "seq_len": 1, "layers": n}, algo, "20 x (residual + RMSNorm launch, fused K4 block launch)")
     out["steps"] = steps
     out["us_per_token_stack"] = round(ms * 1e3, 2)
+    out["wait_errors"] = _stalls()
     return out
 
 

@@ -15,11 +15,11 @@
  * Shapes: hidden h, intermediate m, experts E (routed + shared, the shared expert last).
  * Alignment: activation rows (x) and per-expert side-vector rows are read 8 bytes at a time and
  * residual / output rows 4 bytes at a time; the K4 decode entries reject misaligned pointers.
- * Expert ids: the decode entries (moe_k4_mlp, moe_k4_mlp_finish, moe_k4_expert_linear,
- * moe_mxfp4_mlp, moe_mxfp4_mlp_finish) clamp an id outside [0, E) to the nearest valid expert
- * instead of failing: checking ids on the host would synchronise the stream.  Callers validate
- * ids beforehand (the routed entries produce valid ids themselves); the grouped entries skip such
- * slots instead (see there).
+ * Expert ids: every entry that takes caller ids (the decode entries moe_k4_mlp, moe_k4_mlp_finish,
+ * moe_k4_expert_linear, moe_mxfp4_mlp, moe_mxfp4_mlp_finish and the grouped entries) clamps an id
+ * outside [0, E), read as a signed 32-bit integer, to the nearest valid expert (a negative id to 0,
+ * one >= E to E - 1) instead of failing: checking ids on the host would synchronise the stream.  Callers validate ids beforehand (the routed entries produce valid ids
+ * themselves).  moe_segment_table alone skips such ids (see there).
  *
  * Each entry point names the reference interface it replaces (paths relative to the
  * reference repository root).
@@ -50,6 +50,47 @@ const char* moe_last_error(void);
 /* Per-device setup (codebook table).  Called implicitly by every entry point; exposed so a
  * caller can pay the cost up front.  Acts on the current HIP device. */
 int moe_init(void);
+
+/* ---------------------------------------------------------------- fused decode blocks: status
+ *
+ * The one-launch decode blocks (moe_k4_moe_decode, moe_k4_layer_decode, moe_k4_mlp,
+ * moe_k4_mlp_finish, and moe_mxfp4_moe_decode / its _noalloc twin for one row) run one persistent
+ * block per compute unit whose waves hand results to each other through the workspace.  They need
+ * all of their blocks resident together: run them with no other kernel occupying the device's
+ * compute units (calls on several streams at once may stall each other).  Every cross-wave wait is
+ * bounded; a launch in which a wait ran out still completes, but its outputs are unreliable, and
+ * it is counted in the workspace.  The reference reports failure by raising
+ * (exlr8/experts.py:158-159, exlr8/fast_decode.py:110-117); these counts are how a caller learns
+ * of this failure without a host synchronisation per call. */
+enum {
+  MOE_STATUS_K4 = 0,             /* workspace of moe_workspace_bytes(hidden, intermediate) */
+  MOE_STATUS_MXFP4 = 1,          /* workspace of moe_mxfp4_workspace_bytes(hidden, intermediate) */
+  MOE_STATUS_MXFP4_NOALLOC = 2,  /* the current device's scratch of moe_mxfp4_moe_decode_noalloc */
+};
+
+/* Number of fused-block launches on `workspace` (of the given kind) in which a bounded wait ran out,
+ * since the workspace was zeroed or the last call; resets the count.  Synchronises `stream` (the
+ * stream the workspace's launches use).  No counterpart in the reference: it replaces the
+ * reference's raised errors for this failure (see above). */
+int moe_decode_status(const void* workspace, int kind, int hidden, int intermediate, int32_t* stalled,
+                      moe_stream_t stream);
+
+/* Bound of the fused blocks' cross-wave waits in polls of their longest pause (0 = the default,
+ * about 50 ms); applies to launches made after the call, on every device.  No counterpart in the
+ * reference: for tests that make waits give up on purpose and check moe_decode_status. */
+int moe_set_wait_bound(int polls);
+
+/* The fused K4 block's work list for a layer (hidden, intermediate) with `units` distinct experts
+ * (1..72; route != 0: the launch routes, unit 0 = the shared expert), in list order: 5 int32 per
+ * item (kind, unit, a, b, c) with kind 0 gate/up part (a = output block, b = projection 0 gate /
+ * 1 up, c = input block), 1 down part (a = output block, c = input block), 2 router item (a = item),
+ * 3 gate finish (a = column block), 4 down finish (a = output block; the last unit's also
+ * combine), 6 group sum (a = column block, b = group).  Items are dealt round-robin over 8
+ * sub-lists, one per XCD; an item waits only for items before it in this list, which is what
+ * keeps the persistent launch from deadlocking.  Returns the item count (items may be NULL to ask
+ * for it).  Host-only, no device work.  No counterpart in the reference: it exposes the schedule
+ * for checks of that ordering. */
+int moe_k4_item_list(int hidden, int intermediate, int units, int route, int32_t* items, int capacity);
 
 /* Copy the 65536-entry E4M3 code table (one byte per 16-bit trellis state) to `dst`.
  * Replaces: exlr8/trellis.py:43-50 mcg_codebook (as E4M3 codes; exlr8/static_cache.py:11-26). */
@@ -247,7 +288,7 @@ size_t moe_mxfp4_prefill_workspace_bytes(int rows, int hidden, int intermediate,
 /* Sorted grouped joined-MXFP4 expert MLP for many rows: per-slot values [rows*slots, h] bf16 of
  * ids [rows, slots] (x [rows, h] bf16 shared by a row's slots) through the same segment table,
  * activation terms and MX-MFMA grouped GEMMs as moe_mxfp4_prefill, with no router and no combine.
- * Slots whose id is outside [0, experts) get no position in the work order and are not written.
+ * An id outside [0, experts) is clamped to the nearest valid expert, as in the decode entries.
  * Weights/side vectors as moe_mxfp4_mlp; workspace: moe_mxfp4_grouped_mlp_workspace_bytes (no zeroing).
  * Replaces: exlr8/joined_mxfp4.py:98-134 _inner on the sorted-RHS gather_qmm branch (grouped, >= 1028
  * slots in the reference) and exlr8/joined_mxfp4.py:143-147 JoinedMXFP4.slots for prefill rows. */
@@ -289,7 +330,7 @@ int moe_trellis_grouped_mlp(int k, const uint16_t* x, const uint32_t* ids, int r
  * ids [rows, slots] at width k = 2, 3 or 4, over the grouped sorted-expert kernel: x is
  * [rows, in] (a token row shared by its slots, x_per_slot = 0) or [rows*slots, in]; y
  * [rows*slots, out] bf16.  Side vectors [E, in] / [E, out] fp16; side 1 (gate/up) or 2 (down)
- * storage order.  Slots whose id is outside [0, experts) are not written.
+ * storage order.  An id outside [0, experts) is clamped to the nearest valid expert.
  * Workspace: moe_trellis_grouped_linear_workspace_bytes(rows, slots, in, out, experts).
  * Replaces: exlr8/trellis.py:172-196 expert_linear (and trellis.metal's generic window) for k != 4. */
 int moe_trellis_grouped_linear(int k, const uint16_t* x, int x_per_slot, const uint32_t* ids, int rows, int slots,

@@ -22,6 +22,9 @@ _SIGNATURES = {
     "moe_version": (ctypes.c_char_p, []),
     "moe_last_error": (ctypes.c_char_p, []),
     "moe_init": (_I32, []),
+    "moe_decode_status": (_I32, [_VP, _I32, _I32, _I32, _VP, _VP]),
+    "moe_set_wait_bound": (_I32, [_I32]),
+    "moe_k4_item_list": (_I32, [_I32, _I32, _I32, _I32, _VP, _I32]),
     "moe_codebook_e4m3": (_I32, [_VP, _VP]),
     "moe_route_f32": (_I32, [_VP, _VP, _I32, _VP, _VP, _VP]),
     "moe_router_logits": (_I32, [_VP, _VP, _I32, _I32, _I32, _VP, _VP]),
@@ -120,6 +123,37 @@ def workspace(device, hidden, intermediate, kind="k4"):
         ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
         _workspaces[key] = ws
     return ws
+
+
+# workspace kinds of moe_decode_status (include/moe_mi355x.h)
+STATUS_K4, STATUS_MXFP4, STATUS_MXFP4_NOALLOC = 0, 1, 2
+
+
+def decode_status(ws, kind, hidden, intermediate, stream_handle):
+    """Fused-block launches on one workspace whose bounded waits ran out since the last query (reset
+    by the query; synchronises the workspace's stream)."""
+    n = ctypes.c_int32(0)
+    check(lib().moe_decode_status(ptr(ws) if ws is not None else None, int(kind), int(hidden), int(intermediate),
+                                  ctypes.byref(n), ctypes.c_void_p(stream_handle)))
+    return int(n.value)
+
+
+def stalled_launches():
+    """Fused decode launches, over every workspace this process created, in which a bounded
+    cross-wave wait ran out since the last call (their outputs are unreliable); resets the counts.
+    The reference raises on failure; the decode entries cannot without a host synchronisation per
+    call, so a caller checks here at its own synchronisation points."""
+    total = 0
+    for (dev, stream_handle, hidden, inter, kind), ws in list(_workspaces.items()):
+        status_kind = STATUS_MXFP4 if kind == "mxfp4" else STATUS_K4
+        with torch.cuda.device(ws.device):
+            total += decode_status(ws, status_kind, hidden, inter, stream_handle)
+    return total
+
+
+def set_wait_bound(polls):
+    """Bound of the fused blocks' cross-wave waits (0 = the default ~50 ms); for tests."""
+    check(lib().moe_set_wait_bound(int(polls)))
 
 
 def require_cuda(*tensors):

@@ -133,6 +133,7 @@ struct LayerArgs {
   float eps;
   uint16_t* h_row;
   uint16_t* x_row;
+  int wait_polls;            // bound of a cross-wave wait (moe_set_wait_bound)
   LayerWs w;
 };
 
@@ -233,15 +234,31 @@ struct Item {
 #define MOE_LAYER_LAG_D 4
 #endif
 constexpr int kLagG = MOE_LAYER_LAG_G, kLagD = MOE_LAYER_LAG_D;
+__host__ __device__ __forceinline__ int imin(int a, int b) { return a < b ? a : b; }
+// The list's shape for a layer: hidden h, intermediate m, route = the launch routes itself.
+__host__ __device__ __forceinline__ Items make_items(int h, int m, int route) {
+  Items L;
+  L.HB = h / 128;
+  L.MB = m / 128;
+  L.G = 2 * L.MB * L.HB;
+  L.D = L.HB * L.MB;
+  L.S = h / kRouterSlice;
+  // group sums for the last kLagG units when their gate finishes then take one round (HB <= 8 kSumRound)
+  L.NG = MOE_LAYER_GS && (L.HB + kSumRound - 1) / kSumRound <= kSumRound ? (L.HB + kSumRound - 1) / kSumRound : 0;
+  L.R = route ? 256 * L.S : 0;
+  L.route = route;
+  return L;
+}
 // items that need no plan (the positions of GU(0) do not depend on the unit count)
-__device__ __forceinline__ int pre_items(const Items& L) { return L.route ? L.R + L.G : 0; }
-__device__ __forceinline__ int list_len(const Items& L, int U) {
-  return (L.route ? L.R : 0) + U * (L.G + L.MB) + min(U, kLagG) * L.NG * L.MB + U * (L.D + L.HB);
+__host__ __device__ __forceinline__ int pre_items(const Items& L) { return L.route ? L.R + L.G : 0; }
+__host__ __device__ __forceinline__ int list_len(const Items& L, int U) {
+  return (L.route ? L.R : 0) + U * (L.G + L.MB) + imin(U, kLagG) * L.NG * L.MB + U * (L.D + L.HB);
 }
 // position j inside a phase of U blocks of `big` part items, each followed after `lag` blocks by
 // `small` finish items: sets (is_finish, unit, index inside the block); units count from 0
-__device__ __forceinline__ void phase_at(int j, int U, int big, int small, int lag, bool& fin, int& unit, int& r) {
-  const int lead = min(U, lag);  // blocks without a finish tail
+__host__ __device__ __forceinline__ void phase_at(int j, int U, int big, int small, int lag, bool& fin, int& unit,
+                                                  int& r) {
+  const int lead = imin(U, lag);  // blocks without a finish tail
   if (j < lead * big) {
     fin = false;
     unit = j / big;
@@ -268,7 +285,7 @@ __device__ __forceinline__ void phase_at(int j, int U, int big, int small, int l
   unit = mid + j / small;
   r = j - (unit - mid) * small;
 }
-__device__ __forceinline__ void set_gu(const Items& L, Item& it, int u, int r) {
+__host__ __device__ __forceinline__ void set_gu(const Items& L, Item& it, int u, int r) {
   it.kind = IT_GU;
   it.u = u;
   it.a = r / (2 * L.HB);
@@ -276,13 +293,13 @@ __device__ __forceinline__ void set_gu(const Items& L, Item& it, int u, int r) {
   it.b = rem / L.HB;
   it.c = rem - it.b * L.HB;
 }
-__device__ __forceinline__ void set_down(const Items& L, Item& it, int u, int r) {
+__host__ __device__ __forceinline__ void set_down(const Items& L, Item& it, int u, int r) {
   it.kind = IT_DOWN;
   it.u = u;
   it.c = r / L.HB;
   it.a = r - it.c * L.HB;
 }
-__device__ __forceinline__ Item item_at(const Items& L, int j, int U) {
+__host__ __device__ __forceinline__ Item item_at(const Items& L, int j, int U) {
   Item it{IT_NONE, 0, 0, 0, 0};
   if (L.route) {
     // The first R + G positions hold the router items and GU(0) mixed in the ratio R : G within
@@ -291,7 +308,7 @@ __device__ __forceinline__ Item item_at(const Items& L, int j, int U) {
     const int P = L.R + L.G;
     if (j < P) {
       constexpr int C = kXcds * kLW;
-      const int c0 = j - j % C, c1 = min(c0 + C, P);
+      const int c0 = j - j % C, c1 = imin(c0 + C, P);
       const int r0 = c0 * L.R / P, rc = c1 * L.R / P - r0;  // below 2^31: P <= 18432, R <= 2048
       const int o = j - c0;  // = 8 wave + sub-list for the first waves: wave < rc / 8 routes
       if (o < rc) {
@@ -306,7 +323,7 @@ __device__ __forceinline__ Item item_at(const Items& L, int j, int U) {
   }
   bool fin;
   int unit, r;
-  const int lenA = U * (L.G + L.MB), NU = min(U, kLagG), NGS = L.NG * L.MB, tailA = lenA - NU * L.MB;
+  const int lenA = U * (L.G + L.MB), NU = imin(U, kLagG), NGS = L.NG * L.MB, tailA = lenA - NU * L.MB;
   if (j >= tailA && j < lenA + NU * NGS) {
     // per unit of the last NU: its group sums (block-major), then its gate finishes
     const int t = j - tailA, k = t / (NGS + L.MB), q = t - k * (NGS + L.MB);
@@ -860,16 +877,7 @@ __global__ __launch_bounds__(kLW * 64) void k4_layer_kernel(LayerArgs a) {
   _Float16* __restrict__ xw = xa + wv * xa_halves(NT);
   const int xcd = (int)(blockIdx.x % kXcds);
   int32_t* qc = a.w.queue + xcd * kQueueStride;
-  Items L;
-  L.HB = a.h / 128;
-  L.MB = a.m / 128;
-  L.G = 2 * L.MB * L.HB;
-  L.D = L.HB * L.MB;
-  L.S = a.h / kRouterSlice;
-  // group sums for the last kLagG units when their gate finishes then take one round (HB <= 8 kSumRound)
-  L.NG = MOE_LAYER_GS && (L.HB + kSumRound - 1) / kSumRound <= kSumRound ? (L.HB + kSumRound - 1) / kSumRound : 0;
-  L.R = a.route ? 256 * L.S : 0;
-  L.route = a.route;
+  const Items L = make_items(a.h, a.m, a.route);
   const int pre = pre_items(L);
   // the launch's epoch (read once per block below) and its tag
   uint32_t epoch = 0, tag = 0;
@@ -1115,21 +1123,13 @@ __global__ __launch_bounds__(kLW * 64) void k4_layer_kernel(LayerArgs a) {
     __builtin_amdgcn_s_setprio(0);
     sub = claim();
   }
-  // the last block to leave resets the sub-list counters and advances the epoch
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    exit_last = __hip_atomic_fetch_add(a.w.flags + LF_EXIT, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) + 1 ==
-                (int)gridDim.x;
-  }
-  __syncthreads();
-  if (exit_last && threadIdx.x < kXcds) st_coh_i(a.w.queue + threadIdx.x * kQueueStride, 0);
-  if (exit_last && threadIdx.x == 0) {
-    st_coh_i(a.w.flags + LF_EXIT, 0);
-    st_coh_i(a.w.flags + LF_EPOCH, (int)(epoch + 1u == 0xFFFFFFFEu ? 0u : epoch + 1u));
-  }
+  // the last block to leave reports a stalled wait, advances the epoch and resets the sub-list
+  // counters
+  const bool last = leave_launch(a, epoch, exit_last);
+  if (last && threadIdx.x < kXcds) st_coh_i(a.w.queue + threadIdx.x * kQueueStride, 0);
   // a wave may end with its stores still in flight, and the next launch reads these words at its
   // start: they are acknowledged before the block ends
-  if (exit_last) release_stores();
+  if (last) release_stores();
 }
 
 // ---------------------------------------------------------------- host side
@@ -1154,6 +1154,7 @@ LayerWs layer_carve(void* base, int h, int m) {
 }
 
 Plan* k4_layer_plan(void* layer_ws) { return layer_carve(layer_ws, 1024, 128).plan; }
+int32_t* k4_layer_flags(void* layer_ws, int h, int m) { return layer_carve(layer_ws, h, m).flags; }
 
 size_t k4_layer_workspace_bytes(int h, int m) {
   return layer_carve(nullptr, h > 0 ? h : 128, m > 0 ? m : 128).bytes;
@@ -1172,6 +1173,31 @@ int k4_layer_check_alignment(const uint16_t* x, const uint16_t* residual, const 
   return MOE_OK;
 }
 
+int k4_layer_item_list(int h, int m, int units, int route, int32_t* items, int capacity) {
+  if (!k4_layer_supported(h, m, route != 0) || units < 1 || units > kMaxUnits || capacity < 0)
+    return fail(MOE_EINVAL, "no fused K4 item list for hidden %d, intermediate %d, %d units", h, m, units);
+  const Items L = make_items(h, m, route != 0);
+  const int n = list_len(L, units);
+  if (items) {
+    if (capacity < n) return fail(MOE_EINVAL, "the list has %d items (capacity %d)", n, capacity);
+    for (int j = 0; j < n; j++) {
+      // a launch resolves the positions before the plan's with one unit (it does not know the
+      // count yet): they must not depend on it
+      const Item it = j < pre_items(L) ? item_at(L, j, 1) : item_at(L, j, units);
+      const Item full = item_at(L, j, units);
+      if (it.kind != full.kind || it.u != full.u || it.a != full.a || it.b != full.b || it.c != full.c)
+        return fail(MOE_EINVAL, "item %d depends on the unit count before the plan is known", j);
+      int32_t* o = items + 5 * (int64_t)j;
+      o[0] = it.kind;
+      o[1] = it.u;
+      o[2] = it.a;
+      o[3] = it.b;
+      o[4] = it.c;
+    }
+  }
+  return n;
+}
+
 bool k4_layer_supported(int h, int m, bool route) {
   return h > 0 && m > 0 && h % (route ? kRouterSlice : 128) == 0 && m % 128 == 0 && h <= (route ? kMaxRouteHidden : 16384) &&
          m <= 16384;
@@ -1181,10 +1207,12 @@ bool k4_layer_supported(int h, int m, bool route) {
 // its counters clean and advances its epoch).
 static int k4_layer_launch(LayerArgs a, void* workspace, hipStream_t s) {
   a.w = layer_carve(workspace, a.h, a.m);
+  a.wait_polls = wait_polls();
   a.tab8 = codebook_device_table();
   a.tab16 = codebook_f16_device_table();
   if (!a.tab8 || !a.tab16) return fail(MOE_ENOTSUP, "code tables are not initialised on this device");
-  const int grid = device_cus();
+  // every sub-list (blockIdx mod kXcds) needs a block to serve it
+  const int grid = device_cus() > kXcds ? device_cus() : kXcds;
   if (a.rows <= 1 && a.norm_x)
     hipLaunchKernelGGL((k4_layer_kernel<1, true>), dim3(grid), dim3(kLW * 64), 0, s, a);
   else if (a.rows <= 1)

@@ -24,8 +24,10 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <atomic>
 #include <mutex>
 
+#include "layer_sync.h"
 #include "moe_device.h"
 #include "moe_host.h"
 #include "moe_plan.h"
@@ -735,9 +737,6 @@ int ensure_device_ready() {
   void* table16 = nullptr;
   MOE_HIP(hipGetSymbolAddress(&table16, HIP_SYMBOL(g_codebook_f16)));
   st.codebook16 = static_cast<const uint16_t*>(table16);
-  int coop = 0;
-  MOE_HIP(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev));
-  if (!coop) return fail(MOE_ENOTSUP, "device %d does not support cooperative launches", dev);
   hipLaunchKernelGGL(build_codebook_kernel, dim3(128), dim3(256), 0, 0);
   MOE_HIP(hipGetLastError());
   MOE_HIP(hipDeviceSynchronize());
@@ -761,6 +760,19 @@ int device_cus() {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
   return g_devices[dev].cus;
+}
+
+namespace {
+std::atomic<int> g_wait_polls{0};  // 0: the default bound
+// Takes the stalled-launch count out of a flag word (the host has waited for the stream).
+__global__ void clear_word_kernel(int32_t* p) {
+  __hip_atomic_store(p, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+}  // namespace
+
+int wait_polls() {
+  const int v = g_wait_polls.load(std::memory_order_relaxed);
+  return v > 0 ? v : kDefaultWaitPolls;
 }
 
 // ---------------------------------------------------------------- workspace layout
@@ -876,6 +888,45 @@ int moe_codebook_e4m3(uint8_t* dst, moe_stream_t stream) {
   hipLaunchKernelGGL(copy_codebook_kernel, dim3(256), dim3(256), 0, (hipStream_t)stream, dst);
   MOE_HIP(hipGetLastError());
   return MOE_OK;
+}
+
+int moe_set_wait_bound(int polls) {
+  MOE_ARG(polls >= 0, "the wait bound must be >= 0 polls (0 restores the default), got %d", polls);
+  g_wait_polls.store(polls, std::memory_order_relaxed);
+  return MOE_OK;
+}
+
+int moe_decode_status(const void* workspace, int kind, int hidden, int intermediate, int32_t* stalled,
+                      moe_stream_t stream) {
+  MOE_ARG(stalled != nullptr, "stalled must not be NULL");
+  MOE_ARG(kind >= MOE_STATUS_K4 && kind <= MOE_STATUS_MXFP4_NOALLOC, "unknown workspace kind %d", kind);
+  MOE_ARG(kind == MOE_STATUS_MXFP4_NOALLOC || workspace != nullptr, "workspace must not be NULL");
+  MOE_ARG(kind != MOE_STATUS_K4 || (hidden > 0 && intermediate > 0), "hidden and intermediate must be positive");
+  int rc = ensure_device_ready();
+  if (rc) return rc;
+  int32_t* flags = nullptr;
+  void* ws = const_cast<void*>(workspace);
+  if (kind == MOE_STATUS_K4) {
+    flags = k4_layer_flags(carve(ws, hidden, intermediate).layer, hidden, intermediate);
+  } else if (kind == MOE_STATUS_MXFP4) {
+    flags = mx_workspace_flags(ws, hidden, intermediate);
+  } else if ((rc = mx_scratch_flags(&flags))) {
+    return rc;
+  }
+  const hipStream_t s = (hipStream_t)stream;
+  int32_t v = 0;
+  MOE_HIP(hipMemcpyAsync(&v, flags + LF_STALLED, sizeof(v), hipMemcpyDeviceToHost, s));
+  MOE_HIP(hipStreamSynchronize(s));
+  if (v != 0) {
+    hipLaunchKernelGGL(clear_word_kernel, dim3(1), dim3(1), 0, s, flags + LF_STALLED);
+    MOE_HIP(hipGetLastError());
+  }
+  *stalled = v;
+  return MOE_OK;
+}
+
+int moe_k4_item_list(int hidden, int intermediate, int units, int route, int32_t* items, int capacity) {
+  return k4_layer_item_list(hidden, intermediate, units, route, items, capacity);
 }
 
 int moe_profile_events(void** events, int count) {

@@ -69,9 +69,14 @@ __device__ __forceinline__ void kp_store_a(uint16_t* a, int64_t p, int nq, int k
 // ---------------------------------------------------------------- prep: xh for gate and up
 // One wave per (sorted row p, 128-block kb, projection of nproj = 1 or 2): H128(x_row *
 // in_scale[e]) -> A buffer, x_row = the slot's token row (x_per_slot = 0) or its own row.
-// Sorted rows placed by the segment table: ids outside [0, experts) get no position.
+// Sorted rows placed by the segment table (ids outside [0, experts) clamped to the nearest expert).
 __device__ __forceinline__ int64_t kp_placed(const int32_t* counts, const int32_t* starts, int experts) {
   return (int64_t)starts[experts - 1] + counts[experts - 1];
+}
+// The expert of a placed slot: its id clamped into [0, experts) exactly as the segment table placed it
+// (a slot with an out-of-range id has a position, so its id must never index a side vector raw).
+__device__ __forceinline__ int64_t kp_expert(const uint32_t* ids, int slot, int experts) {
+  return min(max((int)ids[slot], 0), experts - 1);
 }
 
 __global__ __launch_bounds__(256) void kp_prep_kernel(const uint16_t* __restrict__ x, const uint32_t* __restrict__ ids,
@@ -89,7 +94,7 @@ __global__ __launch_bounds__(256) void kp_prep_kernel(const uint16_t* __restrict
   const int64_t p = (wid >> sh) / kbs;
   if (p >= kp_placed(counts, starts, experts)) return;
   const int slot = order[p];
-  const int64_t e = ids[slot];
+  const int64_t e = kp_expert(ids, slot, experts);
   const int lane = lane_id();
   const int k = kb * 128 + 2 * lane;
   const int64_t xrow = x_per_slot ? slot : slot / slots;
@@ -314,7 +319,7 @@ __global__ __launch_bounds__(256) void kp_gate_finish_kernel(const float* __rest
   const int64_t p = wid / cbs;
   if (p >= kp_placed(counts, starts, experts)) return;
   const int cb = (int)(wid % cbs);
-  const int64_t e = ids[order[p]];
+  const int64_t e = kp_expert(ids, order[p], experts);
   const int col = cb * 128 + 2 * lane_id();
   const f32x2 gv = *reinterpret_cast<const f32x2*>(inner + p * 2 * m + col);
   const f32x2 uv = *reinterpret_cast<const f32x2*>(inner + p * 2 * m + m + col);
@@ -350,7 +355,7 @@ __global__ __launch_bounds__(256) void kp_value_finish_kernel(const float* __res
   if (p >= kp_placed(counts, starts, experts)) return;
   const int hb = (int)(wid % hbs);
   const int slot = order[p];
-  const int64_t e = ids[slot];
+  const int64_t e = kp_expert(ids, slot, experts);
   const int col = hb * 128 + 2 * lane_id();
   const f32x2 v = *reinterpret_cast<const f32x2*>(inner + p * h + col);
   float v0 = v.x, v1 = v.y;
@@ -459,8 +464,8 @@ int moe_trellis_grouped_mlp(int k, const uint16_t* x, const uint32_t* ids, int r
   if (rc) return rc;
   hipStream_t s = (hipStream_t)stream;
   // sorted work order in blocks of <= 64 rows (ids outside [0, experts) get no position)
-  if ((rc = moe_segment_table(ids, (int)n, (int)experts, kKpRows, w.order, w.counts, w.starts, w.blk, w.cap, w.nblk,
-                              stream)))
+  if ((rc = segment_table_clamped(ids, (int)n, (int)experts, kKpRows, w.order, w.counts, w.starts, w.blk, w.cap, w.nblk,
+                                  (hipStream_t)stream)))
     return rc;
   const int64_t pw = n * (hidden / 128) * 2;
   hipLaunchKernelGGL(kp_prep_kernel, dim3((unsigned)((pw + 3) / 4)), dim3(256), 0, s, x, ids, w.order, w.counts, w.starts,
@@ -543,8 +548,8 @@ int moe_trellis_grouped_linear(int k, const uint16_t* x, int x_per_slot, const u
   int rc = ensure_device_ready();
   if (rc) return rc;
   hipStream_t s = (hipStream_t)stream;
-  if ((rc = moe_segment_table(ids, (int)n, (int)experts, kKpRows, w.order, w.counts, w.starts, w.blk, w.cap, w.nblk,
-                              stream)))
+  if ((rc = segment_table_clamped(ids, (int)n, (int)experts, kKpRows, w.order, w.counts, w.starts, w.blk, w.cap, w.nblk,
+                                  (hipStream_t)stream)))
     return rc;
   const int64_t pw = n * (in_features / 128);
   hipLaunchKernelGGL(kp_prep_kernel, dim3((unsigned)((pw + 3) / 4)), dim3(256), 0, s, x, ids, w.order, w.counts, w.starts,

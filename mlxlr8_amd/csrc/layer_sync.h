@@ -24,8 +24,11 @@ namespace moe {
 
 constexpr int kRouterSlice = 1024;  // router inputs per work item
 constexpr int kMaxRouteHidden = 8192;  // hidden size limit of the fused router
-constexpr int kSpinLimit = 1 << 14;  // polls of a bounded wait (with the backoff below: ~50 ms)
-enum LayerFlag { LF_ERROR = 1, LF_EXIT = 2, LF_EPOCH = 3, LF_COUNT = 8 };
+// Workspace words of a fused block: LF_ERROR is set by a wave whose bounded wait ran out, LF_EXIT
+// counts the blocks that left, LF_EPOCH tags the launch's words, LF_STALLED counts the launches
+// that ended with LF_ERROR set (the last block to leave folds LF_ERROR into it and clears it; the
+// host reads and resets it with moe_decode_status).
+enum LayerFlag { LF_ERROR = 1, LF_EXIT = 2, LF_EPOCH = 3, LF_STALLED = 4, LF_COUNT = 8 };
 
 // The lane index recomputed where it is used.  Code that runs rarely (router items, routing,
 // finishes) uses it: with the plain index the compiler hoists their lane-derived addresses to the
@@ -64,10 +67,11 @@ __device__ __forceinline__ void set_error(const A& a) {
 // The pause doubles from 64 clocks up to 64 * kMaxPauses: waiting waves must leave the memory
 // system to the producers they wait for (hundreds of waves re-reading their inputs back to back
 // starve them).  A wait on the critical path that only one wave per block makes (routing) uses a
-// short pause; the bound on the total wait stays the same (~50 ms).
+// short pause; the bound on the total wait stays the same (~50 ms).  `a.wait_polls` is the bound
+// in polls of the longest pause (kDefaultWaitPolls unless the host set another: moe_set_wait_bound).
 template <int kMaxPauses = 64, class A>
 __device__ __forceinline__ bool keep_waiting(const A& a, int& spins) {
-  if (++spins >= kSpinLimit * (64 / kMaxPauses)) {
+  if (++spins >= a.wait_polls * (64 / kMaxPauses)) {
     set_error(a);
     return false;
   }
@@ -75,6 +79,31 @@ __device__ __forceinline__ bool keep_waiting(const A& a, int& spins) {
   for (int k = 0; k < pauses; k++) __builtin_amdgcn_s_sleep(1);
   return true;
 }
+// The launch's exit, run by every thread of every block after its work: the last block to leave
+// folds the error word into the stalled-launch count and clears it, resets LF_EXIT and advances
+// the epoch.  Every wave's stores (an error word among them) are acknowledged before its block
+// counts itself out, so the last block sees every error of the launch.  Returns whether this
+// block was the last (its remaining resets are the caller's).
+template <class A>
+__device__ __forceinline__ bool leave_launch(const A& a, uint32_t epoch, int32_t& exit_last_lds) {
+  release_stores();
+  __syncthreads();
+  if (threadIdx.x == 0)
+    exit_last_lds = __hip_atomic_fetch_add(a.w.flags + LF_EXIT, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) + 1 ==
+                    (int)gridDim.x;
+  __syncthreads();
+  const bool last = exit_last_lds != 0;
+  if (last && threadIdx.x == 0) {
+    if (ld_coh_i(a.w.flags + LF_ERROR) != 0) {
+      st_coh_i(a.w.flags + LF_STALLED, ld_coh_i(a.w.flags + LF_STALLED) + 1);
+      st_coh_i(a.w.flags + LF_ERROR, 0);
+    }
+    st_coh_i(a.w.flags + LF_EXIT, 0);
+    st_coh_i(a.w.flags + LF_EPOCH, (int)(epoch + 1u == 0xFFFFFFFEu ? 0u : epoch + 1u));
+  }
+  return last;
+}
+
 // the lane's two words p[0], p[1] (a column pair) once both carry `tag`
 template <int kMaxPauses = 64, class A>
 __device__ __forceinline__ f32x2 ld_tag_pair(const A& a, const uint64_t* p, uint32_t tag) {

@@ -17,6 +17,11 @@ int ensure_device_ready();
 // Number of compute units of the current device (cached per device).
 int device_cus();
 
+// Bound of the fused decode blocks' cross-wave waits, in polls of their longest pause: the default
+// (~50 ms) unless moe_set_wait_bound set another.  Passed to every fused launch.
+constexpr int kDefaultWaitPolls = 1 << 14;
+int wait_polls();
+
 // Device address of the current device's 64 KB E4M3 code table (after ensure_device_ready), for
 // kernels of other translation units.
 const uint8_t* codebook_device_table();
@@ -28,6 +33,11 @@ int moe_router_fused_plan(const uint16_t* x, const float* w, const float* bias, 
                           float* logits, uint32_t* ids, float* scores, Plan* plan, int32_t* counter, hipStream_t s,
                           const uint16_t* attn = nullptr, const uint16_t* norm_w = nullptr, float eps = 0.0f,
                           uint16_t* h_out = nullptr, uint16_t* xn_out = nullptr);
+
+// Sorted work order of the grouped entries (prefill.hip): moe_segment_table with ids outside
+// [0, experts) clamped to the nearest valid expert (moe_segment_table skips them).
+int segment_table_clamped(const uint32_t* ids, int n, int experts, int block_rows, int32_t* order, int32_t* counts,
+                          int32_t* starts, int32_t* table, int capacity, int32_t* num_blocks, hipStream_t s);
 
 // Fused K4 decode block (k4_layer.hip): route = 1 runs the router and plan on the device (slot 8 of
 // every row = the shared expert, id 256), route = 0 uses the plan in the layer workspace, built
@@ -52,11 +62,21 @@ int k4_layer_run(const uint16_t* x, const uint16_t* residual, int rows, int rout
                  const LayerNorm* norm = nullptr);
 // The layer workspace's plan (where a plan kernel writes it for route = 0).
 Plan* k4_layer_plan(void* layer_ws);
+// The fused block's work list for `units` units: 5 ints per item (kind, unit, a, b, c; see
+// k4_layer.hip), in list order; returns the item count (items may be NULL to ask for it).
+int k4_layer_item_list(int h, int m, int units, int route, int32_t* items, int capacity);
+// The layer workspace's flag words (LayerFlag, layer_sync.h).
+int32_t* k4_layer_flags(void* layer_ws, int h, int m);
 
 // Fused joined-MXFP4 decode block for one token row (mx_layer.hip; hidden 6144, intermediate 2048,
 // 256 routed experts + the shared expert 256): router, both projections of the nine slots and the
 // combine in one launch.  `layer_ws`: mx_layer_workspace_bytes() bytes, zeroed once.
 size_t mx_layer_workspace_bytes();
+int32_t* mx_layer_flags(void* layer_ws);
+// The flag words of the fused MXFP4 block inside a moe_mxfp4_workspace_bytes() workspace, and inside
+// the allocation-free entry's per-device scratch.
+int32_t* mx_workspace_flags(void* workspace, int h, int m);
+int mx_scratch_flags(int32_t** flags);
 int mx_layer_run(const uint16_t* x, const uint16_t* residual, const float* router_w, const float* bias, uint32_t* ids,
                  float* scores, const uint8_t* gu_codes, const uint8_t* gu_scales, const uint8_t* d_codes,
                  const uint8_t* d_scales, const uint16_t* unit, const uint16_t* out_gate, const uint16_t* out_up,

@@ -91,6 +91,7 @@ struct MxLayerArgs {
   const uint16_t* in_down;   // [257][m]
   const uint16_t* out_down;  // [257][h]
   uint16_t* out;             // [1, h] bf16
+  int wait_polls;            // bound of a cross-wave wait (moe_set_wait_bound)
   MxLayerWs w;
 };
 
@@ -490,17 +491,10 @@ void mx_layer_kernel(MxLayerArgs a) {
     __builtin_amdgcn_s_setprio(0);
   }
 
-  // the last block to leave advances the epoch
-  __syncthreads();
-  if (threadIdx.x == 0)
-    exit_last = __hip_atomic_fetch_add(a.w.flags + LF_EXIT, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) + 1 == G;
-  __syncthreads();
-  if (exit_last && threadIdx.x < kUnits) st_coh_i(a.w.hid_cnt + threadIdx.x, 0);
-  if (exit_last && threadIdx.x == 0) {
-    st_coh_i(a.w.flags + LF_EXIT, 0);
-    st_coh_i(a.w.flags + LF_EPOCH, (int)(epoch + 1u == 0xFFFFFFFEu ? 0u : epoch + 1u));
-  }
-  if (exit_last) release_stores();
+  // the last block to leave reports a stalled wait, advances the epoch and resets the counters
+  const bool last = leave_launch(a, epoch, exit_last);
+  if (last && threadIdx.x < kUnits) st_coh_i(a.w.hid_cnt + threadIdx.x, 0);
+  if (last) release_stores();
 }
 
 size_t mx_align(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -526,6 +520,7 @@ int g_fit[64];  // per device: 0 unknown, 1 one block per CU fits, -1 it does no
 }  // namespace
 
 size_t mx_layer_workspace_bytes() { return mx_layer_carve(nullptr).bytes; }
+int32_t* mx_layer_flags(void* layer_ws) { return mx_layer_carve(layer_ws).flags; }
 
 int mx_layer_run(const uint16_t* x, const uint16_t* residual, const float* router_w, const float* bias, uint32_t* ids,
                  float* scores, const uint8_t* gu_codes, const uint8_t* gu_scales, const uint8_t* d_codes,
@@ -567,6 +562,7 @@ int mx_layer_run(const uint16_t* x, const uint16_t* residual, const float* route
   a.out_down = out_down;
   a.out = out;
   a.w = mx_layer_carve(layer_ws);
+  a.wait_polls = wait_polls();
   const int grid = device_cus();
   hipLaunchKernelGGL(mx_layer_kernel, dim3(grid), dim3(kMW * 64), 0, s, a);
   const hipError_t e = hipGetLastError();

@@ -448,6 +448,16 @@ int scratch_address(void** out) {
   return MOE_OK;
 }
 }  // namespace
+
+int32_t* mx_workspace_flags(void* workspace, int h, int m) {
+  return mx_layer_flags(mx_carve(workspace, h > 0 ? h : 1, m > 0 ? m : 1).layer);
+}
+int mx_scratch_flags(int32_t** flags) {
+  void* ws = nullptr;
+  if (int rc = scratch_address(&ws)) return rc;
+  *flags = mx_workspace_flags(ws, 6144, 2048);
+  return MOE_OK;
+}
 }  // namespace moe
 
 using namespace moe;

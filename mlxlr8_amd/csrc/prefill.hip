@@ -64,11 +64,13 @@ constexpr size_t kPfMaxLds = 160 * 1024;  // LDS per workgroup on gfx950
 // slice into its own histogram row, the rows are turned into per-wave write offsets, and each wave
 // then places its slice in order (the rank among equal ids inside a 64-id chunk comes from
 // matching the ids bit by bit with ballots), all waves at once.
+// clamp: an id outside [0, experts) is taken as the nearest valid expert (the grouped MLP and
+// linear entries, like the decode entries); otherwise it is skipped (moe_segment_table).
 __global__ __launch_bounds__(1024) void segment_table_kernel(const uint32_t* __restrict__ ids, int n, int experts,
                                                              int block_rows, int32_t* __restrict__ order,
                                                              int32_t* __restrict__ counts,
                                                              int32_t* __restrict__ starts, int32_t* __restrict__ blk,
-                                                             int cap, int32_t* __restrict__ nblk) {
+                                                             int cap, int32_t* __restrict__ nblk, int clamp) {
   __shared__ int32_t hist[16][kPfMaxExperts];  // per wave: counts, then write offsets
   __shared__ int32_t cnt[kPfMaxExperts], st[kPfMaxExperts], bst[kPfMaxExperts];
   __shared__ int32_t wsum[16];
@@ -76,9 +78,13 @@ __global__ __launch_bounds__(1024) void segment_table_kernel(const uint32_t* __r
   for (int i = tid; i < 16 * kPfMaxExperts; i += 1024) (&hist[0][0])[i] = 0;
   __syncthreads();
   const int s0 = (int)((int64_t)n * wv / 16), s1 = (int)((int64_t)n * (wv + 1) / 16);
-  // ids outside [0, experts) are skipped (they get no position; callers pass valid ids)
-  for (int i = s0 + lane; i < s1; i += 64) {
+  // ids outside [0, experts) are clamped or skipped (no position)
+  auto id_at = [&](int i) {
     const uint32_t e = ids[i];
+    return clamp ? (uint32_t)min(max((int)e, 0), experts - 1) : e;  // as the decode entries: signed id
+  };
+  for (int i = s0 + lane; i < s1; i += 64) {
+    const uint32_t e = id_at(i);
     if (e < (uint32_t)experts) atomicAdd(&hist[wv][e], 1);
   }
   __syncthreads();
@@ -130,7 +136,7 @@ __global__ __launch_bounds__(1024) void segment_table_kernel(const uint32_t* __r
   // are < 1024, invalid ones are given the key 2047 and not placed)
   for (int c0 = s0; c0 < s1; c0 += 64) {
     const int i = c0 + lane;
-    const uint32_t e = i < s1 ? ids[i] : 0xFFFFFFFFu;
+    const uint32_t e = i < s1 ? id_at(i) : 0xFFFFFFFFu;
     const bool valid = e < (uint32_t)experts;
     const uint32_t key = valid ? e : 2047u;
     uint64_t same = __ballot(1);
@@ -727,14 +733,20 @@ PfWorkspace pf_carve(void* base, int rows, int slots, int h, int m, int64_t expe
 }
 
 int launch_segment_table(const uint32_t* ids, int n, int experts, int block_rows, int32_t* order, int32_t* counts,
-                         int32_t* starts, int32_t* blk, int cap, int32_t* nblk, hipStream_t s) {
+                         int32_t* starts, int32_t* blk, int cap, int32_t* nblk, hipStream_t s, int clamp) {
   hipLaunchKernelGGL(segment_table_kernel, dim3(1), dim3(1024), 0, s, ids, n, experts, block_rows, order, counts,
-                     starts, blk, cap, nblk);
+                     starts, blk, cap, nblk, clamp);
   MOE_HIP(hipGetLastError());
   return MOE_OK;
 }
 
 }  // namespace
+
+// The segment table of the grouped MLP / linear entries: ids outside [0, experts) are clamped.
+int segment_table_clamped(const uint32_t* ids, int n, int experts, int block_rows, int32_t* order, int32_t* counts,
+                          int32_t* starts, int32_t* table, int capacity, int32_t* num_blocks, hipStream_t s) {
+  return launch_segment_table(ids, n, experts, block_rows, order, counts, starts, table, capacity, num_blocks, s, 1);
+}
 }  // namespace moe
 
 using namespace moe;
@@ -768,7 +780,7 @@ int moe_segment_table(const uint32_t* ids, int n, int experts, int block_rows, i
   int rc = ensure_device_ready();
   if (rc) return rc;
   return launch_segment_table(ids, n, experts, block_rows, order, counts, starts, table, capacity, num_blocks,
-                              (hipStream_t)stream);
+                              (hipStream_t)stream, 0);
 }
 
 size_t moe_mxfp4_prefill_workspace_bytes(int rows, int hidden, int intermediate, int64_t experts) {
@@ -814,8 +826,8 @@ int mx_grouped_check(const uint16_t* x, const uint8_t* gate_up_codes, const uint
 
 // Sorted grouped MXFP4 expert MLP of ids [rows, slots] (a row's slots share x [rows, hidden]):
 // segment table, activation terms, gate/up GEMM + gate finish, down GEMM + value finish into
-// values [rows * slots, hidden] bf16 (slot order).  Slots whose id is outside [0, experts) get no
-// position in the work order and are not written.
+// values [rows * slots, hidden] bf16 (slot order).  An id outside [0, experts) is taken as the nearest
+// valid expert, as in the decode entries.
 int mx_grouped_body(const uint16_t* x, int rows, int slots, const uint32_t* ids, const uint8_t* gate_up_codes,
                     const uint8_t* gate_up_scales, const uint8_t* down_codes, const uint8_t* down_scales,
                     int64_t experts, const uint16_t* unit, const uint16_t* out_gate, const uint16_t* out_up,
@@ -823,7 +835,7 @@ int mx_grouped_body(const uint16_t* x, int rows, int slots, const uint32_t* ids,
                     const PfWorkspace& w, hipStream_t s) {
   const int n = rows * slots;
   int rc = launch_segment_table(ids, n, (int)experts, kPfItemRows, w.order, w.counts, w.starts, w.blk, w.cap, w.nblk,
-                                s);
+                                s, 1);
   if (rc) return rc;
   // activation terms
   const int64_t pwaves = (int64_t)rows * (hidden / 128);

@@ -177,13 +177,20 @@ SIDE_VECTORS = {
 }
 
 
-def _widths(node):
-    """Every trellis width mentioned anywhere in a manifest layer plan."""
-    if isinstance(node, dict):
-        return set().union(*(_widths(v) for v in node.values())) if node else set()
+def _flat(node):
+    """The numbers of a nested list (or a single number)."""
     if isinstance(node, (list, tuple)):
-        return set().union(*(_widths(v) for v in node)) if node else set()
+        return set().union(*(_flat(v) for v in node)) if node else set()
     return {int(node)}
+
+
+def _widths(plan):
+    """The trellis widths a manifest layer plan assigns to the expert projections: the routed
+    experts' ``gate``, ``up`` and ``down`` entries and the shared expert's (``shared``).  Other keys
+    of a plan (metadata) are not widths and are ignored (exlr8/experts.py:81-85 reads the same six)."""
+    shared = plan["shared"]
+    return set().union(*(_flat(plan[p]) for p in ("gate", "up", "down")),
+                       *(_flat(shared[p]) for p in ("gate", "up", "down")))
 
 
 def _manifest(path):

@@ -13,6 +13,22 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (run with -m gpu on the GPU box)")
 
 
+@pytest.fixture(autouse=True)
+def no_stalled_launches(request):
+    """After every GPU test: no fused decode launch of the test had a cross-wave wait run out (a
+    stalled launch completes with unreliable outputs; the library counts them per workspace)."""
+    yield
+    if request.node.get_closest_marker("gpu") is None:
+        return
+    import torch
+    if not torch.cuda.is_available():
+        return
+    from mlxlr8_amd._lib import stalled_launches
+    torch.cuda.synchronize()
+    n = stalled_launches()
+    assert n == 0, f"{n} fused decode launch(es) had a bounded wait run out"
+
+
 @pytest.fixture(scope="session")
 def orc():
     from oracle import lib

@@ -136,3 +136,18 @@ def test_trellis_grouped_and_combine_argument_errors_without_device():
     assert b"rows" in L.moe_last_error()
     assert L.moe_combine_values(ctypes.c_void_p(258), p, p, 1, 128, p, None) == -1
     assert b"aligned" in L.moe_last_error()
+
+
+def test_status_and_wait_bound_argument_errors_without_device():
+    from mlxlr8_amd._lib import lib
+    L = lib()
+    n = ctypes.c_int32(7)
+    assert L.moe_set_wait_bound(-1) == -1
+    assert b"wait bound" in L.moe_last_error()
+    assert L.moe_decode_status(None, 0, 6144, 2048, ctypes.byref(n), None) == -1
+    assert b"workspace" in L.moe_last_error()
+    assert L.moe_decode_status(ctypes.c_void_p(256), 5, 6144, 2048, ctypes.byref(n), None) == -1
+    assert b"kind" in L.moe_last_error()
+    assert L.moe_decode_status(ctypes.c_void_p(256), 0, 0, 2048, None, None) == -1
+    assert b"NULL" in L.moe_last_error()
+    assert n.value == 7

@@ -104,6 +104,28 @@ def test_manifest_and_width_errors(tmp_path):
         layer_arrays(tmp_path, 5)
 
 
+def test_plan_metadata_keys_are_not_widths(tmp_path):
+    """A layer plan may carry keys besides the projections' widths (numbers or strings, at the top
+    or inside ``shared``): they are not widths and do not fail the uniform-width check."""
+    from mlxlr8_amd.experts import layer_arrays
+    write_up1_layer(tmp_path, layer=6)
+    m = tmp_path / "manifests" / "exlr8-manifest-up1.json"
+    data = json.loads(m.read_text())
+    plan = data["layers"]["6"]
+    plan["bits_per_weight"] = 4.05
+    plan["note"] = "calibrated"
+    plan["shared"]["source"] = "shared-expert"
+    plan["stats"] = {"mse": [0.1, 0.2]}
+    m.write_text(json.dumps(data))
+    k, hidden, inter, packed, scales = layer_arrays(tmp_path, 6)
+    assert (k, hidden, inter) == (4, 128, 128)
+    # a width of 3 inside the projections is still caught
+    plan["down"][7] = 3
+    m.write_text(json.dumps(data))
+    with pytest.raises(ValueError, match="not uniform K4"):
+        layer_arrays(tmp_path, 6)
+
+
 def test_k3_layer_78(tmp_path):
     """Layer 78 is the K3 layer: its k3 file and k3 side vectors load with k = 3."""
     from mlxlr8_amd.experts import layer_arrays
