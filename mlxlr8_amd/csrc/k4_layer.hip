@@ -365,9 +365,12 @@ __host__ __device__ __forceinline__ Item item_at(const Items& L, int j, int U) {
 __device__ __forceinline__ bool is_part(const Item& it) { return it.kind == IT_GU || it.kind == IT_DOWN; }
 
 // ---------------------------------------------------------------- tables and LDS
+// The code table in LDS: the 64 KB E4M3 byte table for every row count.  (The 128 KB fp16 form
+// decodes no faster -- measured 28.1 vs 28.6 codewords/ns/CU in a register-fed loop -- and doubles
+// the launch's start-up copy.)
 template <int NT>
 struct LTable {
-  static constexpr bool kF16 = NT == 1;
+  static constexpr bool kF16 = false;
   static constexpr int kBytes = kF16 ? 131072 : 65536;
 };
 constexpr int xa_halves(int nt) { return 2 * 2 * (2 * nt) * 4 * 8; }  // [qb][rh][m][g][8] fp16 per wave
@@ -492,6 +495,10 @@ __device__ __forceinline__ void stage_in(const LayerArgs& a, const UnitInfo& ui,
           v1[t] = hv.y;
         }
       }
+      // the (rare) polling path ends with nothing of its own outstanding: otherwise the compiler,
+      // unsure whether a poll reload is still pending where the paths meet, waits for every memory
+      // operation of the wave (the prefetched quads included) before the registers are reused
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     }
   }
 #pragma unroll
@@ -902,24 +909,34 @@ __global__ __launch_bounds__(kLW * 64) void k4_layer_kernel(LayerArgs a) {
   __shared__ int32_t route_state;  // routing launches: 0 not started, 1 being computed, 2 ready
   bool have_plan = false;
   int units = 1;
-  UnitInfo shared_ui{min(256, a.experts - 1), a.rows, 0, 0, 0, a.rows};
-  if (a.route) {
-    // unit 0 (the shared expert) is known before routing: rows 0.., slots 9 r + 8
-    uint32_t tok = 0, s0 = 0, s1 = 0;
-    for (int t = 0; t < a.rows; t++) {
-      tok |= (uint32_t)t << (3 * t);
-      if (t < 4) s0 |= (uint32_t)(kSlots * t + 8) << (7 * t);
-      else s1 |= (uint32_t)(kSlots * t + 8) << (7 * (t - 4));
-    }
-    shared_ui.tok = tok;
-    shared_ui.sl0 = s0;
-    shared_ui.sl1 = s1;
-  } else {
+  if (!a.route) {
     units = load_plan(a.w.plan, plan_t);
     have_plan = true;
   }
   const float* score = a.route ? plan_t.score : a.scores;
-  auto unit_of = [&](int u) { return (u == 0 && a.route) ? shared_ui : unit_info(plan_t, u, a.experts, a.rows); };
+  // Unit 0 of a routing launch is the shared expert, known before routing: rows 0.., slots
+  // 9 r + 8.  Its fields are formed where they are used (a unit record kept in a variable that the
+  // lambdas share would live in private memory, and its loads would be flat loads, which wait for
+  // every outstanding memory operation of the wave).
+  auto unit_of = [&](int u) {
+    if (u == 0 && a.route) {
+      UnitInfo i;
+      i.e = min(256, a.experts - 1);
+      i.ntok = a.rows;
+      i.rows = a.rows;
+      uint32_t tok = 0, s0 = 0, s1 = 0;
+      for (int t = 0; t < a.rows; t++) {
+        tok |= (uint32_t)t << (3 * t);
+        if (t < 4) s0 |= (uint32_t)(kSlots * t + 8) << (7 * t);
+        else s1 |= (uint32_t)(kSlots * t + 8) << (7 * (t - 4));
+      }
+      i.tok = tok;
+      i.sl0 = s0;
+      i.sl1 = s1;
+      return i;
+    }
+    return unit_info(plan_t, u, a.experts, a.rows);
+  };
   // the item at sub-list position `sub`, if it is known without waiting (kind NONE otherwise); a
   // wave without the plan takes the block's table once it is complete in LDS, so a run of parts
   // goes on from the shared expert's parts into the routed ones without leaving its load pipeline
@@ -989,13 +1006,30 @@ __global__ __launch_bounds__(kLW * 64) void k4_layer_kernel(LayerArgs a) {
     }
   };
 
-  // The code table: every wave copies its share into LDS first, before any other memory traffic
-  // of the launch (which would slow the copy several-fold); the block then meets once.
-  __shared__ uint32_t epoch_lds;
+  // The launch's epoch (every wave reads it: a router item stores tagged words before the table is
+  // in LDS).
+  epoch = (uint32_t)__builtin_amdgcn_readfirstlane(ld_coh_i(a.w.flags + LF_EPOCH));
+  tag = epoch + 1u;
+  // Start-up.  Routing is the launch's first dependency chain (router items -> logits -> top-8 ->
+  // plan -> the routed experts' loads), the code table its first bulk copy.  A wave whose first
+  // item is a router item issues that item's loads ahead of its table share and finishes the item
+  // while the share is in flight; waves 1..kLW-1 then commit their shares and count them in
+  // `tab_ready`; wave 0 copies no share and, when its first item is a router item, finishes it and
+  // routes the block at once.  A wave waits for the whole table only when it is about to decode.
+  // With the layer's norm folded in, router items read the normalised row, which exists only after
+  // the block meets: that instantiation meets once after the norm and the table copy.
+  __shared__ int32_t tab_ready;
   if (threadIdx.x == 0) {
-    epoch_lds = (uint32_t)ld_coh_i(a.w.flags + LF_EPOCH);
     route_state = 0;
+    tab_ready = 0;
   }
+  __syncthreads();
+  int sub = first_sub;
+  Item first;
+  resolve(sub, first);  // positions before the plan's need none
+  const bool first_router = !NORM && first.kind == IT_ROUTER;
+  RouterLoads rl;
+  if (first_router) router_item_issue(a, first.a, L.S, rl);
   // The layer's residual add + RMSNorm (one row): waves 0..3 form the row's square sums exactly as
   // the norm kernel's four waves do, and after the block meets write h and the normalised row;
   // every block writes the same bits, so each block reads values its own stores put in its L2.
@@ -1021,29 +1055,51 @@ __global__ __launch_bounds__(kLW * 64) void k4_layer_kernel(LayerArgs a) {
       rms_row_store<4>(nh, nw, K, t, rms_inv(norm_red, a.h, a.eps), a.x_row);
     }
     copy_table_commit(share, tab, wv);
-  } else if (LTable<NT>::kF16) {
-    TableShare<131072, kLW> share;
-    copy_table_issue(share, a.tab16, wv);
-    copy_table_commit(share, tab, wv);
+    __syncthreads();
+  } else if (wv == 0) {
+    // wave 0 copies no share: when its first item is a router item (the case for every block of a
+    // routing launch at the GLM shape) it finishes the item and goes on to route the block at once
+    if (first_router) {
+      __builtin_amdgcn_s_setprio(3);
+      router_item_finish(a, first.a, L.S, tag, rl);
+      __builtin_amdgcn_s_setprio(0);
+    }
   } else {
-    TableShare<65536, kLW> share;
-    copy_table_issue(share, a.tab8, wv);
-    copy_table_commit(share, tab, wv);
+    TableShare<LTable<NT>::kBytes, kLW - 1> share;
+    copy_table_issue(share, LTable<NT>::kF16 ? (const void*)a.tab16 : (const void*)a.tab8, wv - 1);
+    if (first_router) {
+      __builtin_amdgcn_s_setprio(3);
+      router_item_finish(a, first.a, L.S, tag, rl);
+      __builtin_amdgcn_s_setprio(0);
+    }
+    copy_table_commit(share, tab, wv - 1);
+    // the share is in LDS (this wave's LDS stores complete in order) before it is counted
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    if (lane_id() == 0) __hip_atomic_fetch_add(&tab_ready, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
-  __syncthreads();
-  epoch = (uint32_t)__builtin_amdgcn_readfirstlane((int)epoch_lds);
-  tag = epoch + 1u;
-  int sub = first_sub;
-  Item first;
-  resolve(sub, first);
+  bool table_ok = NORM;
+  // before a wave first decodes: every share of the table (waves 1..kLW-1) is in LDS
+  auto wait_table = [&]() {
+    if (table_ok) return;
+    while (__builtin_amdgcn_readfirstlane(__hip_atomic_load(&tab_ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) <
+           kLW - 1)
+      __builtin_amdgcn_s_sleep(1);
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    table_ok = true;
+  };
   // Router items first.  The block's first wave done with one routes at once, before it claims
   // anything: a wave that routes holds no claimed item and the block's other waves keep claiming,
   // so the router items it waits for are always taken.
   bool route_now = false;
+  bool router_done = first_router;  // the first router item was finished during the table copy
   while (first.kind == IT_ROUTER) {
-    __builtin_amdgcn_s_setprio(3);
-    router_item(a, first.a, L.S, tag);
-    __builtin_amdgcn_s_setprio(0);
+    if (!router_done) {
+      __builtin_amdgcn_s_setprio(3);
+      router_item(a, first.a, L.S, tag);
+      __builtin_amdgcn_s_setprio(0);
+    }
+    router_done = false;
     if (!have_plan) {
       int old = 0;
       if (lane_id() == 0) {
@@ -1097,6 +1153,7 @@ __global__ __launch_bounds__(kLW * 64) void k4_layer_kernel(LayerArgs a) {
     const Item it = item_at(L, j, U);
     if (it.kind == IT_NONE) break;
     if (is_part(it)) {
+      wait_table();
       const UnitInfo ui = unit_of(it.u);
       load_quad(pc, quad_ptr(a, ui, it, 0));
       fetch_in<NT, kDPre>(a, ui, it, in);

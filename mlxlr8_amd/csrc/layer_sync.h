@@ -129,19 +129,35 @@ struct PlanLds {
 // ---------------------------------------------------------------- router
 // item r = e * S + j: partial logit of expert e over inputs [kRouterSlice j, kRouterSlice (j + 1))
 // for every row, stored tagged at logit_part[(row * S + j) * 256 + e].
+// The item in two halves: the loads of its weights and of row 0's inputs (issue), then the sums and
+// stores (finish), so a wave can put other loads in flight between them.
+constexpr int kRouterPer = kRouterSlice / 64;  // 16 inputs per lane
+struct RouterLoads {
+  f32x4 w[kRouterPer / 4];
+  u32x4 x0[kRouterPer / 8];
+};
 template <class A>
-__device__ __forceinline__ void router_item(const A& a, int r, int S, uint32_t tag) {
+__device__ __forceinline__ void router_item_issue(const A& a, int r, int S, RouterLoads& rl) {
+  const int e = r / S, j = r - e * S;
+  const int k0 = j * kRouterSlice + kRouterPer * cold_lane();
+#pragma unroll
+  for (int i = 0; i < kRouterPer / 4; i++)
+    rl.w[i] = *reinterpret_cast<const f32x4*>(a.router_w + (int64_t)e * a.h + k0 + 4 * i);
+#pragma unroll
+  for (int i = 0; i < kRouterPer / 8; i++) rl.x0[i] = *reinterpret_cast<const u32x4*>(a.x + k0 + 8 * i);
+}
+template <class A>
+__device__ __forceinline__ void router_item_finish(const A& a, int r, int S, uint32_t tag, const RouterLoads& rl) {
   const int e = r / S, j = r - e * S;
   const int lane = cold_lane();
-  constexpr int kPer = kRouterSlice / 64;  // 16 inputs per lane
+  constexpr int kPer = kRouterPer;
   const int k0 = j * kRouterSlice + kPer * lane;
-  f32x4 w[kPer / 4];
-#pragma unroll
-  for (int i = 0; i < kPer / 4; i++) w[i] = *reinterpret_cast<const f32x4*>(a.router_w + (int64_t)e * a.h + k0 + 4 * i);
   for (int row = 0; row < a.rows; row++) {
     u32x4 xv[kPer / 8];
 #pragma unroll
-    for (int i = 0; i < kPer / 8; i++) xv[i] = *reinterpret_cast<const u32x4*>(a.x + (int64_t)row * a.h + k0 + 8 * i);
+    for (int i = 0; i < kPer / 8; i++)
+      xv[i] = row == 0 ? rl.x0[i] : *reinterpret_cast<const u32x4*>(a.x + (int64_t)row * a.h + k0 + 8 * i);
+    const f32x4* w = rl.w;
     float acc = 0.0f;
 #pragma unroll
     for (int i = 0; i < kPer / 8; i++) {
@@ -158,6 +174,12 @@ __device__ __forceinline__ void router_item(const A& a, int r, int S, uint32_t t
     const float tot = wave_sum(acc);
     if (lane == 63) st_tag(a.w.logit_part + ((int64_t)row * S + j) * 256 + e, tot, tag);
   }
+}
+template <class A>
+__device__ __forceinline__ void router_item(const A& a, int r, int S, uint32_t tag) {
+  RouterLoads rl;
+  router_item_issue(a, r, S, rl);
+  router_item_finish(a, r, S, tag, rl);
 }
 
 // Routing of every row by one wave into its block's plan table: logits summed over their slices in
