@@ -114,7 +114,7 @@ int moe_router_logits(const uint16_t* x, const float* w, int rows, int hidden, i
 /* ---------------------------------------------------------------- K4 trellis */
 
 /* Decode expert `expert` of a packed trellis tensor to inner weights [in,out] as fp16 bits.
- * packed_bytes is the size of the whole tensor (all experts); k must be 4 in this build.
+ * packed_bytes is the size of the whole tensor (all experts); k is 2, 3 or 4.
  * Replaces: exlr8/trellis.py:199-214 dequantize_trellis (inner part; exlr8/metal/decode.metal). */
 int moe_trellis_decode_f16(const void* packed, int64_t packed_bytes, int k, int in_features, int out_features,
                            int side, int64_t expert, uint16_t* inner, moe_stream_t stream);
@@ -127,6 +127,12 @@ int moe_k4_expert_linear(const uint16_t* x, int x_per_slot, const uint32_t* ids,
                          const void* packed, int64_t packed_bytes, const uint16_t* in_scale,
                          const uint16_t* out_scale, int in_features, int out_features, int side, uint16_t* y,
                          void* workspace, size_t workspace_bytes, moe_stream_t stream);
+
+/* Typed SwiGLU of two bf16 arrays: out[i] = bf16(bf16(g * bf16(sigmoid(g))) * u) with g = gate[i],
+ * u = up[i]; n elements, all three arrays 16-byte aligned (out may alias gate or up).
+ * Replaces: the swiglu(gate, up) step between the expert linears of exlr8/experts.py:176-188
+ *           (mlx_lm.models.activations.swiglu; typed as exlr8/metal/fast_decode_common.metal:40-49). */
+int moe_swiglu_bf16(const uint16_t* gate, const uint16_t* up, int64_t n, uint16_t* out, moe_stream_t stream);
 
 /* Expert MLP over selected experts: values [rows, slots, h] bf16 (gate/up side 1, down side 2,
  * typed SwiGLU, A.5 cast points).  Arguments as moe_k4_expert_linear; scale pairs per projection.

@@ -29,6 +29,7 @@ _SIGNATURES = {
     "moe_route_f32": (_I32, [_VP, _VP, _I32, _VP, _VP, _VP]),
     "moe_router_logits": (_I32, [_VP, _VP, _I32, _I32, _I32, _VP, _VP]),
     "moe_trellis_decode_f16": (_I32, [_VP, _I64, _I32, _I32, _I32, _I32, _I64, _VP, _VP]),
+    "moe_swiglu_bf16": (_I32, [_VP, _VP, _I64, _VP, _VP]),
     "moe_k4_expert_linear": (_I32, [_VP, _I32, _VP, _I32, _I32, _VP, _I64, _VP, _VP, _I32, _I32, _I32, _VP,
                                     _VP, _SZ, _VP]),
     "moe_k4_mlp": (_I32, [_VP, _VP, _I32, _I32, _VP, _VP, _VP, _I64] + [_VP] * 6 + [_I32, _I32, _VP, _VP, _SZ, _VP]),

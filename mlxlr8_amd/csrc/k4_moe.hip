@@ -859,6 +859,28 @@ int launch_gemv(const GemvArgs& a, int max_ntok, int max_units, hipStream_t stre
   return MOE_OK;
 }
 
+// Typed SwiGLU over bf16 arrays, eight elements (16 bytes) per lane and step: the activation
+// between the separate gate/up and down expert linears (exlr8/experts.py:183).
+// Each element is read before it is written by the same lane, so out may alias gate or up.
+__global__ __launch_bounds__(256) void swiglu_bf16_kernel(const uint16_t* gate, const uint16_t* up, int64_t n,
+                                                          uint16_t* out) {
+  const int64_t vecs = n / 8;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; v < vecs; v += stride) {
+    const u32x4 g = *(const u32x4*)(gate + v * 8), u = *(const u32x4*)(up + v * 8);
+    u32x4 o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      o[j] = pack_bf16_pair(swiglu_bf16(bf16_to_f32((uint16_t)(g[j] & 0xFFFFu)), bf16_to_f32((uint16_t)(u[j] & 0xFFFFu))),
+                            swiglu_bf16(bf16_to_f32((uint16_t)(g[j] >> 16)), bf16_to_f32((uint16_t)(u[j] >> 16))));
+    *(u32x4*)(out + v * 8) = o;
+  }
+  if (blockIdx.x == 0 && threadIdx.x < n - vecs * 8) {
+    const int64_t i = vecs * 8 + threadIdx.x;
+    out[i] = f32_to_bf16(swiglu_bf16(bf16_to_f32(gate[i]), bf16_to_f32(up[i])));
+  }
+}
+
 int check_trellis(int64_t bytes, int in_f, int out_f, int64_t* experts) {
   MOE_ARG(in_f > 0 && out_f > 0 && in_f % 128 == 0 && out_f % 128 == 0,
           "trellis dimensions must be positive multiples of 128");
@@ -975,6 +997,19 @@ static int validate_ws(void* workspace, size_t bytes, int hidden, int inter) {
   MOE_ARG(workspace != nullptr, "workspace must not be NULL");
   const size_t need = carve(nullptr, hidden, inter).bytes;
   if (bytes < need) return fail(MOE_EWORKSPACE, "workspace too small: %zu < %zu bytes", bytes, need);
+  return MOE_OK;
+}
+
+int moe_swiglu_bf16(const uint16_t* gate, const uint16_t* up, int64_t n, uint16_t* out, moe_stream_t stream) {
+  MOE_ARG(n >= 0, "element count must not be negative");
+  if (n == 0) return MOE_OK;
+  MOE_ARG(gate && up && out, "gate, up and out must not be NULL");
+  MOE_ARG(((uintptr_t)gate | (uintptr_t)up | (uintptr_t)out) % 16 == 0, "bf16 arrays must be 16-byte aligned");
+  int rc = ensure_device_ready();
+  if (rc) return rc;
+  const int64_t blocks = std::min<int64_t>(std::max<int64_t>((n / 8 + 255) / 256, 1), 4096);
+  hipLaunchKernelGGL(swiglu_bf16_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, gate, up, n, out);
+  MOE_HIP(hipGetLastError());
   return MOE_OK;
 }
 

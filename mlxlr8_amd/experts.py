@@ -10,7 +10,7 @@ import torch
 
 from ._lib import check, lib, ptr, require_cuda, stream, workspace
 from .fast_decode import _weights, expert_values
-from .trellis import BF16, _check_format
+from .trellis import BF16, _check_format, expert_linear, swiglu
 
 
 class ExpertLayer:
@@ -42,12 +42,22 @@ class ExpertLayer:
         return _check_format(self.packed["gate"], self.k, self.hidden, self.intermediate, 1)
 
     def __call__(self, x, ids):
-        """values[*ids.shape, hidden] for the selected experts (exlr8/experts.py:150-188): up to 16
-        rows through the decode MLP, more through the grouped (sorted-by-expert) prefill MLP (K2/K3
-        experts take the grouped MLP at every row count)."""
+        """values[*ids.shape, hidden] for the selected experts (exlr8/experts.py:150-188).
+
+        With ``store.optimize`` (the default) up to 16 rows run through the decode MLP and more
+        through the grouped (sorted-by-expert) prefill MLP; K2/K3 experts take the grouped MLP at
+        every row count.  With ``store.optimize = False`` the layer runs the reference's plain
+        chain instead: gate and up expert linears, SwiGLU, down expert linear
+        (exlr8/experts.py:176-188)."""
         if self.affine is not None:
             return self.affine.slots(x, ids)
-        return expert_values(x, ids, self.packed, self.scales, self.k, self.hidden, self.intermediate)
+        if self.store.optimize:
+            return expert_values(x, ids, self.packed, self.scales, self.k, self.hidden, self.intermediate)
+        gate, up = (expert_linear(x, ids, self.packed[p], *self.scales[p], self.k, self.hidden, self.intermediate, 1)
+                    for p in ("gate", "up"))
+        hidden = swiglu(gate, up)
+        return expert_linear(hidden, ids, self.packed["down"], *self.scales["down"], self.k, self.intermediate,
+                             self.hidden, 2)
 
     def decode_block(self, x, residual, router_weight, bias):
         """Router GEMV + route + expert MLP + combine in one C call (decode batches, <= 8 rows).

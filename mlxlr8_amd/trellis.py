@@ -74,9 +74,21 @@ def dequantize_trellis(packed, suh, svh, k, in_features, out_features, sharded_s
     """
     if _check_format(packed, k, in_features, out_features, sharded_side) != 1:
         raise ValueError("dense dequantization requires one matrix")
-    inner = decode_inner(packed, k, in_features, out_features, sharded_side).float()
-    weight = _block_hadamard(_block_hadamard(inner, 0).T.contiguous(), 1)
+    inner = decode_inner(packed, k, in_features, out_features, sharded_side).float()    # [in, out]
+    # H128 along the output axis, transpose to [out, in], then H128 along the input axis
+    weight = _block_hadamard(_block_hadamard(inner, 1).T.contiguous(), 1)
     return weight * svh.float()[:, None] * suh.float()[None, :]
+
+
+def swiglu(gate, up):
+    """Typed SwiGLU of two bf16 tensors of one shape (the activation of exlr8/experts.py:183)."""
+    if gate.shape != up.shape or gate.dtype != BF16 or up.dtype != BF16:
+        raise ValueError("swiglu takes two bf16 tensors of one shape")
+    require_cuda(gate, up)
+    gate, up = gate.contiguous(), up.contiguous()
+    out = torch.empty_like(gate)
+    check(lib().moe_swiglu_bf16(ptr(gate), ptr(up), gate.numel(), ptr(out), stream(gate.device)))
+    return out
 
 
 def _rows_for(x, indices, in_features):

@@ -1,7 +1,8 @@
 """Independent numpy restatements used to pin the oracle (not the oracle's own formulas).
 
-* codebook_integer: the integer half-bit rounding of tests/test_fast_decode.py:43-53
-  (a different rounding route from the oracle's nearest-level search).
+* codebook_frexp: the K4 codebook (exlr8/trellis.py:22-50) as hash -> fp16 half sum -> E4M3
+  rounding, with the rounding done through frexp/ldexp in float64 (a different route from the
+  oracle's nearest-level search).
 * pack_k4 / pack_trellis: MSB-first bit packing per ponyexl3/ref/trellis.py:13-49 semantics.
 * tensor_core_perm: ponyexl3/ref/perm.py:8-26 as an explicit table.
 * hadamard_matrix: the Sylvester definition H[i,j] = (-1)^popcount(i&j) / sqrt(128).
@@ -9,17 +10,25 @@
 import numpy as np
 
 
-def codebook_integer():
-    states = np.arange(65536, dtype=np.uint32)
-    product = ((states * np.uint32(0xCBAC1FED)) & np.uint32(0x8FFF8FFF)) ^ np.uint32(0x3B603B60)
-    summed = (product & 65535).astype(np.uint16).view(np.float16)
-    summed = summed + (product >> 16).astype(np.uint16).view(np.float16)
-    bits = summed.view(np.uint16).astype(np.uint32)
-    magnitude = bits & 32767
-    rounded = (bits + 63 + ((bits >> 7) & 1)) & 65408
-    normal = rounded.astype(np.uint16).view(np.float16)
-    values = np.where(magnitude < 0x2400, np.rint(summed.astype(np.float32) * 512) / 512, normal)
-    return values.astype(np.float16)
+def _halves_sum(states):
+    """fp16(lo + hi) of the masked MCG hash of each 16-bit state."""
+    word = (np.asarray(states, np.uint64) * 0xCBAC1FED) % (1 << 32)
+    word = (word & 0x8FFF8FFF) ^ 0x3B603B60
+    lo = (word & 0xFFFF).astype(np.uint16).view(np.float16)
+    hi = (word >> 16).astype(np.uint16).view(np.float16)
+    return lo + hi  # numpy adds two float16 arrays with one fp16 rounding
+
+
+def round_e4m3_frexp(v):
+    """Round float values to E4M3 (3 mantissa bits, minimum normal exponent -6, ties to even)."""
+    v = np.asarray(v, np.float64)
+    _, e = np.frexp(np.abs(v))                   # |v| = m * 2**e with m in [0.5, 1)
+    quantum = np.ldexp(1.0, np.maximum(e - 1, -6) - 3)
+    return np.copysign(np.round(np.abs(v) / quantum) * quantum, v)   # np.round is half-to-even
+
+
+def codebook_frexp():
+    return round_e4m3_frexp(_halves_sum(np.arange(1 << 16))).astype(np.float16)
 
 
 def pack_trellis(values, k):

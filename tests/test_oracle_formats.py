@@ -16,9 +16,15 @@ def test_codebook_known_answers(orc):
     assert cb[3] == np.float16(0.8125) and cb[65535] == np.float16(0.875)
 
 
-def test_codebook_matches_integer_rounding_restatement(orc):
-    # independent route: integer half-bit rounding (tests/test_fast_decode.py:43-53)
-    np.testing.assert_array_equal(orc.codebook().view(np.uint16), refmath.codebook_integer().view(np.uint16))
+def test_codebook_matches_frexp_restatement(orc):
+    # independent route: E4M3 rounding through frexp/ldexp (exlr8/trellis.py:22-50 defines the codebook)
+    np.testing.assert_array_equal(orc.codebook().view(np.uint16), refmath.codebook_frexp().view(np.uint16))
+
+
+def test_frexp_rounding_catches_planted_mistakes():
+    # the restatement itself: ties go to even, the subnormal quantum is 2**-9, signs survive
+    got = refmath.round_e4m3_frexp([1.0625, 1.1875, 2.0 ** -9 * 1.5, -0.3, 0.0, 3.0 * 2 ** -10])
+    np.testing.assert_array_equal(got, [1.0, 1.25, 2.0 ** -8, -0.3125, 0.0, 2.0 ** -8])
 
 
 def test_codebook_digest_and_e4m3_property(orc):
