@@ -15,11 +15,13 @@ def say(*a):
     sys.stdout.flush()
 
 
-def _layer(cuda, experts, seed):
+def _layer(cuda, experts, seed, edit_scales=None):
     from mlxlr8_amd import synth
     from mlxlr8_amd.joined_mxfp4 import JoinedMXFP4
     L = synth.mxfp4_layer(cuda, seed, experts=experts)
     (gc, gs), (dc, ds) = L["weights"]["gate_up"], L["weights"]["down"]
+    if edit_scales is not None:
+        edit_scales(gs, ds)
     side = L["side"]
     joined = JoinedMXFP4(L["weights"], L["unit"],
                          {"gate": (None, side["out_gate"]), "up": (None, side["out_up"]),
@@ -139,3 +141,34 @@ def test_mxfp4_fused_block_equals_three_launch_path(cuda):
         same = torch.equal(out.view(torch.int16), ref.view(torch.int16))
         say(f"  seed={seed} ids={ids.cpu().numpy().tolist()} identical={same}")
         assert same
+
+
+def test_mxfp4_fused_block_scales_outside_exact_window(cuda, orc):
+    """e8m0 scale bytes far from the synthetic layers' (whose fp16 widening, as in the grouped
+    prefill GEMMs, would overflow or flush): gate/up groups at 2^14 dominate their rows, down groups
+    at 2^-14 and 2^14 mix with ordinary ones; the one-row block (fp32 products for every scale)
+    still matches the oracle."""
+    from mlxlr8_amd import synth
+
+    def edit(gs, ds):
+        r = torch.arange(gs.shape[1], device=gs.device)[:, None]
+        g = torch.arange(gs.shape[2], device=gs.device)[None, :]
+        gs[:, (r + g) % 13 == 0] = 141
+        r = torch.arange(ds.shape[1], device=ds.device)[:, None]
+        g = torch.arange(ds.shape[2], device=ds.device)[None, :]
+        ds[:, (3 * r + g) % 11 == 0] = 113
+        ds[:, (r + 2 * g) % 17 == 0] = 141
+
+    say("case: mxfp4 fused block, scales outside the exact window")
+    joined, host = _layer(cuda, 257, 7171, edit)
+    assert not joined.grouped_exact
+    w, bias = synth.router(cuda, 7171)
+    x, res = synth.activations(cuda, 7172, 1)
+    out, ids, scores = joined.decode_block(x, res, w, bias)
+    torch.cuda.synchronize()
+    want, _ = _oracle(orc, host, x, ids.cpu().numpy(), scores.cpu().numpy(), bf16_bits(res))
+    got = bits_to_f32(bf16_bits(out))
+    r = bits_to_f32(bf16_bits(res))
+    err, err_moe = rel_l2(got, bits_to_f32(want)), rel_l2(got - r, bits_to_f32(want) - r)
+    say(f"  rel_l2={err:.3e} moe-part={err_moe:.3e} max|out|={np.abs(got).max():.3e}")
+    assert np.isfinite(got).all() and err <= 1e-3 and err_moe <= 1e-3
