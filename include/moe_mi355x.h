@@ -165,6 +165,33 @@ int moe_k4_moe_decode(const uint16_t* x, const uint16_t* residual, int rows, con
                       const uint16_t* out_down, int hidden, int intermediate, uint16_t* out, uint32_t* indices,
                       float* scores, void* workspace, size_t workspace_bytes, moe_stream_t stream);
 
+/* The three decode entries above for K-bit trellis experts, k = 3 or 4 (k = 4 is the K4 entry
+ * itself): the same fused block, arguments and workspace, with packed_bytes a multiple of
+ * hidden * intermediate * k / 8.  A K3 tile is 24 words; each lane reads 12 B of it and takes its 32
+ * codewords as the 16-bit windows that end every 3 bits of its stream (one funnel shift each).
+ * K2 experts take the grouped entries (moe_trellis_grouped_mlp) at every row count.
+ * Replaces: exlr8/fast_decode.py:208-221 fast_expert_mlp and :224-244 compiled_expert_mlp_finish with
+ *           k = 3 (the multi-token-prediction layer's experts, exlr8/experts.py:86,170-173; the
+ *           generic window of exlr8/metal/fast_decode_linear.metal:77-90), and
+ *           exlr8/fast_router.py:27-37 compiled_finish for those experts. */
+int moe_trellis_mlp(int k, const uint16_t* x, const uint32_t* ids, int rows, int slots, const void* packed_gate,
+                    const void* packed_up, const void* packed_down, int64_t packed_bytes, const uint16_t* in_gate,
+                    const uint16_t* out_gate, const uint16_t* in_up, const uint16_t* out_up, const uint16_t* in_down,
+                    const uint16_t* out_down, int hidden, int intermediate, uint16_t* values, void* workspace,
+                    size_t workspace_bytes, moe_stream_t stream);
+int moe_trellis_mlp_finish(int k, const uint16_t* x, const uint32_t* ids, const float* scores,
+                           const uint16_t* residual, int rows, const void* packed_gate, const void* packed_up,
+                           const void* packed_down, int64_t packed_bytes, const uint16_t* in_gate,
+                           const uint16_t* out_gate, const uint16_t* in_up, const uint16_t* out_up,
+                           const uint16_t* in_down, const uint16_t* out_down, int hidden, int intermediate,
+                           uint16_t* out, void* workspace, size_t workspace_bytes, moe_stream_t stream);
+int moe_trellis_moe_decode(int k, const uint16_t* x, const uint16_t* residual, int rows, const float* router_w,
+                           const float* bias, const void* packed_gate, const void* packed_up, const void* packed_down,
+                           int64_t packed_bytes, const uint16_t* in_gate, const uint16_t* out_gate,
+                           const uint16_t* in_up, const uint16_t* out_up, const uint16_t* in_down,
+                           const uint16_t* out_down, int hidden, int intermediate, uint16_t* out, uint32_t* indices,
+                           float* scores, void* workspace, size_t workspace_bytes, moe_stream_t stream);
+
 /* Residual add + RMSNorm of decode rows: h = T(x + residual) (residual may be NULL: h = x),
  * out = T(w * T(h * rsqrt(mean(h^2) + eps))), T = bf16, x/residual/h_out/out [rows, n], w [n];
  * h_out may be NULL.  n a multiple of 2048 up to 8192.

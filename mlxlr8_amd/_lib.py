@@ -37,6 +37,12 @@ _SIGNATURES = {
                           + [_I32, _I32, _VP, _VP, _SZ, _VP]),
     "moe_k4_moe_decode": (_I32, [_VP, _VP, _I32, _VP, _VP, _VP, _VP, _VP, _I64] + [_VP] * 6
                           + [_I32, _I32, _VP, _VP, _VP, _VP, _SZ, _VP]),
+    "moe_trellis_mlp": (_I32, [_I32, _VP, _VP, _I32, _I32, _VP, _VP, _VP, _I64] + [_VP] * 6
+                        + [_I32, _I32, _VP, _VP, _SZ, _VP]),
+    "moe_trellis_mlp_finish": (_I32, [_I32, _VP, _VP, _VP, _VP, _I32, _VP, _VP, _VP, _I64] + [_VP] * 6
+                               + [_I32, _I32, _VP, _VP, _SZ, _VP]),
+    "moe_trellis_moe_decode": (_I32, [_I32, _VP, _VP, _I32, _VP, _VP, _VP, _VP, _VP, _I64] + [_VP] * 6
+                               + [_I32, _I32, _VP, _VP, _VP, _VP, _SZ, _VP]),
     "moe_k4_layer_decode": (_I32, [_VP, _VP, _VP, ctypes.c_float, _I32, _VP, _VP, _VP, _VP, _VP, _I64] + [_VP] * 6
                             + [_I32, _I32, _VP, _VP, _VP, _VP, _SZ, _VP]),
     "moe_residual_rmsnorm": (_I32, [_VP, _VP, _VP, _I32, _I32, ctypes.c_float, _VP, _VP, _VP]),

@@ -69,6 +69,14 @@ namespace moe {
 #define MOE_LAYER_ALU_ODD 2
 #endif
 
+// arithmetic codeword pairs per word (even, odd words of a piece) in the K3 decode
+#ifndef MOE_LAYER3_ALU_EVEN
+#define MOE_LAYER3_ALU_EVEN 2
+#endif
+#ifndef MOE_LAYER3_ALU_ODD
+#define MOE_LAYER3_ALU_ODD 2
+#endif
+
 // longest pause (in 64-clock sleeps) of the finishes' and staging waits: they sit on the launch's
 // final dependency chain, so a wait must not oversleep the value it waits for by long
 #ifndef MOE_LAYER_WAIT
@@ -112,6 +120,7 @@ struct LayerArgs {
   const uint16_t* x;         // expert (and router) input [rows, h] bf16
   const uint16_t* residual;  // [rows, h] bf16 (combine)
   int rows;
+  int bits;                  // trellis width of the experts (3 or 4)
   int route;                 // 1: router items + plan on the device; 0: plan prebuilt from ids
   const float* router_w;     // [256, h] fp32
   const float* bias;         // [256] fp32
@@ -381,7 +390,10 @@ __device__ __forceinline__ uint64_t* part_ptr(const LayerArgs& a, int slot, int 
 }
 
 // ---------------------------------------------------------------- one part: operands
-// The wave's 16 B of quad qb (0, 1) of a part: lane piece of set s4 at +256 s4.
+// The wave's piece of quad qb (0, 1) of a part, K-bit tiles: 8 consecutive tiles (8K words each)
+// per chunk; lane nn takes tile nn / 8 of the first two, piece nn % 8, and set s4 the next two.
+// K4: 16 B pieces, sets at +256 B; K3: 12 B pieces, sets at +192 B.
+template <int KB>
 __device__ __forceinline__ const uint8_t* quad_ptr(const LayerArgs& a, const UnitInfo& ui, const Item& it, int qb) {
   const int lane = lane_id();
   const int g = lane >> 4, nn = lane & 15;
@@ -390,12 +402,22 @@ __device__ __forceinline__ const uint8_t* quad_ptr(const LayerArgs& a, const Uni
   const int in_f = gu ? a.h : a.m;
   const int it_tiles = in_f / 16, obs = gu ? a.m / 128 : a.h / 128;
   const uint8_t* base = a.packed[gu ? it.b : 2];
-  return base + chunk_offset(side, (uint64_t)ui.e, it.a, 8 * it.c + 4 * qb + g, it_tiles, obs) +
-         (nn >> 3) * 128 + (nn & 7) * 16;
+  return base + chunk_index(side, (uint64_t)ui.e, it.a, 8 * it.c + 4 * qb + g, it_tiles, obs) * (uint64_t)(256 * KB) +
+         (nn >> 3) * (32 * KB) + (nn & 7) * (4 * KB);
 }
+template <int KB>
 __device__ __forceinline__ void load_quad(u32x4 (&pc)[4], const uint8_t* qp) {
+  if constexpr (KB == 4) {
 #pragma unroll
-  for (int s4 = 0; s4 < 4; s4++) pc[s4] = load_stream16(qp + 256 * s4);
+    for (int s4 = 0; s4 < 4; s4++) pc[s4] = load_stream16(qp + 256 * s4);
+  } else {
+    static_assert(KB == 3, "the fused block decodes K3 and K4 tiles");
+#pragma unroll
+    for (int s4 = 0; s4 < 4; s4++) {
+      const uint32_t* w = reinterpret_cast<const uint32_t*>(qp + 192 * s4);
+      pc[s4] = u32x4{__builtin_nontemporal_load(w), __builtin_nontemporal_load(w + 1), __builtin_nontemporal_load(w + 2), 0u};
+    }
+  }
 }
 // The raw input block of a part, fetched ahead of its staging.
 //   DPRE (one token): both kinds issue two 64-bit loads into r[0..1] and r[2..3] -- gate/up the
@@ -543,7 +565,7 @@ __device__ __forceinline__ void stage_in(const LayerArgs& a, const UnitInfo& ui,
 }
 // Decode one quad held in pc (the pieces' predecessor words come from the neighbouring lane) and
 // accumulate it on the matrix cores against the staged A fragments of quad qb.
-template <int NT>
+template <int NT, int KB>
 __device__ __forceinline__ void decode_quad(const u32x4 (&pc)[4], int qb, int ntok, const uint8_t* __restrict__ tab,
                                             const _Float16* __restrict__ xw, f32x4 (&acc)[4][2]) {
   const int lane = lane_id();
@@ -557,18 +579,26 @@ __device__ __forceinline__ void decode_quad(const u32x4 (&pc)[4], int qb, int nt
                  : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
   uint32_t prior[4];
 #pragma unroll
-  for (int s4 = 0; s4 < 4; s4++) prior[s4] = (uint32_t)__shfl((int)pc[s4].w, src_lane, 64);
+  for (int s4 = 0; s4 < 4; s4++) prior[s4] = (uint32_t)__shfl((int)(KB == 4 ? pc[s4].w : pc[s4].z), src_lane, 64);
 #pragma unroll
   for (int s4 = 0; s4 < 4; s4++) {
     const u32x4 v = pc[s4];
 #pragma unroll
     for (int rh = 0; rh < 2; rh++) {
       f16x2 q[2][4];
-      const uint32_t w0 = rh ? v.z : v.x, w1 = rh ? v.w : v.y, p0 = rh ? v.y : prior[s4];
-      if (LTable<NT>::kF16)
-        decode_pair_words_f16<MOE_LAYER_ALU_EVEN, MOE_LAYER_ALU_ODD, true>(w0, w1, p0, tab, q);
-      else
-        decode_pair_words_f16<MOE_LAYER8_ALU_EVEN, MOE_LAYER8_ALU_ODD, false>(w0, w1, p0, tab, q);
+      if constexpr (KB == 3) {
+        const uint32_t S[4] = {prior[s4], v.x, v.y, v.z};
+        if (rh == 0)
+          decode_k3_pair_words<MOE_LAYER3_ALU_EVEN, MOE_LAYER3_ALU_ODD, 0>(S, tab, q);
+        else
+          decode_k3_pair_words<MOE_LAYER3_ALU_EVEN, MOE_LAYER3_ALU_ODD, 2>(S, tab, q);
+      } else {
+        const uint32_t w0 = rh ? v.z : v.x, w1 = rh ? v.w : v.y, p0 = rh ? v.y : prior[s4];
+        if (LTable<NT>::kF16)
+          decode_pair_words_f16<MOE_LAYER_ALU_EVEN, MOE_LAYER_ALU_ODD, true>(w0, w1, p0, tab, q);
+        else
+          decode_pair_words_f16<MOE_LAYER8_ALU_EVEN, MOE_LAYER8_ALU_ODD, false>(w0, w1, p0, tab, q);
+      }
       const f16x8 b0 = frag(q[0][0], q[0][1], q[1][0], q[1][1]);
       const f16x8 b1 = frag(q[0][2], q[0][3], q[1][2], q[1][3]);
       acc[s4][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[rh], b0, acc[s4][0], 0, 0, 0);
@@ -872,7 +902,7 @@ __device__ __forceinline__ void copy_table_commit(const TableShare<BYTES, SHARES
 // ---------------------------------------------------------------- the kernel
 // NORM (one row): the launch first forms the layer's residual add + RMSNorm (a separate
 // instantiation, so that the plain one keeps its start unchanged)
-template <int NT, bool NORM>
+template <int NT, bool NORM, int KB>
 __global__ __launch_bounds__(kLW * 64) void k4_layer_kernel(LayerArgs a) {
   constexpr bool kDPre = NT == 1;  // down inputs fetched ahead (registers allow it for one token)
   __shared__ __attribute__((aligned(16))) uint8_t tab[LTable<NT>::kBytes];
@@ -977,7 +1007,7 @@ __global__ __launch_bounds__(kLW * 64) void k4_layer_kernel(LayerArgs a) {
       else
         __builtin_amdgcn_s_setprio(0);
       u32x4 pn[4];
-      load_quad(pn, quad_ptr(a, ui, it, 1));
+      load_quad<KB>(pn, quad_ptr<KB>(a, ui, it, 1));
       // the next item is claimed once this one can no longer wait (a claimed item is only started
       // by its claimer); the claim's round trip is hidden by quad 0
       const int claimed = claim_issue();
@@ -986,7 +1016,7 @@ __global__ __launch_bounds__(kLW * 64) void k4_layer_kernel(LayerArgs a) {
       for (int s4 = 0; s4 < 4; s4++)
 #pragma unroll
         for (int hh = 0; hh < 2; hh++) acc[s4][hh] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      decode_quad<NT>(pc, 0, ui.ntok, tab, xw, acc);
+      decode_quad<NT, KB>(pc, 0, ui.ntok, tab, xw, acc);
       const int nsub = claim_take(claimed);
       Item nit;
       resolve(nsub, nit);
@@ -996,9 +1026,9 @@ __global__ __launch_bounds__(kLW * 64) void k4_layer_kernel(LayerArgs a) {
       const bool more = is_part(nit);
       const Item pit = more ? nit : it;
       const UnitInfo pui = unit_of(pit.u);
-      load_quad(pc, quad_ptr(a, pui, pit, 0));
+      load_quad<KB>(pc, quad_ptr<KB>(a, pui, pit, 0));
       fetch_in<NT, kDPre>(a, pui, pit, in);
-      decode_quad<NT>(pn, 1, ui.ntok, tab, xw, acc);
+      decode_quad<NT, KB>(pn, 1, ui.ntok, tab, xw, acc);
       store_partials<NT>(a, ui, it, acc, tag, L, pst_all + (NT == 1 ? wv * 128 : 0), scale);
       sub = nsub;
       if (!more) return;
@@ -1155,7 +1185,7 @@ __global__ __launch_bounds__(kLW * 64) void k4_layer_kernel(LayerArgs a) {
     if (is_part(it)) {
       wait_table();
       const UnitInfo ui = unit_of(it.u);
-      load_quad(pc, quad_ptr(a, ui, it, 0));
+      load_quad<KB>(pc, quad_ptr<KB>(a, ui, it, 0));
       fetch_in<NT, kDPre>(a, ui, it, in);
       // the run's first part waits for its operands here, so nothing is pending on entry: without
       // this the compiler merges the entry (input block just requested) into the loop's state and
@@ -1270,12 +1300,19 @@ static int k4_layer_launch(LayerArgs a, void* workspace, hipStream_t s) {
   if (!a.tab8 || !a.tab16) return fail(MOE_ENOTSUP, "code tables are not initialised on this device");
   // every sub-list (blockIdx mod kXcds) needs a block to serve it
   const int grid = device_cus() > kXcds ? device_cus() : kXcds;
-  if (a.rows <= 1 && a.norm_x)
-    hipLaunchKernelGGL((k4_layer_kernel<1, true>), dim3(grid), dim3(kLW * 64), 0, s, a);
-  else if (a.rows <= 1)
-    hipLaunchKernelGGL((k4_layer_kernel<1, false>), dim3(grid), dim3(kLW * 64), 0, s, a);
-  else
-    hipLaunchKernelGGL((k4_layer_kernel<kMaxRows, false>), dim3(grid), dim3(kLW * 64), 0, s, a);
+  if (a.bits == 3) {
+    if (a.norm_x) return fail(MOE_ENOTSUP, "the fused residual + RMSNorm is built for K4 experts only");
+    if (a.rows <= 1)
+      hipLaunchKernelGGL((k4_layer_kernel<1, false, 3>), dim3(grid), dim3(kLW * 64), 0, s, a);
+    else
+      hipLaunchKernelGGL((k4_layer_kernel<kMaxRows, false, 3>), dim3(grid), dim3(kLW * 64), 0, s, a);
+  } else if (a.rows <= 1 && a.norm_x) {
+    hipLaunchKernelGGL((k4_layer_kernel<1, true, 4>), dim3(grid), dim3(kLW * 64), 0, s, a);
+  } else if (a.rows <= 1) {
+    hipLaunchKernelGGL((k4_layer_kernel<1, false, 4>), dim3(grid), dim3(kLW * 64), 0, s, a);
+  } else {
+    hipLaunchKernelGGL((k4_layer_kernel<kMaxRows, false, 4>), dim3(grid), dim3(kLW * 64), 0, s, a);
+  }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail((int)e, "launch of the fused K4 block failed: %s", hipGetErrorString(e));
   return MOE_OK;
@@ -1284,7 +1321,9 @@ static int k4_layer_launch(LayerArgs a, void* workspace, hipStream_t s) {
 int k4_layer_run(const uint16_t* x, const uint16_t* residual, int rows, int route, const float* router_w,
                  const float* bias, uint32_t* ids, float* scores, const uint8_t* const packed[3],
                  const uint16_t* const in_scale[3], const uint16_t* const out_scale[3], int h, int m, int experts,
-                 int combine, uint16_t* out, uint16_t* values, void* layer_ws, hipStream_t s, const LayerNorm* norm) {
+                 int combine, uint16_t* out, uint16_t* values, void* layer_ws, hipStream_t s, const LayerNorm* norm,
+                 int bits) {
+  if (bits != 3 && bits != 4) return fail(MOE_EINVAL, "the fused block decodes K3 and K4 experts (got k=%d)", bits);
   if (!k4_layer_supported(h, m, route != 0))
     return fail(MOE_ENOTSUP, "the fused K4 block needs hidden a multiple of %d%s and intermediate a multiple of 128 "
                 "(got %d, %d)", route ? kRouterSlice : 128, route ? " up to 8192 (fused router)" : "", h, m);
@@ -1294,6 +1333,7 @@ int k4_layer_run(const uint16_t* x, const uint16_t* residual, int rows, int rout
   a.x = x;
   a.residual = residual;
   a.rows = rows;
+  a.bits = bits;
   a.route = route;
   a.router_w = router_w;
   a.bias = bias;

@@ -881,6 +881,16 @@ __global__ __launch_bounds__(256) void swiglu_bf16_kernel(const uint16_t* gate, 
   }
 }
 
+// K-bit trellis tensors: h * m * k / 8 bytes per expert
+int check_trellis_k(int64_t bytes, int k, int in_f, int out_f, int64_t* experts) {
+  MOE_ARG(in_f > 0 && out_f > 0 && in_f % 128 == 0 && out_f % 128 == 0,
+          "trellis dimensions must be positive multiples of 128");
+  const int64_t size = (int64_t)in_f * out_f * k / 8;
+  MOE_ARG(bytes > 0 && bytes % size == 0, "packed byte count does not match the trellis dimensions");
+  *experts = bytes / size;
+  return MOE_OK;
+}
+
 int check_trellis(int64_t bytes, int in_f, int out_f, int64_t* experts) {
   MOE_ARG(in_f > 0 && out_f > 0 && in_f % 128 == 0 && out_f % 128 == 0,
           "trellis dimensions must be positive multiples of 128");
@@ -1057,13 +1067,15 @@ static int k4_block(const uint16_t* x, const uint16_t* attn, const uint16_t* nor
                     const void* pu, const void* pd, int64_t bytes, const uint16_t* in_g, const uint16_t* out_g,
                     const uint16_t* in_u, const uint16_t* out_u, const uint16_t* in_d, const uint16_t* out_d, int h,
                     int m, uint16_t* out, uint32_t* indices, float* scores, void* workspace, size_t workspace_bytes,
-                    hipStream_t s) {
+                    hipStream_t s, int bits = 4) {
   MOE_ARG(x && router_w && bias && out && pg && pu && pd && in_g && out_g && in_u && out_u && in_d && out_d,
           "null pointer argument");
   MOE_ARG(norm_w || residual, "null pointer argument");
   MOE_ARG(rows >= 1 && rows <= kMaxRows, "rows must be in 1..%d", kMaxRows);
+  MOE_ARG(bits == 3 || bits == 4, "the decode block takes K3 or K4 experts (got k=%d)", bits);
+  MOE_ARG(bits == 4 || !norm_w, "the fused residual + RMSNorm is built for K4 experts only");
   int64_t experts = 0;
-  int rc = check_trellis(bytes, h, m, &experts);
+  int rc = check_trellis_k(bytes, bits, h, m, &experts);
   if (rc) return rc;
   MOE_ARG(experts == 257, "the routed decode block needs 256 routed experts plus the shared expert (got %lld)",
           (long long)experts);
@@ -1097,7 +1109,7 @@ static int k4_block(const uint16_t* x, const uint16_t* attn, const uint16_t* nor
   const uint16_t* outs[3] = {out_g, out_u, out_d};
   prof_mark(1, s);
   rc = k4_layer_run(xin, res, rows, 1, router_w, bias, ids, sc, packed, ins, outs, h, m, 257, 1, out, nullptr,
-                    w.layer, s, fold ? &ln : nullptr);
+                    w.layer, s, fold ? &ln : nullptr, bits);
   prof_mark(3, s);
   return rc;
 }
@@ -1106,12 +1118,13 @@ static int k4_mlp_common(const uint16_t* x, const uint32_t* ids, const float* sc
                          int rows, int slots, const void* pg, const void* pu, const void* pd, int64_t bytes,
                          const uint16_t* in_g, const uint16_t* out_g, const uint16_t* in_u, const uint16_t* out_u,
                          const uint16_t* in_d, const uint16_t* out_d, int h, int m, uint16_t* values, uint16_t* out,
-                         void* workspace, size_t workspace_bytes, hipStream_t s) {
+                         void* workspace, size_t workspace_bytes, hipStream_t s, int bits = 4) {
   MOE_ARG(x && ids && pg && pu && pd && in_g && out_g && in_u && out_u && in_d && out_d, "null pointer argument");
   MOE_ARG(rows >= 1 && rows <= kMaxRows && slots >= 1 && slots <= kSlots,
           "rows must be in 1..%d and slots in 1..%d", kMaxRows, kSlots);
+  MOE_ARG(bits == 3 || bits == 4, "the decode MLP takes K3 or K4 experts (got k=%d)", bits);
   int64_t experts = 0;
-  int rc = check_trellis(bytes, h, m, &experts);
+  int rc = check_trellis_k(bytes, bits, h, m, &experts);
   if (rc) return rc;
   MOE_ARG(experts >= 1, "no experts");
   MOE_ARG(k4_layer_supported(h, m, false), "hidden and intermediate must be multiples of 128 (got %d, %d)", h, m);
@@ -1134,7 +1147,7 @@ static int k4_mlp_common(const uint16_t* x, const uint32_t* ids, const float* sc
   const uint16_t* outs[3] = {out_g, out_u, out_d};
   prof_mark(1, s);
   rc = k4_layer_run(x, residual, rows, 0, nullptr, nullptr, nullptr, const_cast<float*>(scores), packed, ins, outs, h,
-                    m, ecount, out != nullptr, out, values, w.layer, s);
+                    m, ecount, out != nullptr, out, values, w.layer, s, nullptr, bits);
   prof_mark(3, s);
   return rc;
 }
@@ -1171,6 +1184,40 @@ int moe_k4_moe_decode(const uint16_t* x, const uint16_t* residual, int rows, con
   return k4_block(x, nullptr, nullptr, 0.0f, residual, rows, router_w, bias, packed_gate, packed_up, packed_down,
                   packed_bytes, in_gate, out_gate, in_up, out_up, in_down, out_down, hidden, intermediate, out, indices,
                   scores, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int moe_trellis_mlp(int k, const uint16_t* x, const uint32_t* ids, int rows, int slots, const void* packed_gate,
+                    const void* packed_up, const void* packed_down, int64_t packed_bytes, const uint16_t* in_gate,
+                    const uint16_t* out_gate, const uint16_t* in_up, const uint16_t* out_up, const uint16_t* in_down,
+                    const uint16_t* out_down, int hidden, int intermediate, uint16_t* values, void* workspace,
+                    size_t workspace_bytes, moe_stream_t stream) {
+  MOE_ARG(values != nullptr, "values must not be NULL");
+  return k4_mlp_common(x, ids, nullptr, nullptr, rows, slots, packed_gate, packed_up, packed_down, packed_bytes,
+                       in_gate, out_gate, in_up, out_up, in_down, out_down, hidden, intermediate, values, nullptr,
+                       workspace, workspace_bytes, (hipStream_t)stream, k);
+}
+
+int moe_trellis_mlp_finish(int k, const uint16_t* x, const uint32_t* ids, const float* scores,
+                           const uint16_t* residual, int rows, const void* packed_gate, const void* packed_up,
+                           const void* packed_down, int64_t packed_bytes, const uint16_t* in_gate,
+                           const uint16_t* out_gate, const uint16_t* in_up, const uint16_t* out_up,
+                           const uint16_t* in_down, const uint16_t* out_down, int hidden, int intermediate,
+                           uint16_t* out, void* workspace, size_t workspace_bytes, moe_stream_t stream) {
+  MOE_ARG(out != nullptr, "out must not be NULL");
+  return k4_mlp_common(x, ids, scores, residual, rows, kSlots, packed_gate, packed_up, packed_down, packed_bytes,
+                       in_gate, out_gate, in_up, out_up, in_down, out_down, hidden, intermediate, nullptr, out,
+                       workspace, workspace_bytes, (hipStream_t)stream, k);
+}
+
+int moe_trellis_moe_decode(int k, const uint16_t* x, const uint16_t* residual, int rows, const float* router_w,
+                           const float* bias, const void* packed_gate, const void* packed_up, const void* packed_down,
+                           int64_t packed_bytes, const uint16_t* in_gate, const uint16_t* out_gate,
+                           const uint16_t* in_up, const uint16_t* out_up, const uint16_t* in_down,
+                           const uint16_t* out_down, int hidden, int intermediate, uint16_t* out, uint32_t* indices,
+                           float* scores, void* workspace, size_t workspace_bytes, moe_stream_t stream) {
+  return k4_block(x, nullptr, nullptr, 0.0f, residual, rows, router_w, bias, packed_gate, packed_up, packed_down,
+                  packed_bytes, in_gate, out_gate, in_up, out_up, in_down, out_down, hidden, intermediate, out, indices,
+                  scores, workspace, workspace_bytes, (hipStream_t)stream, k);
 }
 
 int moe_k4_layer_decode(const uint16_t* x, const uint16_t* attn, const uint16_t* norm_w, float eps, int rows,

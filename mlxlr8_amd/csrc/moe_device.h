@@ -8,6 +8,8 @@
 //   * Typed SwiGLU (exlr8/metal/fast_decode_common.metal:40-49).
 #pragma once
 #include <hip/hip_runtime.h>
+
+#include <type_traits>
 #include <stdint.h>
 
 namespace moe {
@@ -189,6 +191,20 @@ __device__ __forceinline__ void load_codebook16_lds(uint8_t* lds) {
 // Word w of a tile with its circular predecessor p holds 8 codewords (A.1 direct form):
 //   slot 0..2 straddle p and w, slot 3..7 lie inside w.
 // Slot s sits at tile row (lane%4)*2 + (s&1) + (s&2)*4 and column lane/4 + (s&4)*2.
+
+// ---------------------------------------------------------------- compile-time loop
+// f(std::integral_constant<int, J>) for J = 0 .. N - 1, unrolled whatever the body's size.
+template <int J, int N, class F>
+__device__ __forceinline__ void static_for_from(F& f) {
+  if constexpr (J < N) {
+    f(std::integral_constant<int, J>{});
+    static_for_from<J + 1, N>(f);
+  }
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_from<0, N>(f);
+}
 
 // ---------------------------------------------------------------- K4 word -> fp16 MFMA operands
 // The same word decode, producing the weights as fp16 pairs ready for a B fragment of
@@ -486,6 +502,85 @@ __device__ __forceinline__ void decode_pair_words_f16(uint32_t w0, uint32_t w1, 
           }
         }
     if (pend_i >= 0) q[pend_i][kOut[pend_k]] = widen_one(lb[pend_i][pend_k]);
+  }
+}
+
+// ---------------------------------------------------------------- K3 piece -> fp16 MFMA operands
+// A K3 tile is 24 words; lane piece m holds words 3m .. 3m + 2, i.e. the tile's codewords
+// 32m .. 32m + 31.  Codeword i of a K-bit tile is the 16 bits of the circular MSB-first tile stream
+// that end after its symbol, at bit (i + 1) K (exlr8/trellis.py:78-102, the generic window of
+// exlr8/metal/trellis.metal:25-40).  With the piece's stream S = [predecessor word, words 0..2]
+// (MSB first) codeword j of the piece ends at bit 3j + 35 of S: one funnel shift puts it in the
+// low half of a register.  Its tile position is that of the K4 decoder's word j / 8, slot j % 8.
+template <int J>
+__device__ __forceinline__ uint32_t k3_window(const uint32_t (&S)[4]) {
+  constexpr int E = 3 * J + 35, ws = (E - 16) / 32, we = (E - 1) / 32;
+  if constexpr (ws == we) {
+    constexpr int sh = 32 * we + 32 - E;  // 0 .. 16
+    if constexpr (sh == 0) return S[we];
+    else return S[we] >> sh;
+  } else {
+    return __builtin_amdgcn_alignbit(S[ws], S[we], 32 * ws + 64 - E);
+  }
+}
+// q[i][p] = (c_2p, c_2p+1) of piece words R0 + i (i = 0, 1), as decode_pair_words_f16 gives them;
+// the first NE (word R0) / NO (word R0 + 1) pairs by the arithmetic route, the rest from the
+// E4M3 code table.
+template <int NE, int NO, int R0>
+__device__ __forceinline__ void decode_k3_pair_words(const uint32_t (&S)[4], const uint8_t* tab, f16x2 (&q)[2][4]) {
+  uint32_t c[2][8];
+  static_for<16>([&](auto jc) {
+    constexpr int j = decltype(jc)::value;
+    c[j / 8][j % 8] = k3_window<8 * R0 + j>(S);
+  });
+  auto nalu = [](int i) { return i ? NO : NE; };
+  // table route first (its loads are then in flight during the arithmetic)
+  uint32_t lb[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int p = 0; p < 4; p++)
+      if (p >= nalu(i)) lb[i][p] = lds_pair_bytes<0, 0>(tab, c[i][2 * p], c[i][2 * p + 1]);
+  uint32_t sm[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int p = 0; p < 4; p++)
+      if (p < nalu(i)) sm[i][p] = halves_sum_pair<0, 0>(c[i][2 * p], c[i][2 * p + 1]);
+  // E4M3 rounding, two arithmetic pairs per fp8 register; the table pairs widened two at a time
+  {
+    int pi = -1, pp = -1;
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+      for (int p = 0; p < 4; p++)
+        if (p < nalu(i)) {
+          if (pi < 0) {
+            pi = i;
+            pp = p;
+          } else {
+            round_e4m3_two(sm[pi][pp], sm[i][p], q[pi][pp], q[i][p]);
+            pi = -1;
+          }
+        }
+    if (pi >= 0) q[pi][pp] = round_e4m3_pair(sm[pi][pp]);
+  }
+  {
+    int pi = -1, pp = -1;
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+      for (int p = 0; p < 4; p++)
+        if (p >= nalu(i)) {
+          if (pi < 0) {
+            pi = i;
+            pp = p;
+          } else {
+            widen_two(lb[pi][pp], lb[i][p], q[pi][pp], q[i][p]);
+            pi = -1;
+          }
+        }
+    if (pi >= 0) q[pi][pp] = widen_one(lb[pi][pp]);
   }
 }
 

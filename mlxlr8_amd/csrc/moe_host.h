@@ -59,7 +59,7 @@ int k4_layer_run(const uint16_t* x, const uint16_t* residual, int rows, int rout
                  const float* bias, uint32_t* ids, float* scores, const uint8_t* const packed[3],
                  const uint16_t* const in_scale[3], const uint16_t* const out_scale[3], int h, int m, int experts,
                  int combine, uint16_t* out, uint16_t* values, void* layer_ws, hipStream_t s,
-                 const LayerNorm* norm = nullptr);
+                 const LayerNorm* norm = nullptr, int bits = 4);
 // The layer workspace's plan (where a plan kernel writes it for route = 0).
 Plan* k4_layer_plan(void* layer_ws);
 // The fused block's work list for `units` units: 5 ints per item (kind, unit, a, b, c; see

@@ -73,8 +73,8 @@ class ExpertLayer:
         The call runs on the stream that is current now (its workspace belongs to that stream)."""
         h = self.hidden
         rows = x.numel() // h
-        if rows > 8 or self.experts != 257 or x.dtype != BF16 or self.k != 4:
-            raise ValueError("prepare_decode needs <= 8 bf16 rows and 256 routed + 1 shared K4 experts")
+        if rows > 8 or self.experts != 257 or x.dtype != BF16 or self.k not in (3, 4):
+            raise ValueError("prepare_decode needs <= 8 bf16 rows and 256 routed + 1 shared K3 or K4 experts")
         require_cuda(x, residual, router_weight, bias)
         call = SimpleNamespace()
         call.x = x.reshape(rows, h).contiguous()
@@ -88,7 +88,11 @@ class ExpertLayer:
         args = (ptr(call.x), ptr(call.residual), rows, ptr(call.w), ptr(call.bias), *_weights(self.packed, self.scales),
                 h, self.intermediate, ptr(call.out), ptr(call.ids), ptr(call.scores), ptr(ws), ws.numel(),
                 stream(x.device))
-        fn = lib().moe_k4_moe_decode
+        if self.k == 4:
+            fn = lib().moe_k4_moe_decode
+        else:
+            k, fn3 = self.k, lib().moe_trellis_moe_decode
+            fn = lambda *a: fn3(k, *a)
 
         def run():
             check(fn(*args))
@@ -143,8 +147,8 @@ class ExpertLayer:
         rows = x.numel() // h
         if rows > 8:
             raise ValueError("decode_block handles up to 8 token rows")
-        if self.experts != 257 or self.k != 4:
-            raise ValueError("decode_block needs 256 routed K4 experts plus the shared expert")
+        if self.experts != 257 or self.k not in (3, 4):
+            raise ValueError("decode_block needs 256 routed K3 or K4 experts plus the shared expert")
         if x.dtype != BF16:
             raise ValueError("this build computes bf16 activations")
         require_cuda(x, residual, router_weight, bias)
@@ -156,9 +160,9 @@ class ExpertLayer:
         ids = torch.empty((rows, 9), dtype=torch.int32, device=x.device)
         scores = torch.empty((rows, 8), dtype=torch.float32, device=x.device)
         ws = workspace(x.device, h, self.intermediate)
-        check(lib().moe_k4_moe_decode(ptr(xr), ptr(res), rows, ptr(w), ptr(b), *_weights(self.packed, self.scales),
-                                      h, self.intermediate, ptr(out), ptr(ids), ptr(scores), ptr(ws), ws.numel(),
-                                      stream(x.device)))
+        args = (ptr(xr), ptr(res), rows, ptr(w), ptr(b), *_weights(self.packed, self.scales), h, self.intermediate,
+                ptr(out), ptr(ids), ptr(scores), ptr(ws), ws.numel(), stream(x.device))
+        check(lib().moe_k4_moe_decode(*args) if self.k == 4 else lib().moe_trellis_moe_decode(self.k, *args))
         return out.reshape(residual.shape), ids, scores
 
 

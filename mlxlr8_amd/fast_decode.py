@@ -49,7 +49,7 @@ def fast_expert_mlp(x, indices, packed, scales, k, hidden, intermediate, *, reus
     if fp8 is not None or expert_to_slot is not None:
         raise NotImplementedError("FP8 expert caches are not part of the MI355X build")
     _validate(x, indices, packed, scales, k, hidden, intermediate)
-    if k != 4:
+    if k not in (3, 4):
         return grouped_expert_mlp(x, indices, packed, scales, k, hidden, intermediate)
     slots = indices.shape[-1]
     ids = indices.reshape(-1, slots).to(torch.int32).contiguous()
@@ -62,8 +62,9 @@ def fast_expert_mlp(x, indices, packed, scales, k, hidden, intermediate, *, reus
     step = min(MAX_ROWS, max(1, 72 // slots))
     for r0 in range(0, rows, step):
         r1 = min(rows, r0 + step)
-        check(lib().moe_k4_mlp(ptr(xr[r0:r1]), ptr(ids[r0:r1]), r1 - r0, slots, *w, hidden, intermediate,
-                               ptr(values[r0 * slots:r1 * slots]), ptr(ws), ws.numel(), st))
+        args = (ptr(xr[r0:r1]), ptr(ids[r0:r1]), r1 - r0, slots, *w, hidden, intermediate,
+                ptr(values[r0 * slots:r1 * slots]), ptr(ws), ws.numel(), st)
+        check(lib().moe_k4_mlp(*args) if k == 4 else lib().moe_trellis_mlp(k, *args))
     return values.reshape(*indices.shape, hidden)
 
 
@@ -86,9 +87,10 @@ def combine_values(values, scores, residual):
 
 def expert_values(x, indices, packed, scales, k, hidden, intermediate):
     """Per-slot values by the reference's row-count rule (exlr8/experts.py:170-175): up to 16 token
-    rows through the decode MLP, more through the sorted grouped MLP (K2/K3 always grouped)."""
+    rows through the decode MLP (K3 and K4 experts), more through the sorted grouped MLP (K2 experts
+    always grouped)."""
     rows = indices.numel() // indices.shape[-1]
-    if k == 4 and rows <= 16:
+    if k in (3, 4) and rows <= 16:
         return fast_expert_mlp(x, indices, packed, scales, k, hidden, intermediate)
     return grouped_expert_mlp(x, indices, packed, scales, k, hidden, intermediate)
 
@@ -99,7 +101,7 @@ def mlp_finish(x, indices, scores, residual, packed, scales, hidden, intermediat
     _validate(x.reshape(-1, hidden), indices.reshape(-1, 9), packed, scales, k, hidden, intermediate)
     rows = x.numel() // hidden
     require_cuda(scores, residual)
-    if k != 4 or rows > MAX_ROWS:
+    if k not in (3, 4) or rows > MAX_ROWS:
         values = expert_values(x.reshape(rows, hidden), indices.reshape(rows, 9), packed, scales, k, hidden,
                                intermediate)
         return combine_values(values, scores, residual)
@@ -109,8 +111,9 @@ def mlp_finish(x, indices, scores, residual, packed, scales, hidden, intermediat
     res = residual.reshape(rows, hidden).to(BF16).contiguous()
     out = torch.empty((rows, hidden), dtype=BF16, device=x.device)
     ws = workspace(x.device, hidden, intermediate)
-    check(lib().moe_k4_mlp_finish(ptr(xr), ptr(ids), ptr(sc), ptr(res), rows, *_weights(packed, scales), hidden,
-                                  intermediate, ptr(out), ptr(ws), ws.numel(), stream(x.device)))
+    args = (ptr(xr), ptr(ids), ptr(sc), ptr(res), rows, *_weights(packed, scales), hidden, intermediate, ptr(out),
+            ptr(ws), ws.numel(), stream(x.device))
+    check(lib().moe_k4_mlp_finish(*args) if k == 4 else lib().moe_trellis_mlp_finish(k, *args))
     return out.reshape(residual.shape)
 
 
