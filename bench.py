@@ -58,6 +58,8 @@ def parse():
                         "prefill, 4 20-layer K4 stack")
     p.add_argument("--k4-prefill", action="store_true",
                    help="instead: the K4 grouped prefill MLP (values of 512 Zipf-routed rows x 9 slots)")
+    p.add_argument("--k3", action="store_true",
+                   help="instead: the K3 layer (the multi-token-prediction layer's width) at batch-1 decode")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="also run a plain 1 GiB device copy (reference point for rocprofv3 FETCH/WRITE_SIZE)")
     return p.parse_args()
@@ -136,6 +138,9 @@ def main():
         sys.exit(2)
     if args.k4_prefill:
         print(json.dumps(bench_k4_prefill(args)), flush=True)
+        return
+    if args.k3:
+        print(json.dumps(bench_k3_decode(args)), flush=True)
         return
     if args.config != 0:
         print(json.dumps(OTHER[args.config](args)), flush=True)
@@ -218,7 +223,7 @@ def main():
         "hbm_frac": round(hbm / HBM_PEAK_GBPS, 4),
         "bytes_per_token": BYTES_TOKEN,
         "wait_errors": wait_errors,
-        "roofline": {"kernel": "k4_layer_kernel<1, false> (router, top-8, shared and routed gate/up and down decode "
+        "roofline": {"kernel": "k4_layer_kernel<1, false, 4> (router, top-8, shared and routed gate/up and down decode "
                                "GEMVs, finishes and combine in one persistent launch)",
                      "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
@@ -318,6 +323,29 @@ def bench_mxfp4_decode(args):
     return dict(line, us_per_token=round(ms * 1e3, 2), wait_errors=stalled_launches())
 
 
+def bench_k3_decode(args):
+    """The routed K3 block, batch 1: K3 trellis experts (3 bits per weight) at the K4 layer's shape."""
+    import torch
+    from mlxlr8_amd import synth
+    from mlxlr8_amd.experts import ExpertLayer
+    dev = torch.device("cuda:0")
+    layers = []
+    for i in range(min(args.layers, 3)):
+        L = synth.k4_layer(dev, args.seed + 17 * i, k=3)
+        layers.append(ExpertLayer(L["packed"], L["scales"], H, M, k=3, number=78))
+    w, bias = synth.router(dev, args.seed)
+    toks = [synth.activations(dev, args.seed + 1000 + t, 1) for t in range(args.tokens)]
+    calls = [[l.prepare_decode(x, r, w, bias) for (x, r) in toks] for l in layers]
+    ms = _time_steps(lambda i: calls[i % len(calls)][i % len(toks)].run(), args.steps, args.warmup)
+    algo = 9 * 3 * (TRELLIS * 3 // 4) + 256 * H * 4 + 9 * 3 * (H + M) * 2 + 256 * 4 + 3 * H * 2
+    line = _line(args, 1e3 / ms, "tokens/s", ms, "f32",
+                 "GLM-5.3-style MoE layer with K3 trellis experts (the multi-token-prediction layer's width), "
+                 "batch-1 decode: hidden 6144, 256 routed + 1 shared, top-8, intermediate 2048",
+                 {"global_batch": 1, "seq_len": 1, "layers_rotated": len(layers)}, algo,
+                 "k4_layer_kernel<1, false, 3>: router, the nine slots' K3 projections and the combine in one launch")
+    return dict(line, us_per_token=round(ms * 1e3, 2), wait_errors=_stalls())
+
+
 def bench_k4_verify(args):
     import torch
     from mlxlr8_amd import synth
@@ -339,7 +367,7 @@ def bench_k4_verify(args):
                       "8-token speculative-verify batch through the K4-trellis MoE layer (correlated rows, "
                       "distinct experts streamed once)",
                       {"global_batch": 8, "seq_len": 1, "distinct_experts": U, "layers_rotated": len(layers)},
-                      algo, "k4_layer_kernel<8, false>: router, the distinct experts' projections and the combine in one launch"),
+                      algo, "k4_layer_kernel<8, false, 4>: router, the distinct experts' projections and the combine in one launch"),
                 us_per_step=round(ms * 1e3, 2), wait_errors=_stalls())
 
 
