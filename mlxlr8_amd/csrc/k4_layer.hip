@@ -835,12 +835,81 @@ __device__ void combine_block(const LayerArgs& a, int ob, uint32_t tag, const fl
 
 // down finish of output block ob of unit ui: per-slot values, or the slot outputs for the combine
 // (and, for the last unit, the combine of the block)
+// The combine of output block ob for a one-row launch, by the last unit's down finish: `own`
+// (slot `js`) is this unit's output, kept in registers (nothing else reads it), `res` the residual
+// pair loaded earlier.  The other slots' words are normally complete; stale ones are waited for.
+__device__ void combine_one_row(const LayerArgs& a, int col, int js, f32x2 own, uint32_t res, uint32_t tag,
+                                const float* score) {
+  const int lane = cold_lane();
+  uint64_t w[kSlots][2];
+#pragma unroll
+  for (int j = 0; j < kSlots; j++) {
+    const uint64_t* q = a.w.yslot + (int64_t)j * a.h + col;
+    w[j][0] = ld_tag(q);
+    w[j][1] = ld_tag(q + 1);
+  }
+  bool ok = true;
+#pragma unroll
+  for (int j = 0; j < kSlots; j++) ok = ok & (j == js || ((int)has_tag(w[j][0], tag) & (int)has_tag(w[j][1], tag)));
+  int spins = 0;
+  while (!__all(ok)) {
+    bool live = true;
+    for (;;) {
+      const int j = lane % kSlots;
+      const uint64_t* q = a.w.yslot + (int64_t)j * a.h + col;
+      if (__all(j == js || has_tag(ld_tag(q), tag))) break;
+      if (!keep_waiting<MOE_LAYER_WAIT>(a, spins)) {
+        live = false;
+        break;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kSlots; j++) {
+      const uint64_t* q = a.w.yslot + (int64_t)j * a.h + col;
+      w[j][0] = ld_tag(q);
+      w[j][1] = ld_tag(q + 1);
+    }
+    if (!live) break;
+    ok = true;
+#pragma unroll
+    for (int j = 0; j < kSlots; j++) ok = ok & (j == js || ((int)has_tag(w[j][0], tag) & (int)has_tag(w[j][1], tag)));
+  }
+  f32x2 y[kSlots];
+#pragma unroll
+  for (int j = 0; j < kSlots; j++) y[j] = j == js ? own : f32x2{tag_value(w[j][0]), tag_value(w[j][1])};
+  float tot0 = y[0].x * score[0] + 0.0f, tot1 = y[0].y * score[0] + 0.0f;
+#pragma unroll
+  for (int j = 1; j < 8; j++) {
+    tot0 = (y[j].x * score[j] + 0.0f) + tot0;
+    tot1 = (y[j].y * score[j] + 0.0f) + tot1;
+  }
+  const float c0f = round_bf16(round_bf16(tot0) + y[8].x);
+  const float c1f = round_bf16(round_bf16(tot1) + y[8].y);
+  const uint32_t packed2 = (uint32_t)f32_to_bf16(bf16_to_f32((uint16_t)(res & 0xFFFFu)) + c0f) |
+                           ((uint32_t)f32_to_bf16(bf16_to_f32((uint16_t)(res >> 16)) + c1f) << 16);
+  *reinterpret_cast<uint32_t*>(a.out + col) = packed2;
+}
+
 __device__ void down_finish(const LayerArgs& a, const UnitInfo& ui, int ob, bool last, uint32_t tag, const Items& L,
                             const float* score) {
   const int lane = cold_lane();
   const int col = ob * 128 + 2 * lane;
   const uint32_t osc = *reinterpret_cast<const uint32_t*>(a.out_scale[2] + (int64_t)ui.e * a.h + col);
   const float os0 = f16_to_f32((uint16_t)(osc & 0xFFFFu)), os1 = f16_to_f32((uint16_t)(osc >> 16));
+  if (a.fin == LFIN_COMBINE && last && a.rows == 1 && ui.ntok == 1) {
+    // The launch's last dependency chain ends here.  One row, one slot of this unit: its output
+    // goes to the combine in registers (no store and read-back), and the residual is requested
+    // before this block's down partials are waited for.
+    const uint32_t res = *reinterpret_cast<const uint32_t*>(a.residual + col);
+    const int js = min(max(ui.slot(0), 0), kSlots - 1);
+    const uint64_t* rows[1] = {part_ptr(a, ui.slot(0), 2 * L.MB * L.HB + ob * L.MB)};
+    f32x2 v[1];
+    sum_parts<1, 16>(a, rows, L.MB, tag, v);
+    float v0 = v[0].x, v1 = v[0].y;
+    hadamard128_wave(v0, v1);
+    combine_one_row(a, col, js, f32x2{round_bf16(v0 * os0), round_bf16(v1 * os1)}, res, tag, score);
+    return;
+  }
   for (int t = 0; t < ui.ntok; t++) {
     const int s = ui.slot(t);
     const uint64_t* rows[1] = {part_ptr(a, s, 2 * L.MB * L.HB + ob * L.MB)};
