@@ -56,6 +56,12 @@ constexpr int kPfRowBytes = 528; // LDS row stride of a staged k step: 256 B hi 
 constexpr int kPfLo = 2;         // fp8 remainder terms
 constexpr int kPfMaxExperts = 1024;
 constexpr size_t kPfMaxLds = 160 * 1024;  // LDS per workgroup on gfx950
+#ifndef MOE_PF_MERGE_GATE
+#define MOE_PF_MERGE_GATE 1
+#endif
+#ifndef MOE_PF_MERGE_DOWN
+#define MOE_PF_MERGE_DOWN 0
+#endif
 
 // ---------------------------------------------------------------- sorted work order
 // One block of 1024 threads (16 waves).  Counting sort of the flat ids (stable: slots of one
@@ -577,7 +583,7 @@ inline size_t pf_large_lds(bool gate, int K) {
 }
 
 template <bool GATE, int MTMIN, int MTMAX>
-__global__ __launch_bounds__(kPfThreads) void pf_gemm_kernel(PfGemm a) {
+__device__ __forceinline__ void pf_gemm_body(const PfGemm& a, int bid) {
   extern __shared__ __attribute__((aligned(16))) uint8_t pf_lds[];
   uint8_t* abuf = pf_lds;
   uint8_t* sbuf = abuf + 2 * PfStage<MTMAX>::kBytes;
@@ -593,12 +599,12 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm_kernel(PfGemm a) {
   // the popular experts): consecutive plan blocks of an output block share an XCD and its weights.
   int b, ob;
   if (MTMAX <= 2) {
-    const int grp = blockIdx.x / (8 * outblocks), r = blockIdx.x % (8 * outblocks);
+    const int grp = bid / (8 * outblocks), r = bid % (8 * outblocks);
     b = 8 * grp + r % 8;
     ob = r / 8;
   } else {
-    b = blockIdx.x / outblocks;
-    ob = blockIdx.x % outblocks;
+    b = bid / outblocks;
+    ob = bid % outblocks;
   }
   if (b >= *a.nblk) return;
   const int e = a.blk[b], first = a.blk[a.cap + b], len = a.blk[2 * a.cap + b];
@@ -623,6 +629,23 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm_kernel(PfGemm a) {
 #undef PF_CASE
 }
 
+template <bool GATE, int MTMIN, int MTMAX>
+__global__ __launch_bounds__(kPfThreads) void pf_gemm_kernel(PfGemm a) {
+  pf_gemm_body<GATE, MTMIN, MTMAX>(a, (int)blockIdx.x);
+}
+
+// Both item classes in one launch: the large items' workgroups first (`nlarge` of them, a multiple
+// of 8 so that the small items keep their XCD mapping), so that the few long items of the popular
+// experts start at once and the many small ones fill the machine around them, instead of running
+// in a launch of their own after the small ones with most compute units idle.
+template <bool GATE>
+__global__ __launch_bounds__(kPfThreads) void pf_gemm_merged_kernel(PfGemm a, int nlarge) {
+  if ((int)blockIdx.x < nlarge)
+    pf_gemm_body<GATE, 3, 4>(a, (int)blockIdx.x);
+  else
+    pf_gemm_body<GATE, 1, 2>(a, (int)blockIdx.x - nlarge);
+}
+
 template <bool GATE>
 int launch_pf_gemm(const PfGemm& a, hipStream_t s) {
   const int n128 = (GATE ? a.m : a.N) / 128;  // 128-column output blocks
@@ -636,11 +659,18 @@ int launch_pf_gemm(const PfGemm& a, hipStream_t s) {
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)small_lds));
   MOE_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&pf_gemm_kernel<GATE, 3, 4>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)large_lds));
-  hipLaunchKernelGGL((pf_gemm_kernel<GATE, 1, 2>), dim3(groups * (n128 / pf_blocks_per_item(2))), dim3(kPfThreads),
-                     small_lds, s, a);
+  const unsigned nsmall = groups * (n128 / pf_blocks_per_item(2)), nlarge = groups * (n128 / pf_blocks_per_item(4));
+  if (GATE ? MOE_PF_MERGE_GATE : MOE_PF_MERGE_DOWN) {
+    const size_t lds = small_lds > large_lds ? small_lds : large_lds;
+    MOE_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&pf_gemm_merged_kernel<GATE>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    hipLaunchKernelGGL((pf_gemm_merged_kernel<GATE>), dim3(nlarge + nsmall), dim3(kPfThreads), lds, s, a, (int)nlarge);
+    MOE_HIP(hipGetLastError());
+    return MOE_OK;
+  }
+  hipLaunchKernelGGL((pf_gemm_kernel<GATE, 1, 2>), dim3(nsmall), dim3(kPfThreads), small_lds, s, a);
   MOE_HIP(hipGetLastError());
-  hipLaunchKernelGGL((pf_gemm_kernel<GATE, 3, 4>), dim3(groups * (n128 / pf_blocks_per_item(4))), dim3(kPfThreads),
-                     large_lds, s, a);
+  hipLaunchKernelGGL((pf_gemm_kernel<GATE, 3, 4>), dim3(nlarge), dim3(kPfThreads), large_lds, s, a);
   MOE_HIP(hipGetLastError());
   return MOE_OK;
 }
