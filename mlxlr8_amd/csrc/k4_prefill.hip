@@ -38,6 +38,9 @@
 #ifndef MOE_KP_ALU_EVEN
 #define MOE_KP_ALU_EVEN 2
 #endif
+#ifndef MOE_KP_MERGED
+#define MOE_KP_MERGED 1
+#endif
 #ifndef MOE_KP_ALU_ODD
 #define MOE_KP_ALU_ODD 3
 #endif
@@ -118,6 +121,9 @@ struct KpGemm {
   const int32_t* blk;         // plan [3][cap]: expert, first sorted row, length
   int cap;
   const int32_t* nblk;
+  const int32_t* ent;         // item entries in launch order: 2 plan block + row half (kp_order_kernel)
+  const int32_t* nent;
+  int32_t* queue;             // this GEMM's claim counter (zeroed by kp_order_kernel)
   float* inner;               // [n][inner_stride] fp32
   int inner_stride;
   int bits;                   // trellis width K (2, 3 or 4)
@@ -167,16 +173,14 @@ __device__ __forceinline__ void kp_generic_frags(const KpWords<KB>& p, int o, co
                       __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(q[2 * rh + 1][h], 1.0f, true));
 }
 
-// MT M-tiles (8 rows each) per item: items of 8 (MT - 1) < len <= 8 MT rows (MT = 1, 2, 4, 8);
-// KB = trellis width
+// One item: rows [first, first + len) of expert e (len <= 8 MT), projection proj, output columns
+// [256 cb, +256).  `ab` holds the two A stages (at least MT * 8 * kKpRowQuad bytes each), `tab` the
+// code table.  Every wave of the block runs it (it meets at block barriers).
 template <int MT, int KB>
-__global__ __launch_bounds__(kKpThreads) void kp_gemm_kernel(KpGemm a) {
-  __shared__ __attribute__((aligned(16))) uint8_t tab[65536];
-  __shared__ __attribute__((aligned(16))) uint8_t abuf[2][MT * 8 * kKpRowQuad];
-  load_codebook_lds(tab, a.codebook);
-  __syncthreads();
+__device__ __forceinline__ void kp_item(const KpGemm& a, const uint8_t* __restrict__ tab, uint8_t* ab0, uint8_t* ab1,
+                                        int e, int first, int len, int proj, int cb) {
   const int w = wave_id_uniform(), lane = lane_id(), nn = lane & 15, g = lane >> 4;
-  const int ncb = (a.N + kKpCols - 1) / kKpCols, nq = a.K / 64, it = a.K / 16, obs = a.N / 128;
+  const int nq = a.K / 64, it = a.K / 16, obs = a.N / 128;
   const int lane_off = (nn >> 3) * 128 + (nn & 7) * 16;
   const int src_lane = (lane & 7) == 0 ? lane + 7 : lane - 1;
   const int s4 = w & 3;
@@ -188,117 +192,191 @@ __global__ __launch_bounds__(kKpThreads) void kp_gemm_kernel(KpGemm a) {
 #pragma unroll
     for (int k = 0; k <= KpWords<KB>::kStream; k++) gw[k] = (b0 / 32 + k) % kNw;
   }
+  uint8_t* const abuf[2] = {ab0, ab1};
+  // the last item of N % 256 == 128 has one column block: waves 4-7 then only stage A
+  const bool active = 2 * cb + (w >> 2) < obs;
+  const int ob = min(2 * cb + (w >> 2), obs - 1);
+  using Piece = std::conditional_t<KB == 4, u32x4, KpWords<KB>>;
+  const uint8_t* wbase = a.packed[proj] + (KB == 4 ? lane_off + 256 * s4 : 32 * KB * (2 * s4 + (nn >> 3)));
+  auto piece = [&](int q) -> Piece {
+    if constexpr (KB == 4) {
+      return *reinterpret_cast<const u32x4*>(wbase + chunk_offset(a.side, e, ob, 4 * q + g, it, obs));
+    } else {
+      const uint32_t* t =
+          reinterpret_cast<const uint32_t*>(wbase + chunk_index(a.side, e, ob, 4 * q + g, it, obs) * (256 * KB));
+      Piece r;
+#pragma unroll
+      for (int k = 0; k <= KpWords<KB>::kStream; k++) r.v[k] = t[gw[k]];
+      return r;
+    }
+  };
+  // A staging: chunk c of the quad = row c / 16, 16 B part c % 16 ([rh][hl][g] of the row)
+  constexpr int kChunks = MT * 8 * 16, kPer = (kChunks + kKpThreads - 1) / kKpThreads;
+  const uint8_t* abase = reinterpret_cast<const uint8_t*>(a.a[proj]);
+  auto fetch_a = [&](int q, i32x4 (&f)[kPer]) {
+#pragma unroll
+    for (int i = 0; i < kPer; i++) {
+      const int c = min((int)threadIdx.x + i * kKpThreads, kChunks - 1);
+      const int64_t p = first + min(c >> 4, len - 1);
+      f[i] = *reinterpret_cast<const i32x4*>(abase + (p * nq + q) * kKpRowQuad + (c & 15) * 16);
+    }
+  };
+  auto put_a = [&](const i32x4 (&f)[kPer], uint8_t* dst) {
+#pragma unroll
+    for (int i = 0; i < kPer; i++) {
+      const int c = (int)threadIdx.x + i * kKpThreads;
+      if (c < kChunks) {
+        const int row = c >> 4, part = c & 15;  // part = (rh * 2 + hl) * 4 + g
+        const int rh = part >> 3, hl = (part >> 2) & 1, gg = part & 3;
+        const int m = 2 * (row & 7) + hl;
+        *reinterpret_cast<i32x4*>(dst + (((row >> 3) * 2 + rh) * 16 + m) * 64 + gg * 16) = f[i];
+      }
+    }
+  };
+  f32x4 acc[MT][2];
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++) acc[mt][0] = acc[mt][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  i32x4 fa[kPer];
+  fetch_a(0, fa);
+  put_a(fa, abuf[0]);
+  Piece pc0 = piece(0), pc1 = piece(min(1, nq - 1));
+  fetch_a(min(1, nq - 1), fa);
+  __syncthreads();
+  auto mfmas = [&](const uint8_t* ab, int rh, const f16x8& b0, const f16x8& b1) {
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) {
+      const f16x8 av = *reinterpret_cast<const f16x8*>(ab + ((mt * 2 + rh) * 16 + nn) * 64 + g * 16);
+      acc[mt][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b0, acc[mt][0], 0, 0, 0);
+      acc[mt][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b1, acc[mt][1], 0, 0, 0);
+    }
+    mfma_acc_guard(acc);
+  };
+  auto quad = [&](const uint8_t* ab, const Piece& pc) {
+    if (!active) return;
+    if constexpr (KB == 4) {
+      const uint32_t prior = (uint32_t)__shfl((int)pc.w, src_lane, 64);
+#pragma unroll
+      for (int rh = 0; rh < 2; rh++) {
+        f16x2 qv[2][4];
+        if (rh == 0)
+          decode_pair_words_f16<MOE_KP_ALU_EVEN, MOE_KP_ALU_ODD>(pc.x, pc.y, prior, tab, qv);
+        else
+          decode_pair_words_f16<MOE_KP_ALU_EVEN, MOE_KP_ALU_ODD>(pc.z, pc.w, pc.y, tab, qv);
+        mfmas(ab, rh, frag(qv[0][0], qv[0][1], qv[1][0], qv[1][1]), frag(qv[0][2], qv[0][3], qv[1][2], qv[1][3]));
+      }
+    } else {
+      f16x8 bf[2][2];
+      kp_generic_frags<KB>(pc, bo, tab, bf);
+      mfmas(ab, 0, bf[0][0], bf[0][1]);
+      mfmas(ab, 1, bf[1][0], bf[1][1]);
+    }
+  };
+  for (int q = 0; q < nq; q += 2) {  // nq is even (K % 128 == 0)
+    quad(abuf[0], pc0);
+    pc0 = piece(min(q + 2, nq - 1));
+    put_a(fa, abuf[1]);
+    fetch_a(min(q + 2, nq - 1), fa);
+    __syncthreads();
+    quad(abuf[1], pc1);
+    pc1 = piece(min(q + 3, nq - 1));
+    if (q + 2 < nq) put_a(fa, abuf[0]);
+    fetch_a(min(q + 3, nq - 1), fa);
+    __syncthreads();
+  }
+  // D rows 4g + i of M-tile mt: rows 2t (hi) and 2t+1 (lo) of item row 8 mt + t, t = 2g + i/2
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+#pragma unroll
+      for (int tt = 0; tt < 2; tt++) {
+        const int row = mt * 8 + 2 * g + tt;
+        if (active && row < len) {
+          const int col = a.col_off[proj] + ob * 128 + 16 * (2 * s4 + (nn >> 3)) + (nn & 7) + 8 * h;
+          a.inner[(int64_t)(first + row) * a.inner_stride + col] =
+              fmaf(acc[mt][h][2 * tt + 1], 1.0f / 2048.0f, acc[mt][h][2 * tt]);
+        }
+      }
+}
+
+// MT M-tiles (8 rows each) per item: items of 8 (MT - 1) < len <= 8 MT rows (MT = 1, 2, 4, 8);
+// KB = trellis width
+template <int MT, int KB>
+__global__ __launch_bounds__(kKpThreads) void kp_gemm_kernel(KpGemm a) {
+  __shared__ __attribute__((aligned(16))) uint8_t tab[65536];
+  __shared__ __attribute__((aligned(16))) uint8_t abuf[2][MT * 8 * kKpRowQuad];
+  load_codebook_lds(tab, a.codebook);
+  __syncthreads();
+  const int ncb = (a.N + kKpCols - 1) / kKpCols;
   const int nblk = *a.nblk;
   const int items = nblk * a.nproj * ncb;
   for (int item = blockIdx.x; item < items; item += gridDim.x) {
     const int cb = item % ncb, proj = (item / ncb) % a.nproj, b = item / (ncb * a.nproj);
     const int len = a.blk[2 * a.cap + b];
     if (len <= (MT / 2) * 8 || len > MT * 8) continue;  // another class
-    const int e = a.blk[b], first = a.blk[a.cap + b];
-    // the last item of N % 256 == 128 has one column block: waves 4-7 then only stage A
-    const bool active = 2 * cb + (w >> 2) < obs;
-    const int ob = min(2 * cb + (w >> 2), obs - 1);
-    using Piece = std::conditional_t<KB == 4, u32x4, KpWords<KB>>;
-    const uint8_t* wbase = a.packed[proj] + (KB == 4 ? lane_off + 256 * s4 : 32 * KB * (2 * s4 + (nn >> 3)));
-    auto piece = [&](int q) -> Piece {
-      if constexpr (KB == 4) {
-        return *reinterpret_cast<const u32x4*>(wbase + chunk_offset(a.side, e, ob, 4 * q + g, it, obs));
-      } else {
-        const uint32_t* t =
-            reinterpret_cast<const uint32_t*>(wbase + chunk_index(a.side, e, ob, 4 * q + g, it, obs) * (256 * KB));
-        Piece r;
-#pragma unroll
-        for (int k = 0; k <= KpWords<KB>::kStream; k++) r.v[k] = t[gw[k]];
-        return r;
-      }
-    };
-    // A staging: chunk c of the quad = row c / 16, 16 B part c % 16 ([rh][hl][g] of the row)
-    constexpr int kChunks = MT * 8 * 16, kPer = (kChunks + kKpThreads - 1) / kKpThreads;
-    const uint8_t* abase = reinterpret_cast<const uint8_t*>(a.a[proj]);
-    auto fetch_a = [&](int q, i32x4 (&f)[kPer]) {
-#pragma unroll
-      for (int i = 0; i < kPer; i++) {
-        const int c = min((int)threadIdx.x + i * kKpThreads, kChunks - 1);
-        const int64_t p = first + min(c >> 4, len - 1);
-        f[i] = *reinterpret_cast<const i32x4*>(abase + (p * nq + q) * kKpRowQuad + (c & 15) * 16);
-      }
-    };
-    auto put_a = [&](const i32x4 (&f)[kPer], uint8_t* dst) {
-#pragma unroll
-      for (int i = 0; i < kPer; i++) {
-        const int c = (int)threadIdx.x + i * kKpThreads;
-        if (c < kChunks) {
-          const int row = c >> 4, part = c & 15;  // part = (rh * 2 + hl) * 4 + g
-          const int rh = part >> 3, hl = (part >> 2) & 1, gg = part & 3;
-          const int m = 2 * (row & 7) + hl;
-          *reinterpret_cast<i32x4*>(dst + (((row >> 3) * 2 + rh) * 16 + m) * 64 + gg * 16) = f[i];
-        }
-      }
-    };
-    f32x4 acc[MT][2];
-#pragma unroll
-    for (int mt = 0; mt < MT; mt++) acc[mt][0] = acc[mt][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    i32x4 fa[kPer];
-    fetch_a(0, fa);
-    put_a(fa, abuf[0]);
-    Piece pc0 = piece(0), pc1 = piece(min(1, nq - 1));
-    fetch_a(min(1, nq - 1), fa);
+    kp_item<MT, KB>(a, tab, abuf[0], abuf[1], a.blk[b], a.blk[a.cap + b], len, proj, cb);
+  }
+}
+
+// The GEMMs' item entries, largest first: plan blocks of 17..64 rows as entries of up to 32 rows
+// (a block beyond 32 rows as two entries, its row halves: each row's sums are the same whatever
+// rows share its tiles), then blocks of 9..16 rows, then of up to 8.  One block of 256 threads
+// after the segment table; it also clears the two GEMMs' claim counters.
+__global__ __launch_bounds__(256) void kp_order_kernel(const int32_t* __restrict__ blk, int cap,
+                                                       const int32_t* __restrict__ nblk, int32_t* __restrict__ ent,
+                                                       int32_t* __restrict__ nent, int32_t* __restrict__ queue) {
+  __shared__ int32_t cnt[3], pos[3];
+  if (threadIdx.x < 3) cnt[threadIdx.x] = pos[threadIdx.x] = 0;
+  __syncthreads();
+  const int nb = min(*nblk, cap);
+  auto cls = [&](int len) { return len > 16 ? 0 : len > 8 ? 1 : 2; };
+  for (int b = threadIdx.x; b < nb; b += 256) {
+    const int len = blk[2 * cap + b];
+    atomicAdd(&cnt[cls(len)], len > 32 ? 2 : 1);
+  }
+  __syncthreads();
+  for (int b = threadIdx.x; b < nb; b += 256) {
+    const int len = blk[2 * cap + b], c = cls(len);
+    const int base = (c > 0 ? cnt[0] : 0) + (c > 1 ? cnt[1] : 0);
+    const int at = base + atomicAdd(&pos[c], len > 32 ? 2 : 1);
+    ent[at] = 2 * b;
+    if (len > 32) ent[at + 1] = 2 * b + 1;
+  }
+  if (threadIdx.x == 0) {
+    *nent = cnt[0] + cnt[1] + cnt[2];
+    queue[0] = 0;
+    queue[32] = 0;
+  }
+}
+
+// Every item class in one persistent launch: the blocks claim items in entry order (largest first)
+// from a counter, so blocks that finish the long items go on to the short ones and the launch has
+// no class boundaries at which compute units wait for the last long item of a class.
+template <int KB>
+__global__ __launch_bounds__(kKpThreads) void kp_gemm_merged_kernel(KpGemm a) {
+  __shared__ __attribute__((aligned(16))) uint8_t tab[65536];
+  __shared__ __attribute__((aligned(16))) uint8_t abuf[2][4 * 8 * kKpRowQuad];
+  __shared__ int32_t claimed;
+  load_codebook_lds(tab, a.codebook);
+  const int ncb = (a.N + kKpCols - 1) / kKpCols, per = a.nproj * ncb;
+  const int total = *a.nent * per;
+  for (;;) {
+    if (threadIdx.x == 0) claimed = __hip_atomic_fetch_add(a.queue, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
-    auto mfmas = [&](const uint8_t* ab, int rh, const f16x8& b0, const f16x8& b1) {
-#pragma unroll
-      for (int mt = 0; mt < MT; mt++) {
-        const f16x8 av = *reinterpret_cast<const f16x8*>(ab + ((mt * 2 + rh) * 16 + nn) * 64 + g * 16);
-        acc[mt][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b0, acc[mt][0], 0, 0, 0);
-        acc[mt][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b1, acc[mt][1], 0, 0, 0);
-      }
-      mfma_acc_guard(acc);
-    };
-    auto quad = [&](const uint8_t* ab, const Piece& pc) {
-      if (!active) return;
-      if constexpr (KB == 4) {
-        const uint32_t prior = (uint32_t)__shfl((int)pc.w, src_lane, 64);
-#pragma unroll
-        for (int rh = 0; rh < 2; rh++) {
-          f16x2 qv[2][4];
-          if (rh == 0)
-            decode_pair_words_f16<MOE_KP_ALU_EVEN, MOE_KP_ALU_ODD>(pc.x, pc.y, prior, tab, qv);
-          else
-            decode_pair_words_f16<MOE_KP_ALU_EVEN, MOE_KP_ALU_ODD>(pc.z, pc.w, pc.y, tab, qv);
-          mfmas(ab, rh, frag(qv[0][0], qv[0][1], qv[1][0], qv[1][1]), frag(qv[0][2], qv[0][3], qv[1][2], qv[1][3]));
-        }
-      } else {
-        f16x8 bf[2][2];
-        kp_generic_frags<KB>(pc, bo, tab, bf);
-        mfmas(ab, 0, bf[0][0], bf[0][1]);
-        mfmas(ab, 1, bf[1][0], bf[1][1]);
-      }
-    };
-    for (int q = 0; q < nq; q += 2) {  // nq is even (K % 128 == 0)
-      quad(abuf[0], pc0);
-      pc0 = piece(min(q + 2, nq - 1));
-      put_a(fa, abuf[1]);
-      fetch_a(min(q + 2, nq - 1), fa);
-      __syncthreads();
-      quad(abuf[1], pc1);
-      pc1 = piece(min(q + 3, nq - 1));
-      if (q + 2 < nq) put_a(fa, abuf[0]);
-      fetch_a(min(q + 3, nq - 1), fa);
-      __syncthreads();
-    }
-    // D rows 4g + i of M-tile mt: rows 2t (hi) and 2t+1 (lo) of item row 8 mt + t, t = 2g + i/2
-#pragma unroll
-    for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-      for (int h = 0; h < 2; h++)
-#pragma unroll
-        for (int tt = 0; tt < 2; tt++) {
-          const int row = mt * 8 + 2 * g + tt;
-          if (active && row < len) {
-            const int col = a.col_off[proj] + ob * 128 + 16 * (2 * s4 + (nn >> 3)) + (nn & 7) + 8 * h;
-            a.inner[(int64_t)(first + row) * a.inner_stride + col] =
-                fmaf(acc[mt][h][2 * tt + 1], 1.0f / 2048.0f, acc[mt][h][2 * tt]);
-          }
-        }
+    const int v = claimed;
+    __syncthreads();
+    if (v >= total) break;
+    const int en = a.ent[v / per], r = v % per;
+    const int b = en >> 1, half = en & 1;
+    const int cb = r % ncb, proj = r / ncb;
+    const int len = a.blk[2 * a.cap + b];
+    const int first = a.blk[a.cap + b] + 32 * half, n = half ? len - 32 : min(len, 32);
+    if (n > 16)
+      kp_item<4, KB>(a, tab, abuf[0], abuf[1], a.blk[b], first, n, proj, cb);
+    else if (n > 8)
+      kp_item<2, KB>(a, tab, abuf[0], abuf[1], a.blk[b], first, n, proj, cb);
+    else
+      kp_item<1, KB>(a, tab, abuf[0], abuf[1], a.blk[b], first, n, proj, cb);
   }
 }
 
@@ -378,6 +456,9 @@ struct KpWorkspace {
   uint16_t* a_down; // [n][m/64][256 B]
   float* inner_gu;  // [n][2m]
   float* inner_d;   // [n][h]
+  int32_t* ent;     // [2 cap] GEMM item entries, nent of them
+  int32_t* nent;
+  int32_t* queue;   // two claim counters, one 128 B line each
   int cap;
   size_t bytes;
 };
@@ -393,6 +474,9 @@ KpWorkspace kp_carve(void* base, int64_t n, int h, int m, int64_t experts) {
   w.starts = reinterpret_cast<int32_t*>(take((size_t)experts * 4));
   w.blk = reinterpret_cast<int32_t*>(take((size_t)3 * w.cap * 4));
   w.nblk = reinterpret_cast<int32_t*>(take(4));
+  w.ent = reinterpret_cast<int32_t*>(take((size_t)2 * w.cap * 4));
+  w.nent = reinterpret_cast<int32_t*>(take(4));
+  w.queue = reinterpret_cast<int32_t*>(take(256));
   w.a_gate = reinterpret_cast<uint16_t*>(take((size_t)n * h * 4));
   w.a_up = reinterpret_cast<uint16_t*>(take((size_t)n * h * 4));
   w.a_down = reinterpret_cast<uint16_t*>(take((size_t)n * m * 4));
@@ -408,6 +492,11 @@ int launch_kp_gemm_k(const KpGemm& g, hipStream_t s) {
   // CU (68-80 KB of LDS) and get 4 blocks per CU queued, so the CUs stay busy to the end of the
   // launch; the 8-tile class (96 KB) runs one block per CU.
   const int blocks = device_cus() > 0 ? device_cus() : 256;
+  if (MOE_KP_MERGED) {
+    hipLaunchKernelGGL((kp_gemm_merged_kernel<KB>), dim3(4 * blocks), dim3(kKpThreads), 0, s, g);
+    MOE_HIP(hipGetLastError());
+    return MOE_OK;
+  }
   hipLaunchKernelGGL((kp_gemm_kernel<1, KB>), dim3(4 * blocks), dim3(kKpThreads), 0, s, g);
   MOE_HIP(hipGetLastError());
   hipLaunchKernelGGL((kp_gemm_kernel<2, KB>), dim3(4 * blocks), dim3(kKpThreads), 0, s, g);
@@ -467,6 +556,9 @@ int moe_trellis_grouped_mlp(int k, const uint16_t* x, const uint32_t* ids, int r
   if ((rc = segment_table_clamped(ids, (int)n, (int)experts, kKpRows, w.order, w.counts, w.starts, w.blk, w.cap, w.nblk,
                                   (hipStream_t)stream)))
     return rc;
+  hipLaunchKernelGGL(kp_order_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, w.blk, w.cap, w.nblk, w.ent, w.nent,
+                     w.queue);
+  MOE_HIP(hipGetLastError());
   const int64_t pw = n * (hidden / 128) * 2;
   hipLaunchKernelGGL(kp_prep_kernel, dim3((unsigned)((pw + 3) / 4)), dim3(256), 0, s, x, ids, w.order, w.counts, w.starts,
                      (int)experts, (int)n, slots, hidden, 2, 0, in_gate, in_up, w.a_gate, w.a_up);
@@ -488,6 +580,9 @@ int moe_trellis_grouped_mlp(int k, const uint16_t* x, const uint32_t* ids, int r
   g.blk = w.blk;
   g.cap = w.cap;
   g.nblk = w.nblk;
+  g.ent = w.ent;
+  g.nent = w.nent;
+  g.queue = w.queue;
   g.inner = w.inner_gu;
   g.inner_stride = 2 * intermediate;
   g.bits = k;
@@ -508,6 +603,9 @@ int moe_trellis_grouped_mlp(int k, const uint16_t* x, const uint32_t* ids, int r
   d.blk = w.blk;
   d.cap = w.cap;
   d.nblk = w.nblk;
+  d.ent = w.ent;
+  d.nent = w.nent;
+  d.queue = w.queue + 32;
   d.inner = w.inner_d;
   d.inner_stride = hidden;
   d.bits = k;
@@ -551,6 +649,9 @@ int moe_trellis_grouped_linear(int k, const uint16_t* x, int x_per_slot, const u
   if ((rc = segment_table_clamped(ids, (int)n, (int)experts, kKpRows, w.order, w.counts, w.starts, w.blk, w.cap, w.nblk,
                                   (hipStream_t)stream)))
     return rc;
+  hipLaunchKernelGGL(kp_order_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, w.blk, w.cap, w.nblk, w.ent, w.nent,
+                     w.queue);
+  MOE_HIP(hipGetLastError());
   const int64_t pw = n * (in_features / 128);
   hipLaunchKernelGGL(kp_prep_kernel, dim3((unsigned)((pw + 3) / 4)), dim3(256), 0, s, x, ids, w.order, w.counts, w.starts,
                      (int)experts, (int)n, slots, in_features, 1, x_per_slot ? 1 : 0, in_scale, in_scale, w.a_gate,
@@ -570,6 +671,9 @@ int moe_trellis_grouped_linear(int k, const uint16_t* x, int x_per_slot, const u
   g.blk = w.blk;
   g.cap = w.cap;
   g.nblk = w.nblk;
+  g.ent = w.ent;
+  g.nent = w.nent;
+  g.queue = w.queue;
   g.inner = w.inner_d;
   g.inner_stride = out_features;
   g.bits = k;
