@@ -38,6 +38,11 @@
 #ifndef MOE_KP_ALU_EVEN
 #define MOE_KP_ALU_EVEN 2
 #endif
+// quads per staging step of the items of up to 16 rows (their two stages of two quads fit the
+// launch's stage buffers)
+#ifndef MOE_KP_PAIR
+#define MOE_KP_PAIR 2
+#endif
 #ifndef MOE_KP_MERGED
 #define MOE_KP_MERGED 1
 #endif
@@ -176,9 +181,11 @@ __device__ __forceinline__ void kp_generic_frags(const KpWords<KB>& p, int o, co
 // One item: rows [first, first + len) of expert e (len <= 8 MT), projection proj, output columns
 // [256 cb, +256).  `ab` holds the two A stages (at least MT * 8 * kKpRowQuad bytes each), `tab` the
 // code table.  Every wave of the block runs it (it meets at block barriers).
-template <int MT, int KB>
+// G quads share a staging step (one block barrier per G quads; a stage then holds G quads).
+template <int MT, int KB, int G = 1>
 __device__ __forceinline__ void kp_item(const KpGemm& a, const uint8_t* __restrict__ tab, uint8_t* ab0, uint8_t* ab1,
                                         int e, int first, int len, int proj, int cb) {
+  static_assert(G == 1 || G == 2, "one or two quads per staging step");
   const int w = wave_id_uniform(), lane = lane_id(), nn = lane & 15, g = lane >> 4;
   const int nq = a.K / 64, it = a.K / 16, obs = a.N / 128;
   const int lane_off = (nn >> 3) * 128 + (nn & 7) * 16;
@@ -236,12 +243,6 @@ __device__ __forceinline__ void kp_item(const KpGemm& a, const uint8_t* __restri
   f32x4 acc[MT][2];
 #pragma unroll
   for (int mt = 0; mt < MT; mt++) acc[mt][0] = acc[mt][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  i32x4 fa[kPer];
-  fetch_a(0, fa);
-  put_a(fa, abuf[0]);
-  Piece pc0 = piece(0), pc1 = piece(min(1, nq - 1));
-  fetch_a(min(1, nq - 1), fa);
-  __syncthreads();
   auto mfmas = [&](const uint8_t* ab, int rh, const f16x8& b0, const f16x8& b1) {
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) {
@@ -271,17 +272,63 @@ __device__ __forceinline__ void kp_item(const KpGemm& a, const uint8_t* __restri
       mfmas(ab, 1, bf[1][0], bf[1][1]);
     }
   };
-  for (int q = 0; q < nq; q += 2) {  // nq is even (K % 128 == 0)
-    quad(abuf[0], pc0);
-    pc0 = piece(min(q + 2, nq - 1));
-    put_a(fa, abuf[1]);
-    fetch_a(min(q + 2, nq - 1), fa);
+  i32x4 fa[kPer];
+  if constexpr (G == 1) {
+    fetch_a(0, fa);
+    put_a(fa, abuf[0]);
+    Piece pc0 = piece(0), pc1 = piece(min(1, nq - 1));
+    fetch_a(min(1, nq - 1), fa);
     __syncthreads();
-    quad(abuf[1], pc1);
-    pc1 = piece(min(q + 3, nq - 1));
-    if (q + 2 < nq) put_a(fa, abuf[0]);
-    fetch_a(min(q + 3, nq - 1), fa);
+    for (int q = 0; q < nq; q += 2) {  // nq is even (K % 128 == 0)
+      quad(abuf[0], pc0);
+      pc0 = piece(min(q + 2, nq - 1));
+      put_a(fa, abuf[1]);
+      fetch_a(min(q + 2, nq - 1), fa);
+      __syncthreads();
+      quad(abuf[1], pc1);
+      pc1 = piece(min(q + 3, nq - 1));
+      if (q + 2 < nq) put_a(fa, abuf[0]);
+      fetch_a(min(q + 3, nq - 1), fa);
+      __syncthreads();
+    }
+  } else {
+    // stage s holds quads 4i + 2s, 4i + 2s + 1 (QB bytes each); nq is even, so quads come in pairs
+    constexpr int QB = MT * 8 * kKpRowQuad;
+    i32x4 fb[kPer];
+    fetch_a(0, fa);
+    fetch_a(min(1, nq - 1), fb);
+    put_a(fa, abuf[0]);
+    put_a(fb, abuf[0] + QB);
+    Piece p0 = piece(0), p1 = piece(min(1, nq - 1)), p2 = piece(min(2, nq - 1)), p3 = piece(min(3, nq - 1));
+    fetch_a(min(2, nq - 1), fa);
+    fetch_a(min(3, nq - 1), fb);
     __syncthreads();
+    for (int q = 0; q < nq; q += 4) {
+      quad(abuf[0], p0);
+      quad(abuf[0] + QB, p1);
+      p0 = piece(min(q + 4, nq - 1));
+      p1 = piece(min(q + 5, nq - 1));
+      if (q + 2 < nq) {
+        put_a(fa, abuf[1]);
+        put_a(fb, abuf[1] + QB);
+      }
+      fetch_a(min(q + 4, nq - 1), fa);
+      fetch_a(min(q + 5, nq - 1), fb);
+      __syncthreads();
+      if (q + 2 < nq) {
+        quad(abuf[1], p2);
+        quad(abuf[1] + QB, p3);
+      }
+      p2 = piece(min(q + 6, nq - 1));
+      p3 = piece(min(q + 7, nq - 1));
+      if (q + 4 < nq) {
+        put_a(fa, abuf[0]);
+        put_a(fb, abuf[0] + QB);
+      }
+      fetch_a(min(q + 6, nq - 1), fa);
+      fetch_a(min(q + 7, nq - 1), fb);
+      __syncthreads();
+    }
   }
   // D rows 4g + i of M-tile mt: rows 2t (hi) and 2t+1 (lo) of item row 8 mt + t, t = 2g + i/2
 #pragma unroll
@@ -357,6 +404,8 @@ __global__ __launch_bounds__(kKpThreads) void kp_gemm_merged_kernel(KpGemm a) {
   __shared__ __attribute__((aligned(16))) uint8_t tab[65536];
   __shared__ __attribute__((aligned(16))) uint8_t abuf[2][4 * 8 * kKpRowQuad];
   __shared__ int32_t claimed;
+  // K2/K3 pieces hold more words: their registers allow one quad per step within 128 VGPRs
+  constexpr int kPair = KB == 4 ? MOE_KP_PAIR : 1;
   load_codebook_lds(tab, a.codebook);
   const int ncb = (a.N + kKpCols - 1) / kKpCols, per = a.nproj * ncb;
   const int total = *a.nent * per;
@@ -374,9 +423,9 @@ __global__ __launch_bounds__(kKpThreads) void kp_gemm_merged_kernel(KpGemm a) {
     if (n > 16)
       kp_item<4, KB>(a, tab, abuf[0], abuf[1], a.blk[b], first, n, proj, cb);
     else if (n > 8)
-      kp_item<2, KB>(a, tab, abuf[0], abuf[1], a.blk[b], first, n, proj, cb);
+      kp_item<2, KB, kPair>(a, tab, abuf[0], abuf[0] + 2 * 8 * kKpRowQuad * kPair, a.blk[b], first, n, proj, cb);
     else
-      kp_item<1, KB>(a, tab, abuf[0], abuf[1], a.blk[b], first, n, proj, cb);
+      kp_item<1, KB, kPair>(a, tab, abuf[0], abuf[0] + 8 * kKpRowQuad * kPair, a.blk[b], first, n, proj, cb);
   }
 }
 
