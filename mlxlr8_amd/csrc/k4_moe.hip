@@ -136,11 +136,66 @@ __global__ __launch_bounds__(1024) void trellis_decode_kernel(const uint32_t* __
   const uint64_t tile = side == 2 ? ((((e * (it / 8u) + tk / 8u) * (ot / 8u) + tn / 8u) * 8u + tk % 8u) * 8u + tn % 8u)
                                   : (((e * (ot / 8u) + tn / 8u) * it + tk) * 8u + tn % 8u);
   const uint32_t* tw = packed + tile * 32u;
-  switch ((blockIdx.x >> 1) & 3) {
+  // the mixes of the decoders in use (fused blocks 1/2, grouped GEMM 2/3) and every per-word count 0..4
+  switch ((blockIdx.x >> 1) % 6) {
     case 0: decode_piece_to_inner<0, 0, T16>(tw, qg, tab, inner, out_f, 16u * tk, 16u * tn); break;
     case 1: decode_piece_to_inner<1, 2, T16>(tw, qg, tab, inner, out_f, 16u * tk, 16u * tn); break;
     case 2: decode_piece_to_inner<2, 2, T16>(tw, qg, tab, inner, out_f, 16u * tk, 16u * tn); break;
+    case 3: decode_piece_to_inner<2, 3, T16>(tw, qg, tab, inner, out_f, 16u * tk, 16u * tn); break;
+    case 4: decode_piece_to_inner<3, 1, T16>(tw, qg, tab, inner, out_f, 16u * tk, 16u * tn); break;
     default: decode_piece_to_inner<4, 4, T16>(tw, qg, tab, inner, out_f, 16u * tk, 16u * tn); break;
+  }
+}
+
+// K3 tiles (24 words): thread = one lane's piece (words 3 qg .. 3 qg + 2, the previous lane's last
+// word cyclically before them), decoded by decode_k3_pair_words, the fused block's K3 decoder, and
+// placed as the K4 decoder's words 0..3.  Each block uses one arithmetic/table mix.
+template <int NE, int NO>
+__device__ __forceinline__ void decode_k3_piece_to_inner(const uint32_t* __restrict__ tw, int qg, const uint8_t* tab,
+                                                         uint16_t* __restrict__ inner, int out_f, uint32_t row0,
+                                                         uint32_t col0) {
+  const uint32_t S[4] = {tw[(3 * qg + 23) % 24], tw[3 * qg], tw[3 * qg + 1], tw[3 * qg + 2]};
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    f16x2 q[2][4];
+    if (h == 0)
+      decode_k3_pair_words<NE, NO, 0>(S, tab, q);
+    else
+      decode_k3_pair_words<NE, NO, 2>(S, tab, q);
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const uint32_t r = row0 + 2 * (2 * h + i) + 8 * (j & 1), c = col0 + qg + 8 * (j >> 1);
+        const uint32_t bits = __builtin_bit_cast(uint32_t, q[i][j]);
+        inner[(int64_t)r * out_f + c] = (uint16_t)(bits & 0xFFFFu);
+        inner[(int64_t)(r + 1) * out_f + c] = (uint16_t)(bits >> 16);
+      }
+  }
+}
+__global__ __launch_bounds__(1024) void trellis_decode_k3_kernel(const uint32_t* __restrict__ packed, int in_f, int out_f,
+                                                                 int side, int64_t expert, uint16_t* __restrict__ inner) {
+  __shared__ __attribute__((aligned(16))) uint8_t tab[65536];
+  load_codebook_lds_t<1024>(tab);
+  __syncthreads();
+  const int64_t pieces = (int64_t)in_f * out_f / 32;  // 8 pieces per 256-weight tile
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= pieces) return;
+  const uint32_t it = (uint32_t)in_f / 16u, ot = (uint32_t)out_f / 16u;
+  const int64_t t = idx >> 3;
+  const int qg = (int)(idx & 7);
+  const uint32_t tk = (uint32_t)(t / ot), tn = (uint32_t)(t % ot);
+  const uint64_t e = (uint64_t)expert;
+  const uint64_t tile = side == 2 ? ((((e * (it / 8u) + tk / 8u) * (ot / 8u) + tn / 8u) * 8u + tk % 8u) * 8u + tn % 8u)
+                                  : (((e * (ot / 8u) + tn / 8u) * it + tk) * 8u + tn % 8u);
+  const uint32_t* tw = packed + tile * 24u;
+  // the fused block's mix (MOE_LAYER3_ALU_EVEN / _ODD = 1 / 2) and every per-word count 0..4
+  switch (blockIdx.x % 5) {
+    case 0: decode_k3_piece_to_inner<1, 2>(tw, qg, tab, inner, out_f, 16u * tk, 16u * tn); break;
+    case 1: decode_k3_piece_to_inner<0, 0>(tw, qg, tab, inner, out_f, 16u * tk, 16u * tn); break;
+    case 2: decode_k3_piece_to_inner<2, 3>(tw, qg, tab, inner, out_f, 16u * tk, 16u * tn); break;
+    case 3: decode_k3_piece_to_inner<4, 4>(tw, qg, tab, inner, out_f, 16u * tk, 16u * tn); break;
+    default: decode_k3_piece_to_inner<3, 1>(tw, qg, tab, inner, out_f, 16u * tk, 16u * tn); break;
   }
 }
 
@@ -985,6 +1040,13 @@ int moe_trellis_decode_f16(const void* packed, int64_t packed_bytes, int k, int 
           (long long)experts);
   rc = ensure_device_ready();
   if (rc) return rc;
+  if (k == 3) {
+    const int64_t pieces = (int64_t)in_f * out_f / 32;
+    hipLaunchKernelGGL(trellis_decode_k3_kernel, dim3((unsigned)((pieces + 1023) / 1024)), dim3(1024), 0,
+                       (hipStream_t)stream, (const uint32_t*)packed, in_f, out_f, side, expert, inner);
+    MOE_HIP(hipGetLastError());
+    return MOE_OK;
+  }
   if (k != 4) {
     const int64_t n = (int64_t)in_f * out_f;
     hipLaunchKernelGGL(trellis_decode_generic_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,

@@ -45,6 +45,8 @@ def test_decode_inner_bit_exact_small(cuda, orc, side):
 
 @pytest.mark.parametrize("side,in_f,out_f", [(1, 6144, 2048), (2, 2048, 6144)])
 def test_decode_inner_bit_exact_glm_shapes(cuda, orc, side, in_f, out_f):
+    """The K4 piece decoder of the GEMVs, the fused block and the grouped GEMM, with the
+    arithmetic/table mixes those use (1/2, 2/3) and every per-word count, on both code tables."""
     from mlxlr8_amd.trellis import decode_inner
     say(f"case: decode glm side={side}")
     g = torch.Generator(device=cuda)
@@ -346,7 +348,10 @@ def test_fp32_accumulation_known_answer(cuda):
 @pytest.mark.parametrize("k", [2, 3])
 @pytest.mark.parametrize("side", [1, 2])
 def test_decode_inner_k2_k3_bit_exact(cuda, orc, k, side):
-    """The K2 / K3 trellis decode (the MTP layer's K3 experts): brute-force symbols and the oracle."""
+    """The K2 / K3 trellis decode (the MTP layer's K3 experts): brute-force symbols and the oracle.
+    K3 runs the fused decode block's piece decoder (decode_k3_pair_words) with its arithmetic/table
+    mix on the small matrix and five mixes across the GLM-size one, so that decoder is pinned bit
+    for bit; K2 runs the per-codeword reference decode."""
     from mlxlr8_amd.trellis import decode_inner
     say(f"case: decode k={k} side={side}")
     rng = np.random.default_rng(60 + 10 * k + side)
