@@ -403,16 +403,19 @@ template <int KB>
 __global__ __launch_bounds__(kKpThreads) void kp_gemm_merged_kernel(KpGemm a) {
   __shared__ __attribute__((aligned(16))) uint8_t tab[65536];
   __shared__ __attribute__((aligned(16))) uint8_t abuf[2][4 * 8 * kKpRowQuad];
-  __shared__ int32_t claimed;
   // K2/K3 pieces hold more words: their registers allow one quad per step within 128 VGPRs
   constexpr int kPair = KB == 4 ? MOE_KP_PAIR : 1;
   load_codebook_lds(tab, a.codebook);
   const int ncb = (a.N + kKpCols - 1) / kKpCols, per = a.nproj * ncb;
   const int total = *a.nent * per;
+  // The claimed item is handed to the block through the first word of the A stage, which no item
+  // uses between its last barrier and the next item's staging: the block's LDS then stays at
+  // 80 KB, so that two blocks fit a CU (a separate shared word would make it one).
+  int32_t* claimed = reinterpret_cast<int32_t*>(&abuf[0][0]);
   for (;;) {
-    if (threadIdx.x == 0) claimed = __hip_atomic_fetch_add(a.queue, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0) *claimed = __hip_atomic_fetch_add(a.queue, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
-    const int v = claimed;
+    const int v = *claimed;
     __syncthreads();
     if (v >= total) break;
     const int en = a.ent[v / per], r = v % per;
