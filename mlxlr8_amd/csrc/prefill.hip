@@ -59,6 +59,9 @@ constexpr size_t kPfMaxLds = 160 * 1024;  // LDS per workgroup on gfx950
 #ifndef MOE_PF_MERGE_GATE
 #define MOE_PF_MERGE_GATE 1
 #endif
+#ifndef MOE_PF_DOWN_TWO
+#define MOE_PF_DOWN_TWO 1
+#endif
 #ifndef MOE_PF_MERGE_DOWN
 #define MOE_PF_MERGE_DOWN 0
 #endif
@@ -634,6 +637,12 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm_kernel(PfGemm a) {
   pf_gemm_body<GATE, MTMIN, MTMAX>(a, (int)blockIdx.x);
 }
 
+// The down GEMM's small items (K = intermediate: 48 KB of LDS per block) held within 128 VGPRs so
+// that two blocks share a CU.
+__global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4))) void pf_gemm_down_small_kernel(PfGemm a) {
+  pf_gemm_body<false, 1, 2>(a, (int)blockIdx.x);
+}
+
 // Both item classes in one launch: the large items' workgroups first (`nlarge` of them, a multiple
 // of 8 so that the small items keep their XCD mapping), so that the few long items of the popular
 // experts start at once and the many small ones fill the machine around them, instead of running
@@ -668,7 +677,13 @@ int launch_pf_gemm(const PfGemm& a, hipStream_t s) {
     MOE_HIP(hipGetLastError());
     return MOE_OK;
   }
-  hipLaunchKernelGGL((pf_gemm_kernel<GATE, 1, 2>), dim3(nsmall), dim3(kPfThreads), small_lds, s, a);
+  if (!GATE && MOE_PF_DOWN_TWO) {
+    MOE_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&pf_gemm_down_small_kernel),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)small_lds));
+    hipLaunchKernelGGL(pf_gemm_down_small_kernel, dim3(nsmall), dim3(kPfThreads), small_lds, s, a);
+  } else {
+    hipLaunchKernelGGL((pf_gemm_kernel<GATE, 1, 2>), dim3(nsmall), dim3(kPfThreads), small_lds, s, a);
+  }
   MOE_HIP(hipGetLastError());
   hipLaunchKernelGGL((pf_gemm_kernel<GATE, 3, 4>), dim3(nlarge), dim3(kPfThreads), large_lds, s, a);
   MOE_HIP(hipGetLastError());
