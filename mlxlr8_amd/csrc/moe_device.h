@@ -713,20 +713,70 @@ __device__ __forceinline__ int a_j(int r) { return 4 * ((r >> 1) & 1) + 2 * ((r 
 // ---------------------------------------------------------------- wave-level H128
 // 128 values held as 2 per lane (element i = 2*lane + j).  Normalised Sylvester order;
 // the butterfly order differs from the reference's numpy loop only in float rounding.
+// Lane bits 0..3 exchange inside a 16-lane row through DPP; a lane then computes own + partner
+// (low half) or own - partner (high half): the high half's value is the negated butterfly
+// (x - y = -(y - x) in round-to-nearest), and the sign is put back by the final scale.  Lane bits
+// 4 and 5 use v_permlane16_swap / v_permlane32_swap, which place both values of a pair in one
+// lane.  No LDS traffic; the values equal those of the lane-shuffle form bit for bit (a zero
+// result is +0, as there).
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov_f32(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+template <int K, int CTRL>
+__device__ __forceinline__ void h128_row_stage(float& v0, float& v1, int lane) {
+  const float s = __builtin_bit_cast(float, 0x3f800000 | ((lane << (31 - K)) & (int)0x80000000));
+  v0 = __builtin_fmaf(dpp_mov_f32<CTRL>(v0), s, v0);
+  v1 = __builtin_fmaf(dpp_mov_f32<CTRL>(v1), s, v1);
+}
+// v_permlane16_swap (odd 16-lane rows of a <-> even rows of b) and v_permlane32_swap (upper 32
+// lanes of a <-> lower 32 lanes of b) on float pairs
+__device__ __forceinline__ void swap16_f32(float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b),
+                                                  false, false);
+  const uint32_t r0 = r[0], r1 = r[1];
+  a = __builtin_bit_cast(float, r0);
+  b = __builtin_bit_cast(float, r1);
+}
+__device__ __forceinline__ void swap32_f32(float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b),
+                                                  false, false);
+  const uint32_t r0 = r[0], r1 = r[1];
+  a = __builtin_bit_cast(float, r0);
+  b = __builtin_bit_cast(float, r1);
+}
 __device__ __forceinline__ void hadamard128_wave(float& v0, float& v1) {
   float a = v0 + v1, b = v0 - v1;
-  v0 = a; v1 = b;
+  v0 = a;
+  v1 = b;
   const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) {
-    float o0 = __shfl_xor(v0, m, 64);
-    float o1 = __shfl_xor(v1, m, 64);
-    const bool hi = (lane & m) != 0;
-    v0 = hi ? (o0 - v0) : (v0 + o0);
-    v1 = hi ? (o1 - v1) : (v1 + o1);
+  h128_row_stage<0, 0xB1>(v0, v1, lane);  // quad_perm [1,0,3,2]: lane ^ 1
+  h128_row_stage<1, 0x4E>(v0, v1, lane);  // quad_perm [2,3,0,1]: lane ^ 2
+  {
+    // lane ^ 4: row_half_mirror (i -> 7 - i in each 8 lanes), then quad_perm [3,2,1,0]
+    const float s = __builtin_bit_cast(float, 0x3f800000 | ((lane << 29) & (int)0x80000000));
+    v0 = __builtin_fmaf(dpp_mov_f32<0x1B>(dpp_mov_f32<0x141>(v0)), s, v0);
+    v1 = __builtin_fmaf(dpp_mov_f32<0x1B>(dpp_mov_f32<0x141>(v1)), s, v1);
   }
-  v0 *= kInvSqrt128;
-  v1 *= kInvSqrt128;
+  h128_row_stage<3, 0x128>(v0, v1, lane);  // row_ror:8: lane ^ 8
+  // lane ^ 16 and lane ^ 32.  After the first swap, lanes of row 0 hold rows 0 and 1 of v0 and
+  // lanes of row 1 hold rows 0 and 1 of v1 (rows 2, 3 likewise); the pair sums and differences
+  // come out in the same arrangement, so one 32-lane swap pairs rows 0 and 2 (1 and 3), and two
+  // swaps in reverse order restore the layout.
+  swap16_f32(v0, v1);
+  a = v0 + v1;
+  b = v0 - v1;
+  swap32_f32(a, b);
+  v0 = a + b;
+  v1 = a - b;
+  swap32_f32(v0, v1);
+  swap16_f32(v0, v1);
+  // sign of the row stages: -1 where lane bits 0..3 hold an odd number of ones
+  const int sg = (__builtin_popcount(lane & 15) & 1) << 31;
+  const float sc = __builtin_bit_cast(float, __builtin_bit_cast(int, kInvSqrt128) ^ sg);
+  // fma with +0: a zero product comes out as +0 whatever the tracked sign
+  v0 = __builtin_fmaf(v0, sc, 0.0f);
+  v1 = __builtin_fmaf(v1, sc, 0.0f);
 }
 
 // ---------------------------------------------------------------- typed SwiGLU
