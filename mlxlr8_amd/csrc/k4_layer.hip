@@ -462,6 +462,27 @@ __device__ __forceinline__ void fetch_in(const LayerArgs& a, const UnitInfo& ui,
     in.r[NT] = *reinterpret_cast<const uint32_t*>(a.in_scale[it.b] + (int64_t)ui.e * a.h + off);
   }
 }
+// The lane's two words of a tagged block (ld_tag_pair), for a block that may not be written yet:
+// while it is not, the wave polls one word of it (lane 0's) and loads the whole block again only
+// once that word carries `tag`.  A waiting wave then requests 8 bytes per poll instead of the
+// block's 1 KB: the waves waiting for one block poll the same lines, and their traffic slows the
+// block's writer.  `known_missing`: the caller has just seen the block incomplete (skip the first
+// full load).
+template <int kMaxPauses, class A>
+__device__ __forceinline__ f32x2 ld_tag_pair_sampled(const A& a, const uint64_t* p, uint32_t tag, bool known_missing) {
+  if (!known_missing) {
+    const uint64_t w0 = ld_tag(p), w1 = ld_tag(p + 1);
+    if (__all(has_tag(w0, tag) && has_tag(w1, tag))) return f32x2{tag_value(w0), tag_value(w1)};
+  }
+  int spins = 0;
+  for (;;) {
+    uint64_t w = 0;
+    if (lane_id() == 0) w = ld_tag(p);
+    if ((uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(w >> 32)) == tag || !keep_waiting<kMaxPauses>(a, spins))
+      break;
+  }
+  return ld_tag_pair<kMaxPauses>(a, p, tag);
+}
 // Largest value over the wave's lanes (valid in every lane after the read of lane 63).
 __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp_f32<0xB1>(v));
@@ -513,7 +534,8 @@ __device__ __forceinline__ void stage_in(const LayerArgs& a, const UnitInfo& ui,
 #pragma unroll
       for (int t = 0; t < NT; t++) {
         if (t < ui.ntok) {
-          const f32x2 hv = ld_tag_pair<MOE_LAYER_WAIT>(a, a.w.down_xh + (int64_t)ui.slot(t) * a.m + 128 * it.c + 2 * lane, tag);
+          const f32x2 hv = ld_tag_pair_sampled<MOE_LAYER_WAIT>(
+              a, a.w.down_xh + (int64_t)ui.slot(t) * a.m + 128 * it.c + 2 * lane, tag, DPRE);
           v0[t] = hv.x;
           v1[t] = hv.y;
         }
