@@ -66,17 +66,25 @@ __device__ __forceinline__ int64_t kp_a_index(int64_t p, int nq, int k, int hl) 
   const int q = k >> 6, g = (k >> 4) & 3, r = k & 15;
   return ((((p * nq + q) * 2 + a_rh(r)) * 2 + hl) * 4 + g) * 8 + a_j(r);
 }
-__device__ __forceinline__ void kp_store_a(uint16_t* a, int64_t p, int nq, int k, float x) {
-  asm volatile("" : "+v"(x));  // x in fp32 before both conversions
-  const _Float16 hi = (_Float16)x;
-  const _Float16 lo = (_Float16)((x - (float)hi) * 2048.0f);
-  a[kp_a_index(p, nq, k, 0)] = __builtin_bit_cast(uint16_t, hi);
-  a[kp_a_index(p, nq, k, 1)] = __builtin_bit_cast(uint16_t, lo);
+
+// The pair (k, k + 1), k even, of one row: adjacent in the buffer (same 16-group, same row half,
+// positions j and j + 1), so the two hi halves and the two lo halves go out as one 32-bit store each.
+__device__ __forceinline__ void kp_store_a2(uint16_t* a, int64_t p, int nq, int k, float x0, float x1) {
+  asm volatile("" : "+v"(x0), "+v"(x1));  // x in fp32 before both conversions
+  const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
+  const _Float16 l0 = (_Float16)((x0 - (float)h0) * 2048.0f), l1 = (_Float16)((x1 - (float)h1) * 2048.0f);
+  *reinterpret_cast<uint32_t*>(a + kp_a_index(p, nq, k, 0)) =
+      (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+  *reinterpret_cast<uint32_t*>(a + kp_a_index(p, nq, k, 1)) =
+      (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
 }
 
 // ---------------------------------------------------------------- prep: xh for gate and up
-// One wave per (sorted row p, 128-block kb, projection of nproj = 1 or 2): H128(x_row *
-// in_scale[e]) -> A buffer, x_row = the slot's token row (x_per_slot = 0) or its own row.
+// One wave per (sorted row p, run of kPrepBlocks 128-blocks, projection of nproj = 1 or 2):
+// H128(x_row * in_scale[e]) -> A buffer, x_row = the slot's token row (x_per_slot = 0) or its own
+// row.  The run's loads are all issued before the first block is transformed (a wave per block
+// left each wave one load round trip with nothing to overlap it).
+constexpr int kPrepBlocks = 8;
 // Sorted rows placed by the segment table (ids outside [0, experts) clamped to the nearest expert).
 __device__ __forceinline__ int64_t kp_placed(const int32_t* counts, const int32_t* starts, int experts) {
   return (int64_t)starts[experts - 1] + counts[experts - 1];
@@ -85,6 +93,10 @@ __device__ __forceinline__ int64_t kp_placed(const int32_t* counts, const int32_
 // (a slot with an out-of-range id has a position, so its id must never index a side vector raw).
 __device__ __forceinline__ int64_t kp_expert(const uint32_t* ids, int slot, int experts) {
   return min(max((int)ids[slot], 0), experts - 1);
+}
+// waves of the prep launch for n sorted rows
+__host__ __device__ __forceinline__ int64_t kp_prep_waves(int64_t n, int K, int nproj) {
+  return n * ((K / 128 + kPrepBlocks - 1) / kPrepBlocks) * nproj;
 }
 
 __global__ __launch_bounds__(256) void kp_prep_kernel(const uint16_t* __restrict__ x, const uint32_t* __restrict__ ids,
@@ -95,25 +107,35 @@ __global__ __launch_bounds__(256) void kp_prep_kernel(const uint16_t* __restrict
                                                       const uint16_t* __restrict__ in_up, uint16_t* __restrict__ a_gate,
                                                       uint16_t* __restrict__ a_up) {
   const int64_t wid = (int64_t)blockIdx.x * 4 + wave_id_uniform();
-  const int kbs = K / 128, sh = nproj - 1;
-  if (wid >= (int64_t)n * kbs * nproj) return;
+  const int kbs = K / 128, kgs = (kbs + kPrepBlocks - 1) / kPrepBlocks, sh = nproj - 1;
+  if (wid >= kp_prep_waves(n, K, nproj)) return;
   const int proj = (int)(wid & sh);
-  const int kb = (int)((wid >> sh) % kbs);
-  const int64_t p = (wid >> sh) / kbs;
+  const int kg = (int)((wid >> sh) % kgs);
+  const int64_t p = (wid >> sh) / kgs;
   if (p >= kp_placed(counts, starts, experts)) return;
   const int slot = order[p];
   const int64_t e = kp_expert(ids, slot, experts);
   const int lane = lane_id();
-  const int k = kb * 128 + 2 * lane;
   const int64_t xrow = x_per_slot ? slot : slot / slots;
-  const uint32_t xv = *reinterpret_cast<const uint32_t*>(x + xrow * K + k);
-  const uint32_t sv = *reinterpret_cast<const uint32_t*>((proj ? in_up : in_gate) + e * K + k);
-  float v0 = bf16_to_f32((uint16_t)(xv & 0xFFFFu)) * f16_to_f32((uint16_t)(sv & 0xFFFFu));
-  float v1 = bf16_to_f32((uint16_t)(xv >> 16)) * f16_to_f32((uint16_t)(sv >> 16));
-  hadamard128_wave(v0, v1);
+  const uint16_t* xr = x + xrow * K;
+  const uint16_t* sr = (proj ? in_up : in_gate) + e * K;
+  uint32_t xv[kPrepBlocks], sv[kPrepBlocks];
+#pragma unroll
+  for (int i = 0; i < kPrepBlocks; i++) {
+    const int k = min(kg * kPrepBlocks + i, kbs - 1) * 128 + 2 * lane;
+    xv[i] = *reinterpret_cast<const uint32_t*>(xr + k);
+    sv[i] = *reinterpret_cast<const uint32_t*>(sr + k);
+  }
   uint16_t* a = proj ? a_up : a_gate;
-  kp_store_a(a, p, K / 64, k, v0);
-  kp_store_a(a, p, K / 64, k + 1, v1);
+#pragma unroll
+  for (int i = 0; i < kPrepBlocks; i++) {
+    const int kb = kg * kPrepBlocks + i;
+    if (kb >= kbs) break;
+    float v0 = bf16_to_f32((uint16_t)(xv[i] & 0xFFFFu)) * f16_to_f32((uint16_t)(sv[i] & 0xFFFFu));
+    float v1 = bf16_to_f32((uint16_t)(xv[i] >> 16)) * f16_to_f32((uint16_t)(sv[i] >> 16));
+    hadamard128_wave(v0, v1);
+    kp_store_a2(a, p, K / 64, kb * 128 + 2 * lane, v0, v1);
+  }
 }
 
 // ---------------------------------------------------------------- grouped GEMM
@@ -466,8 +488,7 @@ __global__ __launch_bounds__(256) void kp_gate_finish_kernel(const float* __rest
   h0 *= lo(idn);
   h1 *= hi(idn);
   hadamard128_wave(h0, h1);
-  kp_store_a(a_down, p, m / 64, col, h0);
-  kp_store_a(a_down, p, m / 64, col + 1, h1);
+  kp_store_a2(a_down, p, m / 64, col, h0, h1);
 }
 
 // ---------------------------------------------------------------- value finish
@@ -611,7 +632,7 @@ int moe_trellis_grouped_mlp(int k, const uint16_t* x, const uint32_t* ids, int r
   hipLaunchKernelGGL(kp_order_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, w.blk, w.cap, w.nblk, w.ent, w.nent,
                      w.queue);
   MOE_HIP(hipGetLastError());
-  const int64_t pw = n * (hidden / 128) * 2;
+  const int64_t pw = kp_prep_waves(n, hidden, 2);
   hipLaunchKernelGGL(kp_prep_kernel, dim3((unsigned)((pw + 3) / 4)), dim3(256), 0, s, x, ids, w.order, w.counts, w.starts,
                      (int)experts, (int)n, slots, hidden, 2, 0, in_gate, in_up, w.a_gate, w.a_up);
   MOE_HIP(hipGetLastError());
@@ -704,7 +725,7 @@ int moe_trellis_grouped_linear(int k, const uint16_t* x, int x_per_slot, const u
   hipLaunchKernelGGL(kp_order_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, w.blk, w.cap, w.nblk, w.ent, w.nent,
                      w.queue);
   MOE_HIP(hipGetLastError());
-  const int64_t pw = n * (in_features / 128);
+  const int64_t pw = kp_prep_waves(n, in_features, 1);
   hipLaunchKernelGGL(kp_prep_kernel, dim3((unsigned)((pw + 3) / 4)), dim3(256), 0, s, x, ids, w.order, w.counts, w.starts,
                      (int)experts, (int)n, slots, in_features, 1, x_per_slot ? 1 : 0, in_scale, in_scale, w.a_gate,
                      w.a_gate);
