@@ -240,8 +240,15 @@ void mx_layer_kernel(MxLayerArgs a) {
   const int c_lo = (int)((int64_t)kDnSlots * gw / WG), nc = (int)((int64_t)kDnSlots * (gw + 1) / WG) - c_lo;
   const int n1 = kUnits * ng;            // gate/up slots
   const int ns = n1 + 2 * na + nc;     // + down slots
-  const int gf_lo = (int)((int64_t)kGfs * gw / WG), gf_hi = (int)((int64_t)kGfs * (gw + 1) / WG);
-  const int cb_lo = (int)((int64_t)kCombines * gw / WG), cb_hi = (int)((int64_t)kCombines * (gw + 1) / WG);
+  // Gate finishes and combines go to the block's first kMW / 2 waves.  Two waves share each SIMD
+  // and the arbiter favours the older one: waves 0..3 end their gate/up rows ~4 us before 4..7,
+  // so a finish there waits less for the rows it sums and delays no late wave's own rows (a
+  // designated wave that was also a late one had held up the last unit's down inputs).
+  const int ho = kMW / 2, hw = (int)blockIdx.x * ho + wv, HW = G * ho;
+  const int gf_lo = wv < ho ? (int)((int64_t)kGfs * hw / HW) : 0;
+  const int gf_hi = wv < ho ? (int)((int64_t)kGfs * (hw + 1) / HW) : 0;
+  const int cb_lo = wv < ho ? (int)((int64_t)kCombines * hw / HW) : 0;
+  const int cb_hi = wv < ho ? (int)((int64_t)kCombines * (hw + 1) / HW) : 0;
 
   // slot s -> (unit, first weight row); true for a gate/up slot
   auto slot_rows = [&](int s, int& u, int& row) {
