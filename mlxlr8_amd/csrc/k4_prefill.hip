@@ -85,6 +85,8 @@ __device__ __forceinline__ void kp_store_a2(uint16_t* a, int64_t p, int nq, int 
 // row.  The run's loads are all issued before the first block is transformed (a wave per block
 // left each wave one load round trip with nothing to overlap it).
 constexpr int kPrepBlocks = 8;
+// 128-blocks per wave of the gate finish and the value finish (loads of the whole run first)
+constexpr int kFinGateBlocks = 4, kFinValueBlocks = 8;
 // Sorted rows placed by the segment table (ids outside [0, experts) clamped to the nearest expert).
 __device__ __forceinline__ int64_t kp_placed(const int32_t* counts, const int32_t* starts, int experts) {
   return (int64_t)starts[experts - 1] + counts[experts - 1];
@@ -455,8 +457,8 @@ __global__ __launch_bounds__(kKpThreads) void kp_gemm_merged_kernel(KpGemm a) {
 }
 
 // ---------------------------------------------------------------- gate finish -> down A operand
-// One wave per (sorted row p, 128-column block cb of the intermediate); the decode GEMV's gate
-// finish arithmetic.
+// One wave per (sorted row p, run of kFinGateBlocks 128-column blocks of the intermediate); the
+// decode GEMV's gate finish arithmetic.
 __global__ __launch_bounds__(256) void kp_gate_finish_kernel(const float* __restrict__ inner, const uint32_t* __restrict__ ids,
                                                              const int32_t* __restrict__ order,
                                                              const int32_t* __restrict__ counts,
@@ -466,33 +468,44 @@ __global__ __launch_bounds__(256) void kp_gate_finish_kernel(const float* __rest
                                                              const uint16_t* __restrict__ in_down,
                                                              uint16_t* __restrict__ a_down) {
   const int64_t wid = (int64_t)blockIdx.x * 4 + wave_id_uniform();
-  const int cbs = m / 128;
-  if (wid >= (int64_t)n * cbs) return;
-  const int64_t p = wid / cbs;
+  const int cbs = m / 128, runs = (cbs + kFinGateBlocks - 1) / kFinGateBlocks;
+  if (wid >= (int64_t)n * runs) return;
+  const int64_t p = wid / runs;
   if (p >= kp_placed(counts, starts, experts)) return;
-  const int cb = (int)(wid % cbs);
+  const int run = (int)(wid % runs);
   const int64_t e = kp_expert(ids, order[p], experts);
-  const int col = cb * 128 + 2 * lane_id();
-  const f32x2 gv = *reinterpret_cast<const f32x2*>(inner + p * 2 * m + col);
-  const f32x2 uv = *reinterpret_cast<const f32x2*>(inner + p * 2 * m + m + col);
-  const uint32_t og = *reinterpret_cast<const uint32_t*>(out_gate + e * m + col);
-  const uint32_t ou = *reinterpret_cast<const uint32_t*>(out_up + e * m + col);
-  const uint32_t idn = *reinterpret_cast<const uint32_t*>(in_down + e * m + col);
+  f32x2 gv[kFinGateBlocks], uv[kFinGateBlocks];
+  uint32_t og[kFinGateBlocks], ou[kFinGateBlocks], idn[kFinGateBlocks];
+#pragma unroll
+  for (int i = 0; i < kFinGateBlocks; i++) {
+    const int col = min(run * kFinGateBlocks + i, cbs - 1) * 128 + 2 * lane_id();
+    gv[i] = *reinterpret_cast<const f32x2*>(inner + p * 2 * m + col);
+    uv[i] = *reinterpret_cast<const f32x2*>(inner + p * 2 * m + m + col);
+    og[i] = *reinterpret_cast<const uint32_t*>(out_gate + e * m + col);
+    ou[i] = *reinterpret_cast<const uint32_t*>(out_up + e * m + col);
+    idn[i] = *reinterpret_cast<const uint32_t*>(in_down + e * m + col);
+  }
   auto lo = [](uint32_t v) { return f16_to_f32((uint16_t)(v & 0xFFFFu)); };
   auto hi = [](uint32_t v) { return f16_to_f32((uint16_t)(v >> 16)); };
-  float g0 = gv.x, g1 = gv.y, u0 = uv.x, u1 = uv.y;
-  hadamard128_wave(g0, g1);
-  hadamard128_wave(u0, u1);
-  float h0 = swiglu_bf16(g0 * lo(og), u0 * lo(ou));
-  float h1 = swiglu_bf16(g1 * hi(og), u1 * hi(ou));
-  h0 *= lo(idn);
-  h1 *= hi(idn);
-  hadamard128_wave(h0, h1);
-  kp_store_a2(a_down, p, m / 64, col, h0, h1);
+#pragma unroll
+  for (int i = 0; i < kFinGateBlocks; i++) {
+    const int cb = run * kFinGateBlocks + i;
+    if (cb >= cbs) break;
+    float g0 = gv[i].x, g1 = gv[i].y, u0 = uv[i].x, u1 = uv[i].y;
+    hadamard128_wave(g0, g1);
+    hadamard128_wave(u0, u1);
+    float h0 = swiglu_bf16(g0 * lo(og[i]), u0 * lo(ou[i]));
+    float h1 = swiglu_bf16(g1 * hi(og[i]), u1 * hi(ou[i]));
+    h0 *= lo(idn[i]);
+    h1 *= hi(idn[i]);
+    hadamard128_wave(h0, h1);
+    kp_store_a2(a_down, p, m / 64, cb * 128 + 2 * lane_id(), h0, h1);
+  }
 }
 
 // ---------------------------------------------------------------- value finish
-// One wave per (sorted row p, 128-column block): T(H128(inner) * out_down[e]) -> values[slot].
+// One wave per (sorted row p, run of kFinValueBlocks 128-column blocks): T(H128(inner) * out_down[e])
+// -> values[slot].
 __global__ __launch_bounds__(256) void kp_value_finish_kernel(const float* __restrict__ inner, const uint32_t* __restrict__ ids,
                                                               const int32_t* __restrict__ order,
                                                               const int32_t* __restrict__ counts,
@@ -500,21 +513,31 @@ __global__ __launch_bounds__(256) void kp_value_finish_kernel(const float* __res
                                                               const uint16_t* __restrict__ out_down,
                                                               uint16_t* __restrict__ values) {
   const int64_t wid = (int64_t)blockIdx.x * 4 + wave_id_uniform();
-  const int hbs = h / 128;
-  if (wid >= (int64_t)n * hbs) return;
-  const int64_t p = wid / hbs;
+  const int hbs = h / 128, runs = (hbs + kFinValueBlocks - 1) / kFinValueBlocks;
+  if (wid >= (int64_t)n * runs) return;
+  const int64_t p = wid / runs;
   if (p >= kp_placed(counts, starts, experts)) return;
-  const int hb = (int)(wid % hbs);
+  const int run = (int)(wid % runs);
   const int slot = order[p];
   const int64_t e = kp_expert(ids, slot, experts);
-  const int col = hb * 128 + 2 * lane_id();
-  const f32x2 v = *reinterpret_cast<const f32x2*>(inner + p * h + col);
-  float v0 = v.x, v1 = v.y;
-  hadamard128_wave(v0, v1);
-  const uint32_t od = *reinterpret_cast<const uint32_t*>(out_down + e * h + col);
-  const uint32_t pk = (uint32_t)f32_to_bf16(v0 * f16_to_f32((uint16_t)(od & 0xFFFFu))) |
-                      ((uint32_t)f32_to_bf16(v1 * f16_to_f32((uint16_t)(od >> 16))) << 16);
-  *reinterpret_cast<uint32_t*>(values + (int64_t)slot * h + col) = pk;
+  f32x2 v[kFinValueBlocks];
+  uint32_t od[kFinValueBlocks];
+#pragma unroll
+  for (int i = 0; i < kFinValueBlocks; i++) {
+    const int col = min(run * kFinValueBlocks + i, hbs - 1) * 128 + 2 * lane_id();
+    v[i] = *reinterpret_cast<const f32x2*>(inner + p * h + col);
+    od[i] = *reinterpret_cast<const uint32_t*>(out_down + e * h + col);
+  }
+#pragma unroll
+  for (int i = 0; i < kFinValueBlocks; i++) {
+    const int hb = run * kFinValueBlocks + i;
+    if (hb >= hbs) break;
+    float v0 = v[i].x, v1 = v[i].y;
+    hadamard128_wave(v0, v1);
+    const uint32_t pk = (uint32_t)f32_to_bf16(v0 * f16_to_f32((uint16_t)(od[i] & 0xFFFFu))) |
+                        ((uint32_t)f32_to_bf16(v1 * f16_to_f32((uint16_t)(od[i] >> 16))) << 16);
+    *reinterpret_cast<uint32_t*>(values + (int64_t)slot * h + hb * 128 + 2 * lane_id()) = pk;
+  }
 }
 
 // ---------------------------------------------------------------- workspace
@@ -660,7 +683,7 @@ int moe_trellis_grouped_mlp(int k, const uint16_t* x, const uint32_t* ids, int r
   g.inner_stride = 2 * intermediate;
   g.bits = k;
   if ((rc = launch_kp_gemm(g, s))) return rc;
-  const int64_t fw = n * (intermediate / 128);
+  const int64_t fw = n * ((intermediate / 128 + kFinGateBlocks - 1) / kFinGateBlocks);
   hipLaunchKernelGGL(kp_gate_finish_kernel, dim3((unsigned)((fw + 3) / 4)), dim3(256), 0, s, w.inner_gu, ids, w.order,
                      w.counts, w.starts, (int)experts, (int)n, intermediate, out_gate, out_up, in_down, w.a_down);
   MOE_HIP(hipGetLastError());
@@ -683,7 +706,7 @@ int moe_trellis_grouped_mlp(int k, const uint16_t* x, const uint32_t* ids, int r
   d.inner_stride = hidden;
   d.bits = k;
   if ((rc = launch_kp_gemm(d, s))) return rc;
-  const int64_t vw = n * (hidden / 128);
+  const int64_t vw = n * ((hidden / 128 + kFinValueBlocks - 1) / kFinValueBlocks);
   hipLaunchKernelGGL(kp_value_finish_kernel, dim3((unsigned)((vw + 3) / 4)), dim3(256), 0, s, w.inner_d, ids, w.order,
                      w.counts, w.starts, (int)experts, (int)n, hidden, out_down, values);
   MOE_HIP(hipGetLastError());
@@ -751,7 +774,7 @@ int moe_trellis_grouped_linear(int k, const uint16_t* x, int x_per_slot, const u
   g.inner_stride = out_features;
   g.bits = k;
   if ((rc = launch_kp_gemm(g, s))) return rc;
-  const int64_t vw = n * (out_features / 128);
+  const int64_t vw = n * ((out_features / 128 + kFinValueBlocks - 1) / kFinValueBlocks);
   hipLaunchKernelGGL(kp_value_finish_kernel, dim3((unsigned)((vw + 3) / 4)), dim3(256), 0, s, w.inner_d, ids, w.order,
                      w.counts, w.starts, (int)experts, (int)n, out_features, out_scale, y);
   MOE_HIP(hipGetLastError());
