@@ -478,8 +478,12 @@ __device__ __forceinline__ f32x2 ld_tag_pair_sampled(const A& a, const uint64_t*
   for (;;) {
     uint64_t w = 0;
     if (lane_id() == 0) w = ld_tag(p);
-    if ((uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(w >> 32)) == tag || !keep_waiting<kMaxPauses>(a, spins))
-      break;
+    if ((uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(w >> 32)) == tag) break;
+    if (!keep_waiting<kMaxPauses>(a, spins)) {
+      // the bound ran out (the error word is set): the words as they are, without a second wait
+      const uint64_t w0 = ld_tag(p), w1 = ld_tag(p + 1);
+      return f32x2{tag_value(w0), tag_value(w1)};
+    }
   }
   return ld_tag_pair<kMaxPauses>(a, p, tag);
 }
