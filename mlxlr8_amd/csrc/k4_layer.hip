@@ -100,6 +100,7 @@ constexpr int kLW = MOE_LAYER_WAVES;
 constexpr int kXcds = 8;            // queue sub-lists
 constexpr int kQueueStride = 32;    // ints between sub-list counters (one 128 B line each)
 constexpr int kSumRound = 8;        // partial rows summed per round by the gate finishes
+constexpr int kStraggle = 256;      // claims since a part's own after which it counts as behind
 
 enum LayerFin { LFIN_VALUES = 0, LFIN_COMBINE = 1 };
 
@@ -1120,6 +1121,11 @@ __global__ __launch_bounds__(kLW * 64) void k4_layer_kernel(LayerArgs a) {
         for (int hh = 0; hh < 2; hh++) acc[s4][hh] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
       decode_quad<NT, KB>(pc, 0, ui.ntok, tab, xw, acc);
       const int nsub = claim_take(claimed);
+      // A part whose sub-list has handed out more than kStraggle items since the part was claimed
+      // (a sub-list serves ~32 blocks x 12 waves: about half that many claims in a part's first
+      // quad) has fallen behind the waves around it, and finishes may be waiting for it: its
+      // second quad runs at raised priority.
+      if (nsub - sub > kStraggle) __builtin_amdgcn_s_setprio(2);
       Item nit;
       resolve(nsub, nit);
       // the next part's quad 0 and input block -- this part's again when the next item is not a
